@@ -1,0 +1,74 @@
+// Host-side launchers implemented by the kernel translation units; the C ABI (abi.hip)
+// validates arguments and calls these.  Every launcher enqueues on `st` and returns the
+// hipError_t of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/aipu_q4k.h"
+
+namespace aipu {
+
+// elementwise.hip
+hipError_t launch_dequant(int type, const void* blocks, int64_t n_weights, float* out, hipStream_t st);
+hipError_t launch_q4k_scale_min(const void* blocks, int64_t n_blocks, uint16_t* out, hipStream_t st);
+hipError_t launch_bf16_round(const float* x, int64_t n, uint16_t* out, hipStream_t st);
+hipError_t launch_act(int which, const uint16_t* x, int64_t n, uint16_t* y, hipStream_t st);  // 0 silu, 1 sigmoid
+hipError_t launch_rsqrt(const float* x, int64_t n, float* y, hipStream_t st);
+hipError_t launch_stream_read(const void* p, int64_t bytes, uint32_t* sink, hipStream_t st);
+hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t scale_bits,
+                              int32_t* sel_idx, uint16_t* sel_w, uint16_t* gates, hipStream_t st);
+
+// gemv_ref.hip -- bit-exact reference order
+hipError_t launch_gemv_ref(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
+                           uint16_t* y, float* y_f32, hipStream_t st);
+// Slot-gathered form (MoE reference path): grid z = slot; slot z < topk uses weight matrix
+// sel[z] of the stack (stride wstride bytes), slot topk the shared matrix w_alt.
+hipError_t launch_gemv_ref_gather(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
+                                  uint16_t* y, float* y_f32, int nslots, const int32_t* sel, int topk, int64_t E,
+                                  int64_t wstride, const void* w_alt, int64_t x_zstride, int64_t y_zstride,
+                                  hipStream_t st);
+hipError_t launch_gemv_ref_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t M,
+                               uint16_t* y, float* y_f32, hipStream_t st);
+
+// gemv_fast.hip -- tolerance-mode streaming GEMV
+hipError_t launch_gemv_fast(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
+                            uint16_t* y, float* y_f32, hipStream_t st);
+hipError_t launch_gemv_tiles(const aipu_tile_desc* tiles, int n_tiles, int64_t N, int64_t K, const uint16_t* x,
+                             int64_t M, uint16_t* y, float* y_f32, int mode, hipStream_t st);
+
+// moe.hip
+struct MoeArgs {
+    int router_type;
+    const void* router_w;
+    int type;
+    const uint8_t* gate_exps;
+    const uint8_t* up_exps;
+    const uint8_t* down_exps;
+    const uint8_t* sh_gate;
+    const uint8_t* sh_up;
+    const uint8_t* sh_down;
+    int64_t E, H, I;
+    int topk;
+    uint32_t scale_bits;
+    const uint16_t* x;
+    uint16_t* y;
+    int32_t* sel_idx_out;
+    uint16_t* sel_w_out;
+    int mode;
+    void* ws;
+};
+int64_t moe_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
+hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st);
+hipError_t launch_swiglu_expert(int type, const void* wg, const void* wu, const void* wd, int64_t H, int64_t I,
+                                const uint16_t* x, uint16_t* y, uint16_t* h_out, int mode, void* ws,
+                                hipStream_t st);
+
+// prefill.hip
+hipError_t launch_gemm_prefill(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
+                               uint16_t* y, int precision, hipStream_t st);
+
+int device_cu_count();
+
+}  // namespace aipu

@@ -35,6 +35,12 @@ def lib():
         L.oq_f16_to_f32.restype = ctypes.c_float
         L.oq_rsqrt.argtypes = [ctypes.c_float]
         L.oq_rsqrt.restype = ctypes.c_float
+        L.oq_bf16_round_bits.argtypes = [ctypes.c_uint32]
+        L.oq_bf16_round_bits.restype = ctypes.c_uint16
+        L.oq_rsqrt_bits.argtypes = [ctypes.c_uint32]
+        L.oq_rsqrt_bits.restype = ctypes.c_uint32
+        L.oq_f16_to_f32_bits.argtypes = [ctypes.c_uint16]
+        L.oq_f16_to_f32_bits.restype = ctypes.c_uint32
         L.oq_glm_silu.argtypes = [ctypes.c_uint16]
         L.oq_glm_silu.restype = ctypes.c_uint16
         L.oq_glm_sigmoid.argtypes = [ctypes.c_uint16]

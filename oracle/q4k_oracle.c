@@ -230,3 +230,8 @@ uint16_t oq_glm_silu(uint16_t xb) {
     float s = oq_sigmoid_f32(x);
     return oq_bf16_round(s * sanitize16(x));
 }
+
+/* Bit-pattern wrappers (callers that marshal floats through doubles would quiet sNaNs). */
+uint16_t oq_bf16_round_bits(uint32_t u) { return oq_bf16_round(u2f(u)); }
+uint32_t oq_rsqrt_bits(uint32_t u) { return f2u(oq_rsqrt(u2f(u))); }
+uint32_t oq_f16_to_f32_bits(uint16_t h) { return f2u(oq_f16_to_f32(h)); }

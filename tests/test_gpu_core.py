@@ -1,0 +1,204 @@
+"""GPU parity for the core numerics through the C ABI: exact dequant of every type, bf16
+rounding, glm activations, reference-order GEMV (bit-exact) and the fast streaming GEMV
+(tolerance: |acc - exact| <= 1e-5 * sum|a*w|, bf16 within 1 ulp of the reference order)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from aipu_amd import device as dev
+from oracle import c_oracle as co
+from oracle import glm_oracle as go
+from oracle import q4k_oracle as qo
+
+from .gpu_util import assert_bits_equal, d_bf16, d_u8, h_bits, h_f32, note, u32
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ------------------------------------------------------------------- dequant
+def test_dequant_f16_exhaustive():
+    note("dequant F16 exhaustive")
+    allh = np.arange(65536, dtype=np.uint16)
+    got = h_f32(dev.dequantize(qo.GGML_F16, d_u8(allh.view(np.uint8))))
+    exp = qo.f16_bits_to_f32(allh)
+    fin = (allh & 0x7C00) != 0x7C00
+    inf = ((allh & 0x7C00) == 0x7C00) & ((allh & 0x3FF) == 0)
+    assert_bits_equal(u32(got)[fin | inf], u32(exp)[fin | inf], "F16 finite/inf")
+    nan = ~(fin | inf)
+    assert np.all(np.isnan(got[nan]))          # NaN stays NaN (payload quieting is not part of the contract)
+    assert u32(got)[1] == 0x33800000           # test/q4k_prim_tb.v:45 smallest subnormal KAT
+
+
+def _q4k_edge_blocks(rng):
+    out = []
+    for dh, dmh in [(0x0001, 0x0001), (0x03FF, 0x0000), (0x0000, 0x3C00), (0x8000, 0x0400), (0x7BFF, 0x7BFF),
+                    (0x5800, 0x0013)]:
+        blk = qo.random_q4k_blocks(rng, 1).copy()
+        blk[0:2] = np.array([dh], np.uint16).view(np.uint8)
+        blk[2:4] = np.array([dmh], np.uint16).view(np.uint8)
+        out.append(blk)
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("t", [qo.GGML_Q4_K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16, 30])
+def test_dequant_random_bitexact(t):
+    note(f"dequant type {t}")
+    rng = np.random.default_rng(100 + t)
+    if t == 30:
+        raw = qo.random_bf16(rng, 4096).view(np.uint8)
+        exp = qo.bf16_bits_to_f32(raw.view(np.uint16))
+        n = 4096
+    else:
+        raw = qo.random_weights(rng, t, 64, 4096)
+        if t == qo.GGML_Q4_K:
+            raw = np.concatenate([raw, _q4k_edge_blocks(rng)])
+        n = raw.size // qo.BLOCK_BYTES[t] * qo.BLOCK_WEIGHTS[t]
+        exp = qo.dequant(t, raw)
+    got = h_f32(dev.dequantize(t, d_u8(raw), n))
+    assert_bits_equal(u32(got), u32(exp), f"dequant {t}")
+
+
+def test_q4k_scale_min_kat_and_random():
+    note("scale_min")
+    sc_hex = 0x6B2A36C53CC261873FE85103
+    kat = [0x1C3, 0x851, 0x0A8, 0xF3F, 0xB05, 0x4D6, 0xCBA, 0x18B]
+    blk = np.zeros(144, np.uint8)
+    blk[4:16] = [(sc_hex >> (8 * i)) & 0xFF for i in range(12)]
+    rng = np.random.default_rng(7)
+    raw = np.concatenate([blk, qo.random_q4k_blocks(rng, 500)])
+    got = h_bits(dev.q4k_scale_min(d_u8(raw)).view(torch.int16)).astype(np.int64)
+    sc, m = qo.unpack_scales_q4k(raw.reshape(-1, 144)[:, 4:16])
+    assert np.array_equal(got & 0xFF, sc) and np.array_equal(got >> 8, m)
+    assert [int(((v >> 8) << 6) | (v & 0xFF)) for v in got[0]] == kat
+
+
+def test_bf16_round():
+    note("bf16_round")
+    rng = np.random.default_rng(8)
+    cases = np.array([0x3F800000, 0x3F808000, 0x3F818000, 0x3F7FFFFF, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F800000,
+                      0x7FC00001, 0x7F800001, 0x00000001, 0x80008000, 0x00018000], np.uint32)
+    u = np.concatenate([cases, rng.integers(0, 2 ** 32, 100000, dtype=np.uint64).astype(np.uint32)])
+    got = h_bits(dev.bf16_round(torch.from_numpy(u.view(np.float32).copy()).to("cuda")))
+    assert_bits_equal(got, qo.bf16_round_bits(u.view(np.float32)), "bf16")
+
+
+# ---------------------------------------------------------------- activations
+def test_glm_act_tables_exhaustive():
+    note("glm_silu / glm_sigmoid exhaustive")
+    t = np.load(os.path.join(GOLD, "act_tables.npz"))
+    allb = np.arange(65536, dtype=np.uint16)
+    assert_bits_equal(h_bits(dev.glm_silu(d_bf16(allb))), t["silu"], "silu")
+    assert_bits_equal(h_bits(dev.glm_sigmoid(d_bf16(allb))), t["sigmoid"], "sigmoid")
+
+
+def test_fp32_rsqrt_golden():
+    note("fp32_rsqrt")
+    r = np.load(os.path.join(GOLD, "rsqrt_cases.npz"))
+    got = h_f32(dev.fp32_rsqrt(torch.from_numpy(r["x"].view(np.float32).copy()).to("cuda")))
+    assert_bits_equal(u32(got), r["y"], "rsqrt")
+
+
+# ------------------------------------------------------- reference-order GEMV
+REF_CASES = [
+    (qo.GGML_Q4_K, 200, 768, 1), (qo.GGML_Q4_K, 131, 512, 3), (qo.GGML_Q4_K, 64, 256, 9),
+    (qo.GGML_Q6_K, 96, 512, 2), (qo.GGML_Q8_0, 70, 512, 1), (qo.GGML_F16, 65, 256, 2), (30, 64, 512, 1),
+]
+
+
+@pytest.mark.parametrize("t,N,K,M", REF_CASES)
+def test_gemv_ref_bitexact(t, N, K, M):
+    note(f"gemv ref type={t} N={N} K={K} M={M}")
+    rng = np.random.default_rng(N * K + M)
+    raw = qo.random_bf16(rng, N * K).view(np.uint8) if t == 30 else qo.random_weights(rng, t, N, K)
+    x = qo.random_bf16(rng, (M, K))
+    y, yf = dev.gemv(t, d_u8(raw), N, K, d_bf16(x), mode="ref", out_f32=True)
+    if t == 30:
+        acc, ye = qo.gemv_ref(qo.bf16_bits_to_f32(raw.view(np.uint16)).reshape(N, K), qo.bf16_bits_to_f32(x))
+    else:
+        acc, ye = co.gemv_ref(t, raw, N, K, x)
+    assert_bits_equal(u32(h_f32(yf)), u32(acc), "acc")
+    assert_bits_equal(h_bits(y), ye, "y")
+
+
+def test_gemv_ref_full_north_star_shape():
+    """K = N = 6144, M = 1: every output bit-exact against the C oracle."""
+    note("gemv ref 6144x6144")
+    rng = np.random.default_rng(6144)
+    raw = qo.random_q4k_blocks(rng, 6144 * 24)
+    x = qo.random_bf16(rng, (1, 6144))
+    y, yf = dev.gemv(qo.GGML_Q4_K, d_u8(raw), 6144, 6144, d_bf16(x), mode="ref", out_f32=True)
+    acc, ye = co.gemv_ref(qo.GGML_Q4_K, raw, 6144, 6144, x)
+    assert_bits_equal(u32(h_f32(yf)), u32(acc), "acc")
+    assert_bits_equal(h_bits(y), ye, "y")
+
+
+def test_gemv_f32_matmul_q4k_col():
+    note("gemv_f32")
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((37, 300)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((2, 300)).astype(np.float32)   # not bf16-valued: full fp32 inputs
+    y, yf = dev.gemv_f32(torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda(), out_f32=True)
+    acc, ye = qo.gemv_ref(w, x)
+    assert_bits_equal(u32(h_f32(yf)), u32(acc), "acc")
+    assert_bits_equal(h_bits(y), ye, "y")
+
+
+# ------------------------------------------------------------------ fast GEMV
+FAST_CASES = [
+    (6144, 6144, 1), (4096, 4096, 1), (6144, 6144, 2), (6144, 6144, 4), (6144, 6144, 8),
+    (1001, 2048, 1), (77, 256, 3), (300, 2304, 1), (64, 18432, 1), (2048, 6144, 5),
+]
+
+
+@pytest.mark.parametrize("N,K,M", FAST_CASES)
+def test_gemv_fast_tolerance(N, K, M):
+    note(f"gemv fast Q4_K N={N} K={K} M={M}")
+    rng = np.random.default_rng(N + K + M)
+    raw = qo.random_q4k_blocks(rng, N * K // 256)
+    x = qo.random_bf16(rng, (M, K))
+    wd = d_u8(raw)
+    y, yf = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(x), mode="fast", out_f32=True)
+    yr = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(x), mode="ref")
+    w = qo.dequant_q4k(raw).reshape(N, K)
+    ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf), rel=1e-5)
+    assert ok, f"tolerance gate exceeded: worst {worst:.3f} of the 1e-5*sum|a*w| bound"
+    ulp = qo.bf16_ulp_distance(h_bits(y), h_bits(yr))
+    assert ulp.max() <= 1, f"bf16 outputs differ by up to {ulp.max()} ulp"
+    # deterministic: a second run is bitwise identical
+    y2, yf2 = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(x), mode="fast", out_f32=True)
+    assert np.array_equal(u32(h_f32(yf2)), u32(h_f32(yf)))
+
+
+def test_gemv_fast_bf16_router_shape():
+    note("gemv fast BF16 256x6144")
+    rng = np.random.default_rng(11)
+    wbits = qo.random_bf16(rng, (256, 6144), scale=0.02)
+    x = qo.random_bf16(rng, (1, 6144))
+    y, yf = dev.gemv(30, d_u8(wbits.view(np.uint8)), 256, 6144, d_bf16(x), mode="fast", out_f32=True)
+    w = qo.bf16_bits_to_f32(wbits)
+    ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
+    assert ok, worst
+    _, ye = qo.gemv_ref(w, qo.bf16_bits_to_f32(x))
+    assert qo.bf16_ulp_distance(h_bits(y), ye).max() <= 1
+
+
+def test_gemv_fast_detects_corrupted_weights():
+    """Must-fail twin: flipping one nibble moves the output beyond the gate."""
+    note("gemv fast corruption twin")
+    rng = np.random.default_rng(12)
+    N, K = 64, 2048
+    raw = qo.random_q4k_blocks(rng, N * K // 256)
+    off = 5 * 144 * 8                             # row 5, block 0
+    raw[off + 4:off + 16] = qo.pack_scales_q4k([32] * 8, [1] * 8)
+    raw[off + 16 + 3] &= 0xF0                     # weight 3 has code 0 ...
+    x = qo.random_bf16(rng, (1, K))
+    x[0, 3] = qo.bf16_round_bits(np.float32(4.0))
+    w = qo.dequant_q4k(raw).reshape(N, K)
+    bad = raw.copy()
+    bad[off + 16 + 3] |= 0x0F                     # ... and 15 in the corrupted copy
+    _, yf = dev.gemv(qo.GGML_Q4_K, d_u8(bad), N, K, d_bf16(x), mode="fast", out_f32=True)
+    ok, _ = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
+    assert not ok

