@@ -20,7 +20,8 @@ LIB = os.path.join(HERE, "libaipu_q4k.so")
 OBJDIR = os.path.join(ROOT, "_build", "obj")
 ARCH = "gfx950"
 
-SOURCES = ["abi.hip", "elementwise.hip", "gemv_ref.hip", "gemv_fast.hip", "moe.hip", "tiles.hip", "prefill.hip"]
+SOURCES = ["abi.hip", "elementwise.hip", "router.hip", "gemv_ref.hip", "gemv_fast.hip", "moe.hip", "tiles.hip",
+           "prefill.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

@@ -48,9 +48,11 @@ const char* type_name(int t) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-// Alignment the kernels need for a weight pointer of this type: Q4_K blocks are read
-// with 16-B loads, every other type with 2-B (or byte) loads.
-uintptr_t weight_align(int t) { return t == aipu::T_Q4_K ? 16 : 2; }
+// Alignment the kernels need for a weight pointer of this type: Q4_K blocks (both modes)
+// and bf16 rows in fast mode are read with 16-B loads, everything else with 2-B loads.
+uintptr_t weight_align(int t, int mode = AIPU_MODE_FAST) {
+    return (t == aipu::T_Q4_K || (t == aipu::T_BF16 && mode == AIPU_MODE_FAST)) ? 16 : 2;
+}
 
 hipStream_t S(void* s) { return (hipStream_t)s; }
 
@@ -67,8 +69,9 @@ int check_gemv(int type, const void* w, int64_t N, int64_t K, const void* x, int
                     aipu::type_qk(type));
     if (K % 256) return fail(AIPU_ERR_SHAPE, "K=%lld must be a multiple of 256", (long long)K);
     if (N > (1LL << 31) || M > (1LL << 24)) return fail(AIPU_ERR_SHAPE, "N or M out of range");
-    if (!aligned(w, weight_align(type))) return fail(AIPU_ERR_ALIGN, "%s weights must be %d-byte aligned",
-                                                    type_name(type), (int)weight_align(type));
+    if (!aligned(w, weight_align(type, mode)))
+        return fail(AIPU_ERR_ALIGN, "%s weights must be %d-byte aligned", type_name(type),
+                    (int)weight_align(type, mode));
     if (!aligned(x, mode == AIPU_MODE_FAST ? 16 : 2))
         return fail(AIPU_ERR_ALIGN, "activations must be %d-byte aligned", mode == AIPU_MODE_FAST ? 16 : 2);
     if (!aligned(y, 2) || (yf && !aligned(yf, 4))) return fail(AIPU_ERR_ALIGN, "misaligned output");
@@ -202,7 +205,7 @@ int aipu_swiglu_expert(int ggml_type, const void* wg, const void* wu, const void
     int rc = check_gemv(ggml_type, wg, I, H, x, 1, y, nullptr, mode);
     if (rc) return rc;
     if (H % 256 || I % 256) return fail(AIPU_ERR_SHAPE, "H and I must be multiples of 256");
-    if (!aligned(wu, weight_align(ggml_type)) || !aligned(wd, weight_align(ggml_type)))
+    if (!aligned(wu, weight_align(ggml_type, mode)) || !aligned(wd, weight_align(ggml_type, mode)))
         return fail(AIPU_ERR_ALIGN, "misaligned weights");
     if (h_out && !aligned(h_out, 16)) return fail(AIPU_ERR_ALIGN, "h_out must be 16-byte aligned");
     const int64_t need = aipu::moe_workspace_bytes(1, H, I, 1);
@@ -231,7 +234,7 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
     rc = check_gemv(ggml_type, gate_exps, I, H, x, 1, y, nullptr, mode);
     if (rc) return fail(rc, "experts: %s", g_err.c_str());
     if (I % 256) return fail(AIPU_ERR_SHAPE, "I must be a multiple of 256");
-    const uintptr_t wa = weight_align(ggml_type);
+    const uintptr_t wa = weight_align(ggml_type, mode);
     if (!aligned(up_exps, wa) || !aligned(down_exps, wa) || (sh_all && (!aligned(shared_gate, wa) ||
                                                                         !aligned(shared_up, wa) ||
                                                                         !aligned(shared_down, wa))))

@@ -1,6 +1,6 @@
-// Exact dequantisation, scale unpack, bf16 rounding, glm activations and the MoE router
-// tail.  These are bit-exact restatements of the reference's per-element arithmetic; none
-// of them is bandwidth-critical on the decode path except the router tail's latency.
+// Exact dequantisation, scale unpack, bf16 rounding and glm activations: bit-exact
+// restatements of the reference's per-element arithmetic (none is on the decode path's
+// bandwidth-critical leg), plus the read-bandwidth probe.
 #include "common.hpp"
 #include "glm_act.hpp"
 #include "launch.hpp"
@@ -118,15 +118,25 @@ __global__ void k_rsqrt(const float* __restrict__ x, int64_t n, float* __restric
         y[i] = glm_rsqrt(x[i]);
 }
 
-// Read-bandwidth probe: every thread streams 16-B loads grid-stride and xor-folds them.
-__global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ p, int64_t n16, uint32_t* sink) {
+// Read-bandwidth probe: each thread issues 8 independent 16-B loads (a 32 KB tile per
+// 256-thread workgroup, coalesced) before folding them, grid-striding over the buffer.
+// The fold is stored only when it equals `magic` (practically never), so the probe
+// measures reads without a write or atomic stream behind it.
+__global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ p, int64_t n16, uint32_t* sink,
+                                                     uint32_t magic) {
     uint32_t acc = 0;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x) {
-        const uint4 v = p[i];
-        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    const int64_t tile = 256 * 8;
+    for (int64_t base = (int64_t)blockIdx.x * tile; base < n16; base += (int64_t)gridDim.x * tile) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t i = base + u * 256 + threadIdx.x;
+            v[u] = i < n16 ? p[i] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
-    for (int off = 32; off > 0; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
-    if ((threadIdx.x & 63) == 0) atomicXor(&sink[blockIdx.x & 255], acc);
+    if (acc == magic) sink[blockIdx.x & 255] = acc;
 }
 
 }  // namespace
@@ -136,96 +146,7 @@ hipError_t launch_stream_read(const void* p, int64_t bytes, uint32_t* sink, hipS
     int64_t g = (n16 + 256 * 8 - 1) / (256 * 8);
     if (g > 256 * 16) g = 256 * 16;
     if (g < 1) g = 1;
-    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)g), dim3(256), 0, st, (const uint4*)p, n16, sink);
-    return hipGetLastError();
-}
-
-// -------------------------------------------------------------- router tail
-// One workgroup of 1024 threads.  Each thread owns experts e = tid, tid+1024, ...
-// Gates are glm_sigmoid of the bf16 logits; the winner of each of the topk rounds is the
-// maximum of the composite key (fp32 order key << 32 | ~index), i.e. largest gate first
-// and the lower expert index on ties (tools/glm_model_q4k_ref.py:671-673).  Thread 0 then
-// forms the balanced +0-padded fp32 add tree over the winners in slot order (:691-699),
-// rs = f32(f32(rsqrt(s)^2) * scale) (:678-679) and sel_w = bf16(gate * rs) (:680).
-constexpr int kRouterThreads = 1024;
-constexpr int kRouterMaxPerThread = 4;   // E <= 4096
-constexpr int kMaxTopk = 32;
-
-__device__ __forceinline__ uint64_t u64max(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-__global__ __launch_bounds__(kRouterThreads) void k_router_tail(const uint16_t* __restrict__ logits, int E, int topk,
-                                                                 uint32_t scale_bits, int32_t* __restrict__ sel_idx,
-                                                                 uint16_t* __restrict__ sel_w,
-                                                                 uint16_t* __restrict__ gates_out) {
-    __shared__ uint64_t wave_best[kRouterThreads / 64];
-    __shared__ uint64_t winners[kMaxTopk];
-    const int tid = threadIdx.x;
-    uint64_t key[kRouterMaxPerThread];
-#pragma unroll
-    for (int r = 0; r < kRouterMaxPerThread; ++r) {
-        const int e = tid + r * kRouterThreads;
-        key[r] = 0;
-        if (e < E) {
-            const uint32_t gb = glm_sigmoid_bf16(logits[e]);
-            if (gates_out) gates_out[e] = (uint16_t)gb;
-            key[r] = ((uint64_t)f32_order_key(bf16_to_f32(gb)) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-        }
-    }
-    for (int s = 0; s < topk; ++s) {
-        uint64_t best = 0;
-#pragma unroll
-        for (int r = 0; r < kRouterMaxPerThread; ++r) best = u64max(best, key[r]);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const uint32_t lo = __shfl_xor((uint32_t)best, off, 64);
-            const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, 64);
-            best = u64max(best, ((uint64_t)hi << 32) | lo);
-        }
-        if ((tid & 63) == 0) wave_best[tid >> 6] = best;
-        __syncthreads();
-        if (tid == 0) {
-            uint64_t b = 0;
-            for (int w = 0; w < kRouterThreads / 64; ++w) b = u64max(b, wave_best[w]);
-            winners[s] = b;
-        }
-        __syncthreads();
-        const uint64_t win = winners[s];
-#pragma unroll
-        for (int r = 0; r < kRouterMaxPerThread; ++r)
-            if (key[r] == win) key[r] = 0;
-        __syncthreads();
-    }
-    if (tid == 0) {
-        float node[kMaxTopk];
-        int lev = 1, npow = 2;
-        while (npow < topk) { npow <<= 1; ++lev; }
-        for (int i = 0; i < npow; ++i) {
-            if (i < topk) {
-                const uint32_t ok = (uint32_t)(winners[i] >> 32);
-                node[i] = __uint_as_float((ok >> 31) ? (ok ^ 0x80000000u) : ~ok);
-            } else {
-                node[i] = 0.0f;
-            }
-        }
-        for (int l = 0; l < lev; ++l) {
-            for (int i = 0; i < (npow >> (l + 1)); ++i) node[i] = node[2 * i] + node[2 * i + 1];
-        }
-        const float rr = glm_rsqrt(node[0]);
-        const float rr2 = rr * rr;
-        const float rs = rr2 * __uint_as_float(scale_bits);
-        for (int i = 0; i < topk; ++i) {
-            const uint32_t ok = (uint32_t)(winners[i] >> 32);
-            const float g = __uint_as_float((ok >> 31) ? (ok ^ 0x80000000u) : ~ok);
-            sel_idx[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)winners[i]);
-            sel_w[i] = (uint16_t)bf16_rne(g * rs);
-        }
-    }
-}
-
-hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t scale_bits, int32_t* sel_idx,
-                              uint16_t* sel_w, uint16_t* gates, hipStream_t st) {
-    hipLaunchKernelGGL(k_router_tail, dim3(1), dim3(kRouterThreads), 0, st, logits, E, topk, scale_bits, sel_idx,
-                       sel_w, gates);
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)g), dim3(256), 0, st, (const uint4*)p, n16, sink, 0x9E3779B9u);
     return hipGetLastError();
 }
 

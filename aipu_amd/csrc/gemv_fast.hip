@@ -249,44 +249,187 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_stream(Items items, Epi epi,
     }
 }
 
-// ------------------------------------------------------------- MoE down
-// Items are (output row d, slot s) flattened as d * nslots + s within the workgroup's
-// rows.  Each slot's activations h[s] are permuted into the lane layout once per
-// workgroup and kept in LDS; each item's bf16 result goes to LDS, and after the last
-// batch every output row is combined in slot order:
-//   facc = f32(facc + f32(g_s * y_s)),  y = bf16(facc)   (tools/glm_model_q4k_ref.py:799-809)
-// with g = 1 for the shared-expert slot (adding y_sh directly, as the reference does).
-constexpr int kDownPasses = 4;
+// -------------------------------------------------------- row kernel (M = 1)
+// For M = 1 and K <= 8192 each wave walks whole row pairs (half-wave = one row, all
+// segments), so no cross-wave reduction is needed.  Each wave first issues the weight loads
+// of its first two row pairs, then the workgroup builds the permuted activation layout
+// once in LDS (every wave reads it back per segment), and the pair loop is software
+// pipelined: the loads of pair p + 2*nw are issued as soon as pair p's registers are free.
+// Launch shape of the row kernel (compile-time): waves per workgroup and the cap on
+// workgroups per CU used to size the grid.
+#ifndef AIPU_ROW_WAVES
+#define AIPU_ROW_WAVES 4
+#endif
+#ifndef AIPU_ROW_WG_PER_CU
+#define AIPU_ROW_WG_PER_CU 4
+#endif
+constexpr int kRowWaves = AIPU_ROW_WAVES;
 
-struct DownGeom {
-    int nsb, nseg, segw, rgc, nbatch;
-    int rows_per_wg;
-    int nslots, topk, E;
-    int passthrough;   // single expert: y is the slot's bf16 output itself (no combine)
+template <int NSEG>
+struct RowBuf {
+    Raw r[NSEG];
+};
+
+template <int NSEG, class Items>
+__device__ __forceinline__ void rows_load(RowBuf<NSEG>& b, const Items& items, int64_t pair, const Geo& G,
+                                          const int (&blkc)[NSEG]) {
+    const uint8_t* row = items.row(pair, G.half);
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) b.r[s] = raw_load(row + (int64_t)blkc[s] * 144, G);
+}
+
+template <int NSEG>
+__device__ __forceinline__ float rows_part(const RowBuf<NSEG>& b, const uint4* sxa, const float2* ssum,
+                                           const Geo& G, const bool (&ok)[NSEG]) {
+    float part = 0.f;
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+        Act A;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint4 q = sxa[(s * 8 + i) * 32 + G.s];
+            A.xa[4 * i] = q.x;
+            A.xa[4 * i + 1] = q.y;
+            A.xa[4 * i + 2] = q.z;
+            A.xa[4 * i + 3] = q.w;
+        }
+        const float2 sm = ssum[s * 32 + G.s];
+        A.alo = sm.x;
+        A.ahi = sm.y;
+        const Hdr H = hdr_decode(b.r[s].h, G);
+        float Slo, Shi;
+        code_dots(b.r[s], A, Slo, Shi);
+        const float v = lane_part(H, Slo, Shi, A);
+        part += ok[s] ? v : 0.f;
+        // keep the compiler from hoisting the next segment's LDS reads above this
+        // segment's math: 161 instead of 222 VGPRs, i.e. 3 waves per SIMD
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return part;
+}
+
+template <int NSEG, class Items, class Epi>
+__global__ __launch_bounds__(kRowWaves * 64) void k_rows(Items items, Epi epi, const uint16_t* __restrict__ X,
+                                                        int nsb, int64_t npairs) {
+    __shared__ uint4 sxa[NSEG * 8 * 32];
+    __shared__ float2 ssum[NSEG * 32];
+    const int lane = threadIdx.x & 63;
+    const Geo G = make_geo(lane);
+    const int64_t nw = (int64_t)gridDim.x * kRowWaves;
+    const int64_t p0 = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
+    int blkc[NSEG];
+    bool ok[NSEG];
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+        const int blk = s * kSegBlocks + G.bs;
+        ok[s] = blk < nsb;
+        blkc[s] = ok[s] ? blk : 0;
+    }
+    RowBuf<NSEG> ba, bb;
+    if (p0 < npairs) rows_load(ba, items, p0, G, blkc);
+    if (p0 + nw < npairs) rows_load(bb, items, p0 + nw, G, blkc);
+
+    if (threadIdx.x < NSEG * 32) {
+        const int s = threadIdx.x >> 5, ls = threadIdx.x & 31;
+        const Geo g2 = make_geo(ls);
+        Act A;
+        act_load(A, X, s, g2, s * kSegBlocks + g2.bs < nsb);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            sxa[(s * 8 + i) * 32 + ls] = make_uint4(A.xa[4 * i], A.xa[4 * i + 1], A.xa[4 * i + 2], A.xa[4 * i + 3]);
+        ssum[s * 32 + ls] = make_float2(A.alo, A.ahi);
+    }
+    __syncthreads();
+
+    for (int64_t p = p0; p < npairs; p += 2 * nw) {
+        float tot = half_sum_dpp(rows_part<NSEG>(ba, sxa, ssum, G, ok));
+        if (p + 2 * nw < npairs) rows_load(ba, items, p + 2 * nw, G, blkc);
+        float other = __shfl(tot, 31, 64);
+        if (lane == 63) epi(p, other, tot);
+        const int64_t q = p + nw;
+        if (q >= npairs) break;
+        tot = half_sum_dpp(rows_part<NSEG>(bb, sxa, ssum, G, ok));
+        if (q + 2 * nw < npairs) rows_load(bb, items, q + 2 * nw, G, blkc);
+        other = __shfl(tot, 31, 64);
+        if (lane == 63) epi(q, other, tot);
+    }
+}
+
+// ------------------------------------------------------ MoE down (row tasks)
+// A wave owns whole output rows d.  Row d needs one item per slot (expert e_s's row d
+// against h[s]); a pass handles two slots (one per half-wave), so a row takes
+// NP = ceil(nslots / 2) passes.  Passes are software pipelined two deep across the wave's
+// whole (row, pass) sequence.  All slots' activations are permuted into the lane layout
+// once per workgroup in LDS.  After each pass lane 63 folds the two slot results into the
+// row's fp32 combine in slot order
+//     facc = f32(facc + f32(g_s * bf16(y_s)))   (tools/glm_model_q4k_ref.py:799-809)
+// (g = 1 for the shared-expert slot, i.e. facc + y_sh) and writes bf16(facc) after the
+// row's last pass.  In passthrough mode (a single expert) y is bf16(y_0) itself.
+struct DownRowsArgs {
+    int nsb, nslots, topk, E, np, passthrough;
     int64_t H, I, ebytes, rb;
 };
 
-__global__ __launch_bounds__(kMaxWaves * 64) void k_moe_down(const uint8_t* __restrict__ D,
-                                                             const uint8_t* __restrict__ shD,
-                                                             const int32_t* __restrict__ sel,
-                                                             const uint16_t* __restrict__ selw,
-                                                             const uint16_t* __restrict__ hbuf,
-                                                             uint16_t* __restrict__ Y, DownGeom dg) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float red[2][kMaxWaves][kDownPasses][2];
-    const int units = dg.nslots * dg.nseg * 32;
-    uint4* lxa = (uint4*)smem;                                          // [unit/32][8][32] uint4
-    float2* lsum = (float2*)(smem + (size_t)units * 128);              // [unit]
-    float* ys = (float*)(smem + (size_t)units * 136);                  // [rows_per_wg][nslots]
+template <int NSEG>
+struct DownBuf {
+    Raw r[NSEG];
+};
 
-    // 1. activations -> LDS in the lane layout
+template <int NSEG>
+__device__ __forceinline__ void down_load(DownBuf<NSEG>& b, const uint8_t* D, const uint8_t* shD, const int32_t* sel,
+                                          const DownRowsArgs& a, int64_t d, int q, const Geo& G,
+                                          const int (&blkc)[NSEG]) {
+    int s = 2 * q + G.half;
+    s = s < a.nslots ? s : a.nslots - 1;
+    const uint8_t* base;
+    if (s < a.topk) {
+        int e = sel[s];
+        e = e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
+        base = D + (int64_t)e * a.ebytes;
+    } else {
+        base = shD;
+    }
+    const uint8_t* row = base + d * a.rb;
+#pragma unroll
+    for (int g = 0; g < NSEG; ++g) b.r[g] = raw_load(row + (int64_t)blkc[g] * 144, G);
+}
+
+template <int NSEG>
+__global__ __launch_bounds__(256) void k_down_rows(const uint8_t* __restrict__ D, const uint8_t* __restrict__ shD,
+                                                   const int32_t* __restrict__ sel,
+                                                   const uint16_t* __restrict__ selw,
+                                                   const uint16_t* __restrict__ hbuf, uint16_t* __restrict__ Y,
+                                                   DownRowsArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int units = a.nslots * NSEG * 32;
+    uint4* lxa = (uint4*)smem;                              // [slot*NSEG + seg][8][32]
+    float2* lsum = (float2*)(smem + (size_t)units * 128);  // [slot*NSEG + seg][32]
+    const int lane = threadIdx.x & 63;
+    const Geo G = make_geo(lane);
+    const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+    const int64_t w0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    int blkc[NSEG];
+    bool ok[NSEG];
+#pragma unroll
+    for (int g = 0; g < NSEG; ++g) {
+        const int blk = g * kSegBlocks + G.bs;
+        ok[g] = blk < a.nsb;
+        blkc[g] = ok[g] ? blk : 0;
+    }
+    // this wave's units: rows d = w0 + k*nw, passes q = 0..np-1
+    const int64_t nrows_w = w0 < a.H ? (a.H - w0 + nw - 1) / nw : 0;
+    const int64_t nunits = nrows_w * a.np;
+    DownBuf<NSEG> ba, bb;
+    if (nunits > 0) down_load(ba, D, shD, sel, a, w0, 0, G, blkc);
+    if (nunits > 1) down_load(bb, D, shD, sel, a, w0 + (1 / a.np) * nw, 1 % a.np, G, blkc);
+
     for (int u = threadIdx.x; u < units; u += blockDim.x) {
-        const int s = u / (dg.nseg * 32);
-        const int rem = u - s * dg.nseg * 32;
+        const int sl = u / (NSEG * 32);
+        const int rem = u - sl * NSEG * 32;
         const int seg = rem >> 5, ls = rem & 31;
-        Geo G = make_geo(ls);
+        const Geo g2 = make_geo(ls);
         Act A;
-        act_load(A, hbuf + (int64_t)s * dg.I, seg, G, seg * kSegBlocks + G.bs < dg.nsb);
+        act_load(A, hbuf + (int64_t)sl * a.I, seg, g2, seg * kSegBlocks + g2.bs < a.nsb);
         const int base = (u >> 5) * 256;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -295,96 +438,67 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_moe_down(const uint8_t* __re
     }
     __syncthreads();
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rg = wave / dg.segw, wseg = wave - rg * dg.segw;
-    const Geo G = make_geo(lane);
-    const int64_t d0 = (int64_t)blockIdx.x * dg.rows_per_wg;
-    const int nrows = (int)((dg.H - d0) < dg.rows_per_wg ? (dg.H - d0) : dg.rows_per_wg);
-    const int nitems = nrows * dg.nslots;
-    constexpr int VP = Pow2<kDownPasses>::v;
-    constexpr int LV = Pow2<kDownPasses>::lg;
-
-    int buf = 0;
-    for (int b = 0; b < dg.nbatch; ++b) {
-        const int it0 = ((rg * dg.nbatch) + b) * 2 * kDownPasses;
-        float part[kDownPasses];
-        int itm[kDownPasses];
+    float facc = 0.f;
+    auto step = [&](int64_t u, DownBuf<NSEG>& cur) {
+        const int64_t r = u / a.np;
+        const int q = (int)(u - r * a.np);
+        const int64_t d = w0 + r * nw;
+        int s = 2 * q + G.half;
+        const bool svalid = s < a.nslots;
+        s = svalid ? s : a.nslots - 1;
+        float part = 0.f;
 #pragma unroll
-        for (int p = 0; p < kDownPasses; ++p) {
-            part[p] = 0.f;
-            int it = it0 + 2 * p + G.half;
-            itm[p] = it < nitems ? it : nitems - 1;
-        }
-        const int seg = wseg;
-        const int blk = seg * kSegBlocks + G.bs;
-        const bool bvalid = blk < dg.nsb;
-        Raw r[kDownPasses];
-#pragma unroll
-        for (int p = 0; p < kDownPasses; ++p) {
-            const int d = itm[p] / dg.nslots, s = itm[p] - (itm[p] / dg.nslots) * dg.nslots;
-            const uint8_t* base;
-            if (s < dg.topk) {
-                int e = sel[s];
-                e = e < 0 ? 0 : (e >= dg.E ? dg.E - 1 : e);
-                base = D + (int64_t)e * dg.ebytes;
-            } else {
-                base = shD;
-            }
-            r[p] = raw_load(base + (d0 + d) * dg.rb + (int64_t)(bvalid ? blk : 0) * 144, G);
-        }
-#pragma unroll
-        for (int p = 0; p < kDownPasses; ++p) {
-            const int s = itm[p] % dg.nslots;
-            const int u = (s * dg.nseg + seg) * 32 + G.s;
+        for (int g = 0; g < NSEG; ++g) {
+            const int ub = (s * NSEG + g) * 32;
             Act A;
-            const int base = (u >> 5) * 256;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint4 q = lxa[base + i * 32 + G.s];
-                A.xa[4 * i] = q.x;
-                A.xa[4 * i + 1] = q.y;
-                A.xa[4 * i + 2] = q.z;
-                A.xa[4 * i + 3] = q.w;
+                const uint4 v = lxa[(ub >> 5) * 256 + i * 32 + G.s];
+                A.xa[4 * i] = v.x;
+                A.xa[4 * i + 1] = v.y;
+                A.xa[4 * i + 2] = v.z;
+                A.xa[4 * i + 3] = v.w;
             }
-            const float2 sm = lsum[u];
+            const float2 sm = lsum[ub + G.s];
             A.alo = sm.x;
             A.ahi = sm.y;
-            const Hdr H = hdr_decode(r[p].h, G);
+            const Hdr Hh = hdr_decode(cur.r[g].h, G);
             float Slo, Shi;
-            code_dots(r[p], A, Slo, Shi);
-            part[p] = bvalid ? lane_part(H, Slo, Shi, A) : 0.f;
+            code_dots(cur.r[g], A, Slo, Shi);
+            const float v = lane_part(Hh, Slo, Shi, A);
+            part += ok[g] ? v : 0.f;
+            __builtin_amdgcn_sched_barrier(0);
         }
-        float v[VP];
-#pragma unroll
-        for (int i = 0; i < VP; ++i) v[i] = i < kDownPasses ? part[i] : 0.f;
-        const float tot = half_reduce<VP>(v, lane);
-        const int vi = (G.s >> (5 - LV)) & (VP - 1);
-        if ((G.s & ((32 >> LV) - 1)) == 0 && vi < kDownPasses) red[buf][wave][vi][G.half] = tot;
-        __syncthreads();
-        const int t = threadIdx.x;
-        if (t < dg.rgc * kDownPasses * 2) {
-            const int erg = t / (2 * kDownPasses), ev = t - erg * 2 * kDownPasses;
-            const int p = ev >> 1, hf = ev & 1;
-            float acc = 0.f;
-            for (int w = 0; w < dg.segw; ++w) acc += red[buf][erg * dg.segw + w][p][hf];
-            const int it = ((erg * dg.nbatch) + b) * 2 * kDownPasses + 2 * p + hf;
-            if (it < nitems) ys[it] = bf16_to_f32(bf16_rne(acc));
+        if (u + 2 < nunits) {
+            const int64_t r2 = (u + 2) / a.np;
+            down_load(cur, D, shD, sel, a, w0 + r2 * nw, (int)(u + 2 - r2 * a.np), G, blkc);
         }
-        buf ^= 1;
-    }
-    __syncthreads();
-    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
-        if (dg.passthrough) {
-            Y[d0 + r] = (uint16_t)(__float_as_uint(ys[r * dg.nslots]) >> 16);
-            continue;
+        const float tot = half_sum_dpp(svalid ? part : 0.f);
+        const float v0 = __shfl(tot, 31, 64);
+        if (lane == 63) {
+            const int s0 = 2 * q;
+            if (a.passthrough) {
+                Y[d] = (uint16_t)bf16_rne(v0);
+            } else {
+                const float y0 = bf16_to_f32(bf16_rne(v0));
+                const float p0 = (s0 < a.topk ? bf16_to_f32(selw[s0]) : 1.0f) * y0;
+                facc = facc + p0;
+                if (s0 + 1 < a.nslots) {
+                    const float y1 = bf16_to_f32(bf16_rne(tot));
+                    const float p1 = (s0 + 1 < a.topk ? bf16_to_f32(selw[s0 + 1]) : 1.0f) * y1;
+                    facc = facc + p1;
+                }
+                if (q == a.np - 1) {
+                    Y[d] = (uint16_t)bf16_rne(facc);
+                    facc = 0.f;
+                }
+            }
         }
-        float facc = 0.f;
-        for (int s = 0; s < dg.nslots; ++s) {
-            const float g = s < dg.topk ? bf16_to_f32(selw[s]) : 1.0f;
-            const float prod = g * ys[r * dg.nslots + s];
-            facc = facc + prod;
-        }
-        Y[d0 + r] = (uint16_t)bf16_rne(facc);
+    };
+    for (int64_t u = 0; u < nunits; u += 2) {
+        step(u, ba);
+        if (u + 1 >= nunits) break;
+        step(u + 1, bb);
     }
 }
 
@@ -436,11 +550,55 @@ hipError_t run_stream(const Items& items, const Epi& epi, const uint16_t* X, int
     return hipGetLastError();
 }
 
+template <class Items, class Epi>
+hipError_t run_rows(const Items& items, const Epi& epi, const uint16_t* X, int64_t K, int64_t npairs, hipStream_t st) {
+    const int nsb = (int)(K / QK_K);
+    const int nseg = (nsb + kSegBlocks - 1) / kSegBlocks;
+    int64_t nwg = (npairs + kRowWaves - 1) / kRowWaves;
+    const int64_t cap = (int64_t)AIPU_ROW_WG_PER_CU * device_cu_count();
+    if (nwg > cap) nwg = cap;
+    const dim3 grid((unsigned)nwg), block(kRowWaves * 64);
+    switch (nseg) {
+        case 1: hipLaunchKernelGGL((k_rows<1, Items, Epi>), grid, block, 0, st, items, epi, X, nsb, npairs); break;
+        case 2: hipLaunchKernelGGL((k_rows<2, Items, Epi>), grid, block, 0, st, items, epi, X, nsb, npairs); break;
+        case 3: hipLaunchKernelGGL((k_rows<3, Items, Epi>), grid, block, 0, st, items, epi, X, nsb, npairs); break;
+        case 4: hipLaunchKernelGGL((k_rows<4, Items, Epi>), grid, block, 0, st, items, epi, X, nsb, npairs); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Epilogue of the row kernel for a plain GEMV (one activation row).
+struct RowsPlainEpi {
+    uint16_t* Y;
+    float* Yf;
+    int64_t N;
+    __device__ void operator()(int64_t pair, float v0, float v1) const {
+        const int64_t r = 2 * pair;
+        Y[r] = (uint16_t)bf16_rne(v0);
+        if (Yf) Yf[r] = v0;
+        if (r + 1 < N) {
+            Y[r + 1] = (uint16_t)bf16_rne(v1);
+            if (Yf) Yf[r + 1] = v1;
+        }
+    }
+};
+
+struct RowsGateUpEpi {
+    uint16_t* h;
+    __device__ void operator()(int64_t pair, float v0, float v1) const {
+        const uint32_t g = bf16_rne(v0), u = bf16_rne(v1);
+        h[pair] = (uint16_t)bf16_rne(bf16_to_f32(glm_silu_bf16(g)) * bf16_to_f32(u));
+    }
+};
+
 template <int TYPE, int PASSES>
 hipError_t gemv_stream_mc(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
                           float* yf, hipStream_t st) {
     const PlainItems items{W, N, row_bytes(TYPE, K)};
     const int64_t npairs = (N + 1) / 2;
+    if (TYPE == T_Q4_K && M == 1 && K <= 4 * kSegWeights)
+        return run_rows(items, RowsPlainEpi{y, yf, N}, x, K, npairs, st);
     hipError_t e = hipSuccess;
     for (int64_t m0 = 0; m0 < M && e == hipSuccess; m0 += 4) {
         const int mr = (int)((M - m0) < 4 ? (M - m0) : 4);
@@ -474,45 +632,49 @@ hipError_t launch_moe_gateup_fast(const uint8_t* G, const uint8_t* U, const uint
     const int64_t rb = row_bytes(T_Q4_K, H);
     const GateUpItems items{G, U, shG, shU, sel, topk, nslots, (int)I, (int)E, rb * I, rb};
     const int64_t npairs = (int64_t)nslots * I;
+    if (H <= 4 * kSegWeights) return run_rows(items, RowsGateUpEpi{h}, x, H, npairs, st);
     const GateUpEpi epi{h, npairs};
     return run_stream<T_Q4_K, 1, 4>(items, epi, x, H, 1, npairs, st);
 }
 
-int64_t moe_down_lds_bytes(int nslots, int64_t I, int rows_per_wg) {
+int64_t moe_down_lds_bytes(int nslots, int64_t I) {
     const int nseg = (int)((I / QK_K + kSegBlocks - 1) / kSegBlocks);
-    return (int64_t)nslots * nseg * 32 * 136 + (int64_t)rows_per_wg * nslots * 4;
+    return (int64_t)nslots * nseg * 32 * 136;
 }
+
+#ifndef AIPU_DOWN_WG_PER_CU
+#define AIPU_DOWN_WG_PER_CU 2
+#endif
 
 hipError_t launch_moe_down_fast(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
                                 int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h, uint16_t* y,
                                 int passthrough, hipStream_t st) {
-    DownGeom dg;
-    dg.passthrough = passthrough;
-    dg.nsb = (int)(I / QK_K);
-    dg.nseg = (dg.nsb + kSegBlocks - 1) / kSegBlocks;
-    if (dg.nseg > kMaxWaves) return hipErrorInvalidValue;
-    dg.segw = dg.nseg;
-    dg.rgc = dg.segw >= 4 ? 1 : (4 + dg.segw - 1) / dg.segw;
-    const int cus = device_cu_count();
-    int rows = (int)((H + cus - 1) / cus);
-    if (rows < 1) rows = 1;
-    if (rows > 64) rows = 64;
-    dg.rows_per_wg = rows;
-    dg.nslots = nslots;
-    dg.topk = topk;
-    dg.E = (int)E;
-    dg.H = H;
-    dg.I = I;
-    dg.rb = row_bytes(T_Q4_K, I);
-    dg.ebytes = dg.rb * H;
-    const int items = rows * nslots;
-    const int per_batch = dg.rgc * 2 * kDownPasses;
-    dg.nbatch = (items + per_batch - 1) / per_batch;
-    const int64_t lds = moe_down_lds_bytes(nslots, I, rows);
+    DownRowsArgs a;
+    a.nsb = (int)(I / QK_K);
+    const int nseg = (a.nsb + kSegBlocks - 1) / kSegBlocks;
+    a.nslots = nslots;
+    a.topk = topk;
+    a.E = (int)E;
+    a.np = (nslots + 1) / 2;
+    a.passthrough = passthrough;
+    a.H = H;
+    a.I = I;
+    a.rb = row_bytes(T_Q4_K, I);
+    a.ebytes = a.rb * H;
+    const int64_t lds = moe_down_lds_bytes(nslots, I);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((H + rows - 1) / rows));
-    const dim3 block(64 * dg.segw * dg.rgc);
-    hipLaunchKernelGGL(k_moe_down, grid, block, (size_t)lds, st, D, shD, sel, selw, h, y, dg);
+    const int waves = 4;
+    int64_t nwg = (H + waves - 1) / waves;
+    const int64_t cap = (int64_t)AIPU_DOWN_WG_PER_CU * device_cu_count();
+    if (nwg > cap) nwg = cap;
+    const dim3 grid((unsigned)nwg), block(64 * waves);
+    switch (nseg) {
+        case 1: hipLaunchKernelGGL(k_down_rows<1>, grid, block, (size_t)lds, st, D, shD, sel, selw, h, y, a); break;
+        case 2: hipLaunchKernelGGL(k_down_rows<2>, grid, block, (size_t)lds, st, D, shD, sel, selw, h, y, a); break;
+        case 3: hipLaunchKernelGGL(k_down_rows<3>, grid, block, (size_t)lds, st, D, shD, sel, selw, h, y, a); break;
+        case 4: hipLaunchKernelGGL(k_down_rows<4>, grid, block, (size_t)lds, st, D, shD, sel, selw, h, y, a); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -6,7 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/aipu_q4k.h"
+#include "aipu_q4k.h"
 
 namespace aipu {
 
@@ -17,8 +17,15 @@ hipError_t launch_bf16_round(const float* x, int64_t n, uint16_t* out, hipStream
 hipError_t launch_act(int which, const uint16_t* x, int64_t n, uint16_t* y, hipStream_t st);  // 0 silu, 1 sigmoid
 hipError_t launch_rsqrt(const float* x, int64_t n, float* y, hipStream_t st);
 hipError_t launch_stream_read(const void* p, int64_t bytes, uint32_t* sink, hipStream_t st);
+
+// router.hip
 hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t scale_bits,
                               int32_t* sel_idx, uint16_t* sel_w, uint16_t* gates, hipStream_t st);
+// bf16 router GEMV + tail in one launch; `counter` is a workspace word that must be 0 on
+// entry (the kernel leaves it 0).  sel2/selw2 (nullable) receive a copy of the routing.
+hipError_t launch_router_bf16_fused(const uint16_t* W, const uint16_t* x, int64_t K, int E, int topk,
+                                    uint32_t scale_bits, uint16_t* logits, uint32_t* counter, int32_t* sel,
+                                    uint16_t* selw, int32_t* sel2, uint16_t* selw2, hipStream_t st);
 
 // gemv_ref.hip -- bit-exact reference order
 hipError_t launch_gemv_ref(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,

@@ -20,7 +20,7 @@ hipError_t launch_moe_gateup_fast(const uint8_t* G, const uint8_t* U, const uint
 hipError_t launch_moe_down_fast(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
                                 int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h, uint16_t* y,
                                 int passthrough, hipStream_t st);
-int64_t moe_down_lds_bytes(int nslots, int64_t I, int rows_per_wg);
+int64_t moe_down_lds_bytes(int nslots, int64_t I);
 
 namespace {
 
@@ -28,13 +28,14 @@ constexpr int64_t kAlign = 256;
 inline int64_t up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    int64_t logits, sel, selw, h, g, u, ys, total;
+    int64_t counter, logits, sel, selw, h, g, u, ys, total;
 };
 
 WsLayout ws_layout(int64_t E, int64_t H, int64_t I, int topk) {
     const int64_t nslots = topk + 1;
     WsLayout L;
     int64_t o = 0;
+    L.counter = o; o += up(4);
     L.logits = o; o += up(E * 2);
     L.sel = o;    o += up(64 * 4);
     L.selw = o;   o += up(64 * 2);
@@ -107,16 +108,21 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
     const int nslots = a.topk + (has_shared ? 1 : 0);
     const bool fast = a.mode == AIPU_MODE_FAST && a.type == T_Q4_K;
 
-    // 1. router logits (bf16)
-    if (a.mode == AIPU_MODE_FAST && (a.router_type == T_Q4_K || a.router_type == T_BF16))
-        AIPU_TRY(launch_gemv_fast(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
-    else
-        AIPU_TRY(launch_gemv_ref(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
-    // 2. router tail
-    AIPU_TRY(launch_router_tail(logits, (int)a.E, a.topk, a.scale_bits, sel, selw, nullptr, st));
-    if (a.sel_idx_out || a.sel_w_out) {
-        hipLaunchKernelGGL(k_copy_sel, dim3(1), dim3(64), 0, st, sel, selw, a.topk, a.sel_idx_out, a.sel_w_out);
-        AIPU_TRY(hipGetLastError());
+    // 1-2. router logits (bf16) and router tail
+    if (a.mode == AIPU_MODE_FAST && a.router_type == T_BF16) {
+        AIPU_TRY(launch_router_bf16_fused((const uint16_t*)a.router_w, a.x, a.H, (int)a.E, a.topk, a.scale_bits,
+                                          logits, (uint32_t*)(ws + L.counter), sel, selw, a.sel_idx_out,
+                                          a.sel_w_out, st));
+    } else {
+        if (a.mode == AIPU_MODE_FAST && a.router_type == T_Q4_K)
+            AIPU_TRY(launch_gemv_fast(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
+        else
+            AIPU_TRY(launch_gemv_ref(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
+        AIPU_TRY(launch_router_tail(logits, (int)a.E, a.topk, a.scale_bits, sel, selw, nullptr, st));
+        if (a.sel_idx_out || a.sel_w_out) {
+            hipLaunchKernelGGL(k_copy_sel, dim3(1), dim3(64), 0, st, sel, selw, a.topk, a.sel_idx_out, a.sel_w_out);
+            AIPU_TRY(hipGetLastError());
+        }
     }
     if (fast) {
         AIPU_TRY(launch_moe_gateup_fast(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, sel, a.topk, nslots, a.E, a.H,

@@ -138,18 +138,29 @@ __device__ __forceinline__ Raw raw_load(const uint8_t* __restrict__ blk, const G
     return r;
 }
 
+// (x & 0x000F000F) | 0x43004300 in one v_bfi_b32: the two nibbles at bits 0-3 and 16-19
+// become the bf16 pair (128 + n0, 128 + n1).  The constants live in registers (gfx9 VOP3
+// encodings take no literals; one SGPR operand fits the constant-bus limit), so the
+// select is a single VALU op.
+__device__ __forceinline__ uint32_t nib2bf(uint32_t x, uint32_t mask, uint32_t bias) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(x), "v"(bias));
+    return r;
+}
+
 // Sub-block dot sums of one lane: S = sum (128 + q) * a over its 32 low-nibble and 32
 // high-nibble weights.
 __device__ __forceinline__ void code_dots(const Raw& r, const Act& A, float& Slo, float& Shi) {
     const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t M = __builtin_amdgcn_readfirstlane(0x000F000Fu), B = 0x43004300u;
     float l0 = 0.f, l1 = 0.f, h0 = 0.f, h1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint32_t x = q[i];
-        const uint32_t c0 = (x & 0x000F000Fu) | 0x43004300u;          // bytes 0,2 low nibble
-        const uint32_t c1 = ((x >> 8) & 0x000F000Fu) | 0x43004300u;   // bytes 1,3 low nibble
-        const uint32_t c2 = ((x >> 4) & 0x000F000Fu) | 0x43004300u;   // bytes 0,2 high nibble
-        const uint32_t c3 = ((x >> 12) & 0x000F000Fu) | 0x43004300u;  // bytes 1,3 high nibble
+        const uint32_t c0 = nib2bf(x, M, B);          // bytes 0,2 low nibble
+        const uint32_t c1 = nib2bf(x >> 8, M, B);     // bytes 1,3 low nibble
+        const uint32_t c2 = nib2bf(x >> 4, M, B);     // bytes 0,2 high nibble
+        const uint32_t c3 = nib2bf(x >> 12, M, B);    // bytes 1,3 high nibble
         l0 = dot2(A.xa[4 * i + 0], c0, l0);
         l1 = dot2(A.xa[4 * i + 1], c1, l1);
         h0 = dot2(A.xa[4 * i + 2], c2, h0);
@@ -185,6 +196,23 @@ __device__ __forceinline__ float lane_part(const Hdr& H, float Slo, float Shi, c
     const float u = __builtin_fmaf(H.sc1, thi, H.sc0 * tlo);
     const float v = __builtin_fmaf(H.m1, A.ahi, H.m0 * A.alo);
     return __builtin_fmaf(H.d, u, -(H.dm * v));
+}
+
+// Sum over the 32 lanes of each half-wave with DPP: quad xor 1, quad xor 2, half-row mirror,
+// row mirror (each lane then holds its 16-lane row sum), and a row_bcast:15 into rows 1
+// and 3.  The half-wave totals land in lanes 16..31 and 48..63.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xF, false));
+}
+
+__device__ __forceinline__ float half_sum_dpp(float v) {
+    v += dpp_f<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f<0x141, 0xF>(v);   // row_half_mirror
+    v += dpp_f<0x140, 0xF>(v);   // row_mirror
+    v += dpp_f<0x142, 0xA>(v);   // row_bcast:15 -> rows 1, 3
+    return v;
 }
 
 // Sum V values across the 32 lanes of each half-wave with a transposing butterfly: the

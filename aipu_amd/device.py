@@ -158,10 +158,12 @@ def router_topk(logits, topk, scale_bits=RSCALE_BITS, return_gates=False):
 
 
 def moe_workspace(E, H, I, topk, device):
+    """Zero-filled workspace (the fused router keeps a ticket word in it that must start at 0;
+    every call leaves it at 0 again)."""
     n = _lib.lib().aipu_moe_workspace_bytes(E, H, I, topk)
     if n < 0:
         raise ValueError("bad MoE shape")
-    return torch.empty(n, dtype=torch.uint8, device=device)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
 def swiglu_expert(ggml_type, wg, wu, wd, H, I, x, mode="fast", workspace=None, return_h=False):

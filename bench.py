@@ -83,7 +83,21 @@ def pct(vals, q):
     return float(np.percentile(np.asarray(vals), q))
 
 
-def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label=""):
+def time_eager(fn_list):
+    """Eager launches bracketed by HIP events (lets a kernel tracer see every dispatch)."""
+    import torch
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for f in fn_list:
+        f()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
+def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label="", eager=False):
     """Rotating-buffer GEMV timing.  Returns dict with us/launch, GB/s, percentiles, hot number."""
     device = "cuda"
     wb = q4k_bytes(N, K)
@@ -102,6 +116,14 @@ def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label
         launcher(i)()
     torch.cuda.synchronize()
     fns = [launcher(i) for i in range(steps)]
+    if eager:
+        total_ms = time_eager(fns)
+        alg = wb + 2 * K * M + 2 * N * M
+        us = 1000.0 * total_ms / steps
+        log(f"{label} eager N={N} K={K} M={M} {mode}: {us:.2f} us/launch, {alg / (us * 1e-6) / 1e9:.0f} GB/s")
+        return dict(N=N, K=K, M=M, mode=mode, us_per_launch=us, gbs=alg / (us * 1e-6) / 1e9, alg_bytes=alg,
+                    weight_rotation_bytes=nbuf * wb, rotation_buffers=nbuf, pct_peak=100.0 * alg / (us * 1e-6) / 1e9 / PEAK_GBS,
+                    timing="eager launches")
     ms, _ = time_graph(fns, reps=1)
     total_ms = ms[0]
     # launch-group distribution: graphs of nbuf launches, replayed
@@ -135,6 +157,19 @@ def bench_stream_read(dev, torch, nbytes=2 << 30, reps=10):
     del buf
     torch.cuda.empty_cache()
     return dict(bytes=nbytes, gbs_best=nbytes / (best * 1e-3) / 1e9, gbs_median=nbytes / (pct(ms, 50) * 1e-3) / 1e9)
+
+
+def bench_stream_read_sized(dev, torch, nbytes, rot_bytes, steps=1000):
+    """Read ceiling at one GEMV's size: `nbytes` per launch over rotating buffers."""
+    nbuf = max(2, math.ceil(rot_bytes / nbytes))
+    nb16 = (nbytes + 15) // 16 * 16
+    buf = torch.ones(nbuf * nb16, dtype=torch.uint8, device="cuda").view(nbuf, nb16)
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    ms, _ = time_graph([(lambda j=i % nbuf: dev.stream_read(buf[j], sink)) for i in range(steps)], reps=2)
+    us = 1000.0 * min(ms) / steps
+    del buf
+    torch.cuda.empty_cache()
+    return dict(bytes=nb16, us_per_launch=us, gbs=nb16 / (us * 1e-6) / 1e9)
 
 
 def bench_moe(dev, torch, steps, E=256, H=6144, I=2048, topk=8, mode="fast"):
@@ -279,6 +314,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=200)
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of one HIP graph")
+    ap.add_argument("--only", choices=["gemv", "moe", "stream"], default=None,
+                    help="run one measurement only (for kernel tracing)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU sharding is a design "
@@ -294,11 +332,25 @@ def main():
     torch.cuda.init()
     rot = 0.3e9 if args.quick else 1.05e9
 
-    head = bench_gemv(dev, torch, 6144, 6144, 1, args.steps, args.warmup, rot, label="north star")
+    if args.only == "moe":
+        print(json.dumps(bench_moe(dev, torch, args.moe_steps)))
+        return
+    if args.only == "stream":
+        r = bench_stream_read(dev, torch)
+        r["gemv_size"] = bench_stream_read_sized(dev, torch, q4k_bytes(6144, 6144) + 4 * 6144, rot)
+        print(json.dumps(r))
+        return
+    head = bench_gemv(dev, torch, 6144, 6144, 1, args.steps, args.warmup, rot, label="north star", eager=args.eager)
+    if args.only == "gemv":
+        print(json.dumps(head))
+        return
     extra = {}
     if not args.no_extra:
         extra["stream_read_ceiling"] = bench_stream_read(dev, torch)
         log(f"stream read ceiling: {extra['stream_read_ceiling']['gbs_best']:.0f} GB/s")
+        extra["stream_read_gemv_size"] = bench_stream_read_sized(dev, torch, head["alg_bytes"], rot)
+        log(f"stream read of one GEMV's bytes per launch: {extra['stream_read_gemv_size']['us_per_launch']:.2f} us, "
+            f"{extra['stream_read_gemv_size']['gbs']:.0f} GB/s")
         extra["moe_decode_c2"] = bench_moe(dev, torch, args.moe_steps)
         extra["gemv_c0_4096"] = bench_gemv(dev, torch, 4096, 4096, 1, 1000, 50, rot, label="C0")
         for M in (2, 4, 8):

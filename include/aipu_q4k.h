@@ -6,8 +6,8 @@
  *   - takes plain device pointers and int64 sizes (no framework types);
  *   - is stream-ordered on the hipStream_t passed as `stream` (NULL = default stream)
  *     and never synchronises the host;
- *   - never allocates device memory; entry points that need scratch take a caller-owned
- *     `workspace` of at least the size the matching *_workspace_bytes() call returns;
+ *   - never allocates device memory; entry points that need scratch take a caller-owned,
+ *     zero-initialised `workspace` of at least the size *_workspace_bytes() returns;
  *   - validates its arguments before touching the GPU and returns AIPU_OK (0) or a negative
  *     status; aipu_last_error() then returns a thread-local message.
  *
@@ -121,7 +121,10 @@ int aipu_fp32_rsqrt(const float* x, int64_t n, float* y, void* stream);
 int aipu_router_topk(const uint16_t* logits, int64_t E, int topk, uint32_t scale_bits,
                      int32_t* sel_idx, uint16_t* sel_w, uint16_t* gates, void* stream);
 
-/* Workspace bytes for aipu_swiglu_expert / aipu_moe_swiglu_decode. */
+/* Workspace bytes for aipu_swiglu_expert / aipu_moe_swiglu_decode.  The workspace must be
+ * zero-filled before its first use (it holds a ticket counter the decode step's router
+ * uses for its last-workgroup hand-off; every call leaves it at zero again) and must not be
+ * shared by calls that can run concurrently. */
 int64_t aipu_moe_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
 
 /* One SwiGLU expert: gate/up GEMVs (bf16), h = bf16(f32(silu(gate)) * f32(up)),

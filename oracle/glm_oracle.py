@@ -304,7 +304,9 @@ def router_logits(router_type, router_w, E, H, x_bits):
     ``router_type`` is a ggml type id (bf16 weights use ``BF16_TYPE``).
     """
     if router_type == BF16_TYPE:
-        w = qo.bf16_bits_to_f32(np.asarray(router_w, np.uint16).reshape(E, H))
+        rw = np.asarray(router_w)
+        rw = rw.view(np.uint16) if rw.dtype == np.uint8 else rw.astype(np.uint16)
+        w = qo.bf16_bits_to_f32(rw.reshape(E, H))
         _, y = qo.gemv_ref(w, qo.bf16_bits_to_f32(np.asarray(x_bits, np.uint16))[None, :])
         return y[0]
     _, y = qo.gemv_quant_ref(router_type, router_w, E, H, x_bits)

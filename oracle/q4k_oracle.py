@@ -412,6 +412,28 @@ def tolerance_gate(wdeq, x, acc_test, rel=1e-5):
     return bool(np.all(delta <= bound)), float(np.max(ratio)) if ratio.size else 0.0
 
 
+def bf16_parity(y_test_bits, acc_ref, wdeq, x, rel=1e-5):
+    """bf16 outputs of a reordered sum vs the reference-order accumulators.
+
+    Where the sum is well conditioned (|acc_ref| >= 2^9 * rel * sum|a*w|, so that two
+    in-tolerance fp32 results cannot straddle more than one bf16 rounding boundary) the
+    outputs must be within 1 bf16 ulp; elsewhere (cancelled sums) they must be within the
+    accumulator tolerance plus one ulp.  Returns (ok, max_ulp_well_conditioned, n_cancelled).
+    """
+    w = np.asarray(wdeq, dtype=np.float64)
+    xx = np.atleast_2d(np.asarray(x, dtype=np.float64))
+    mag = np.abs(xx) @ np.abs(w).T
+    ref_bits = bf16_round_bits(np.asarray(acc_ref, np.float32))
+    ulp = bf16_ulp_distance(y_test_bits, ref_bits)
+    acc = np.abs(np.asarray(acc_ref, np.float64))
+    good = acc >= (2 ** 9) * rel * mag
+    yt = bf16_bits_to_f32(y_test_bits).astype(np.float64)
+    yr = bf16_bits_to_f32(ref_bits).astype(np.float64)
+    loose = np.abs(yt - yr) <= rel * mag + np.abs(yr) * 2.0 ** -7
+    ok = bool(np.all(ulp[good] <= 1) and np.all(loose[~good]))
+    return ok, int(ulp[good].max()) if good.any() else 0, int((~good).sum())
+
+
 def bf16_ulp_distance(a_bits, b_bits):
     """|ordered-integer distance| between bf16 bit patterns (sign-magnitude ordering)."""
     def key(b):

@@ -203,7 +203,7 @@ def test_mixed_tiles(mode):
     else:
         ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
         assert ok, worst
-        assert qo.bf16_ulp_distance(h_bits(y), qo.bf16_round_bits(acc)).max() <= 1
+        assert qo.bf16_parity(h_bits(y), acc, w, qo.bf16_bits_to_f32(x))[0]
 
 
 # --------------------------------------------------- reference-interface mirrors
