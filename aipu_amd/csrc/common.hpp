@@ -65,6 +65,27 @@ __device__ __forceinline__ float q4k_weight_exact(float D, float Mn, uint32_t q)
     return p - Mn;
 }
 
+// ------------------------------------------------------------ buffer loads
+// Raw buffer loads through a buffer resource of `bytes` bytes: an access at or beyond
+// `bytes` returns 0 instead of touching memory.  Used where a load must be issued
+// unconditionally (so the compiler neither branches around it nor waits for unrelated
+// earlier loads where branches join) but may fall outside the data.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    // word 3 = 0x00020000: raw (untyped) 32-bit data format on gfx9-family parts
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
+}
+
 // ---------------------------------------------------------------- wave helpers
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
     return __shfl_xor(v, mask, 64);

@@ -112,11 +112,13 @@ struct Pow2 {
 struct PlainItems {
     const uint8_t* W;
     int64_t N, rb;
-    __device__ const uint8_t* row(int64_t pair, int half) const {
+    __device__ int expert(int64_t) const { return 0; }
+    __device__ const uint8_t* row_e(int64_t pair, int half, int) const {
         int64_t r = 2 * pair + half;
         r = r < N ? r : N - 1;
         return W + r * rb;
     }
+    __device__ const uint8_t* row(int64_t pair, int half) const { return row_e(pair, half, 0); }
 };
 
 struct PlainEpi {
@@ -149,21 +151,26 @@ struct GateUpItems {
     int topk, nslots, I;
     int E;
     int64_t ebytes, rb;
-    __device__ const uint8_t* row(int64_t pair, int half) const {
+    // Routed expert of the item's slot (loaded from the router's output), clamped to [0, E).
+    __device__ int expert(int64_t pair) const {
         const int npairs = nslots * I;
-        int p = (int)(pair < npairs ? pair : npairs - 1);
+        const int p = (int)(pair < npairs ? pair : npairs - 1);
+        const int s = p / I;
+        // a buffer load (0 beyond the topk entries) rather than a branch around a load: at
+        // a branch join the compiler would wait for every earlier load
+        const int e = (int)buf_load4(buf_rsrc(sel, 4u * (uint32_t)topk), 4u * (uint32_t)s);
+        return e < 0 ? 0 : (e >= E ? E - 1 : e);
+    }
+    __device__ const uint8_t* row_e(int64_t pair, int half, int e) const {
+        const int npairs = nslots * I;
+        const int p = (int)(pair < npairs ? pair : npairs - 1);
         const int s = p / I;
         const int i = p - s * I;
-        const uint8_t* base;
-        if (s < topk) {
-            int e = sel[s];
-            e = e < 0 ? 0 : (e >= E ? E - 1 : e);
-            base = (half ? U : G) + (int64_t)e * ebytes;
-        } else {
-            base = half ? shU : shG;
-        }
-        return base + (int64_t)i * rb;
+        const uint8_t* routed = (half ? U : G) + (int64_t)e * ebytes;
+        const uint8_t* shared = half ? shU : shG;
+        return (s < topk ? routed : shared) + (int64_t)i * rb;
     }
+    __device__ const uint8_t* row(int64_t pair, int half) const { return row_e(pair, half, expert(pair)); }
 };
 
 // h = bf16(f32(glm_silu(bf16 gate)) * f32(bf16 up))  (tools/glm_model_q4k_ref.py:705-707)
@@ -257,23 +264,20 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_stream(Items items, Epi epi,
 // pipelined: the loads of pair p + 2*nw are issued as soon as pair p's registers are free.
 // Launch shape of the row kernel (compile-time): waves per workgroup and the cap on
 // workgroups per CU used to size the grid.
-#ifndef AIPU_ROW_WAVES
-#define AIPU_ROW_WAVES 4
-#endif
-#ifndef AIPU_ROW_WG_PER_CU
-#define AIPU_ROW_WG_PER_CU 4
-#endif
-constexpr int kRowWaves = AIPU_ROW_WAVES;
+// Launch shape of the row kernel: 4-wave workgroups (one wave per SIMD), at most
+// kRowWgPerCu per CU; waves loop over row pairs.  Measured on MI355X at K=N=6144 this
+// beats both thinner grids (one pair per wave, staging repeated per 4 pairs) and fat
+// 8/12-wave workgroups (one per CU, all waves held at the staging barriers).
+constexpr int kRowWaves = 4;
+constexpr int kRowWgPerCu = 2;
 
 template <int NSEG>
 struct RowBuf {
     Raw r[NSEG];
 };
 
-template <int NSEG, class Items>
-__device__ __forceinline__ void rows_load(RowBuf<NSEG>& b, const Items& items, int64_t pair, const Geo& G,
-                                          const int (&blkc)[NSEG]) {
-    const uint8_t* row = items.row(pair, G.half);
+template <int NSEG>
+__device__ __forceinline__ void rows_load(RowBuf<NSEG>& b, const uint8_t* row, const Geo& G, const int (&blkc)[NSEG]) {
 #pragma unroll
     for (int s = 0; s < NSEG; ++s) b.r[s] = raw_load(row + (int64_t)blkc[s] * 144, G);
 }
@@ -311,8 +315,9 @@ __device__ __forceinline__ float rows_part(const RowBuf<NSEG>& b, const uint4* s
 template <int NSEG, class Items, class Epi>
 __global__ __launch_bounds__(kRowWaves * 64) void k_rows(Items items, Epi epi, const uint16_t* __restrict__ X,
                                                         int nsb, int64_t npairs) {
-    __shared__ uint4 sxa[NSEG * 8 * 32];
-    __shared__ float2 ssum[NSEG * 32];
+    __shared__ uint4 snat[NSEG * 256];          // activations in natural order (8 bf16 per entry)
+    __shared__ uint4 sxa[NSEG * 8 * 32];        // activations in the lanes' dot2 order
+    __shared__ float2 ssum[NSEG * 32];          // per-lane sub-block activation sums
     const int lane = threadIdx.x & 63;
     const Geo G = make_geo(lane);
     const int64_t nw = (int64_t)gridDim.x * kRowWaves;
@@ -325,31 +330,64 @@ __global__ __launch_bounds__(kRowWaves * 64) void k_rows(Items items, Epi epi, c
         ok[s] = blk < nsb;
         blkc[s] = ok[s] ? blk : 0;
     }
-    RowBuf<NSEG> ba, bb;
-    if (p0 < npairs) rows_load(ba, items, p0, G, blkc);
-    if (p0 + nw < npairs) rows_load(bb, items, p0 + nw, G, blkc);
+    // Row addresses first: for routed experts they depend on a load of the expert id.
+    const int e_a = items.expert(p0), e_b = items.expert(p0 + nw);
+    const uint8_t* row_a = items.row_e(p0, G.half, e_a);
+    const uint8_t* row_b = items.row_e(p0 + nw, G.half, e_b);
+    __builtin_amdgcn_sched_barrier(0);
 
+    // Activations: every thread loads NSEG 16-B pieces of x, unconditionally (clamped
+    // address, masked value), before any weight load.  Vector loads complete in order, so
+    // storing them to LDS below waits only for these small cache-resident loads, never for
+    // the weight stream, and no workgroup waits at the barriers for HBM.
+    static_assert(kRowWaves == 4, "the activation staging assumes 256 threads");
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)nsb * QK_K * 2u);   // 0 beyond K
+    uint4 xv[NSEG];
+#pragma unroll
+    for (int j = 0; j < NSEG; ++j) xv[j] = buf_load16(xr, 16u * (threadIdx.x + 256u * j));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Unconditional (Items::row clamps out-of-range pairs to a valid row).
+    RowBuf<NSEG> ba, bb;
+    rows_load(ba, row_a, G, blkc);
+    rows_load(bb, row_b, G, blkc);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int j = 0; j < NSEG; ++j) snat[threadIdx.x + 256 * j] = xv[j];
+    __syncthreads();
     if (threadIdx.x < NSEG * 32) {
-        const int s = threadIdx.x >> 5, ls = threadIdx.x & 31;
-        const Geo g2 = make_geo(ls);
+        const int st_s = threadIdx.x >> 5, st_l = threadIdx.x & 31;
+        const Geo g2 = make_geo(st_l);
+        const int base = ((st_s * kSegBlocks + g2.bs) * QK_K + 64 * g2.g) / 8;
+        uint32_t xs[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = snat[base + i];
+            xs[4 * i] = v.x;
+            xs[4 * i + 1] = v.y;
+            xs[4 * i + 2] = v.z;
+            xs[4 * i + 3] = v.w;
+        }
         Act A;
-        act_load(A, X, s, g2, s * kSegBlocks + g2.bs < nsb);
+        act_from_natural(A, xs);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            sxa[(s * 8 + i) * 32 + ls] = make_uint4(A.xa[4 * i], A.xa[4 * i + 1], A.xa[4 * i + 2], A.xa[4 * i + 3]);
-        ssum[s * 32 + ls] = make_float2(A.alo, A.ahi);
+            sxa[(st_s * 8 + i) * 32 + st_l] =
+                make_uint4(A.xa[4 * i], A.xa[4 * i + 1], A.xa[4 * i + 2], A.xa[4 * i + 3]);
+        ssum[st_s * 32 + st_l] = make_float2(A.alo, A.ahi);
     }
     __syncthreads();
 
     for (int64_t p = p0; p < npairs; p += 2 * nw) {
         float tot = half_sum_dpp(rows_part<NSEG>(ba, sxa, ssum, G, ok));
-        if (p + 2 * nw < npairs) rows_load(ba, items, p + 2 * nw, G, blkc);
+        if (p + 2 * nw < npairs) rows_load(ba, items.row(p + 2 * nw, G.half), G, blkc);
         float other = __shfl(tot, 31, 64);
         if (lane == 63) epi(p, other, tot);
         const int64_t q = p + nw;
         if (q >= npairs) break;
         tot = half_sum_dpp(rows_part<NSEG>(bb, sxa, ssum, G, ok));
-        if (q + 2 * nw < npairs) rows_load(bb, items, q + 2 * nw, G, blkc);
+        if (q + 2 * nw < npairs) rows_load(bb, items.row(q + 2 * nw, G.half), G, blkc);
         other = __shfl(tot, 31, 64);
         if (lane == 63) epi(q, other, tot);
     }
@@ -375,21 +413,29 @@ struct DownBuf {
     Raw r[NSEG];
 };
 
-template <int NSEG>
-__device__ __forceinline__ void down_load(DownBuf<NSEG>& b, const uint8_t* D, const uint8_t* shD, const int32_t* sel,
-                                          const DownRowsArgs& a, int64_t d, int q, const Geo& G,
-                                          const int (&blkc)[NSEG]) {
+// Expert of pass q's slot for this lane's half-wave (loaded from the router's output).
+__device__ __forceinline__ int down_expert(const int32_t* sel, const DownRowsArgs& a, int q, const Geo& G) {
     int s = 2 * q + G.half;
     s = s < a.nslots ? s : a.nslots - 1;
-    const uint8_t* base;
-    if (s < a.topk) {
-        int e = sel[s];
-        e = e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
-        base = D + (int64_t)e * a.ebytes;
-    } else {
-        base = shD;
-    }
-    const uint8_t* row = base + d * a.rb;
+    // a buffer load (0 beyond the topk entries) rather than a branch around a load
+    const int e = (int)buf_load4(buf_rsrc(sel, 4u * (uint32_t)a.topk), 4u * (uint32_t)s);
+    return e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
+}
+
+__device__ __forceinline__ const uint8_t* down_row_e(const uint8_t* D, const uint8_t* shD, const DownRowsArgs& a,
+                                                     int64_t d, int q, const Geo& G, int e) {
+    int s = 2 * q + G.half;
+    s = s < a.nslots ? s : a.nslots - 1;
+    return (s < a.topk ? D + (int64_t)e * a.ebytes : shD) + d * a.rb;
+}
+
+__device__ __forceinline__ const uint8_t* down_row(const uint8_t* D, const uint8_t* shD, const int32_t* sel,
+                                                   const DownRowsArgs& a, int64_t d, int q, const Geo& G) {
+    return down_row_e(D, shD, a, d, q, G, down_expert(sel, a, q, G));
+}
+
+template <int NSEG>
+__device__ __forceinline__ void down_load(DownBuf<NSEG>& b, const uint8_t* row, const Geo& G, const int (&blkc)[NSEG]) {
 #pragma unroll
     for (int g = 0; g < NSEG; ++g) b.r[g] = raw_load(row + (int64_t)blkc[g] * 144, G);
 }
@@ -419,23 +465,67 @@ __global__ __launch_bounds__(256) void k_down_rows(const uint8_t* __restrict__ D
     // this wave's units: rows d = w0 + k*nw, passes q = 0..np-1
     const int64_t nrows_w = w0 < a.H ? (a.H - w0 + nw - 1) / nw : 0;
     const int64_t nunits = nrows_w * a.np;
-    DownBuf<NSEG> ba, bb;
-    if (nunits > 0) down_load(ba, D, shD, sel, a, w0, 0, G, blkc);
-    if (nunits > 1) down_load(bb, D, shD, sel, a, w0 + (1 / a.np) * nw, 1 % a.np, G, blkc);
 
-    for (int u = threadIdx.x; u < units; u += blockDim.x) {
-        const int sl = u / (NSEG * 32);
+    // Row addresses of the first two units first: they depend on a load of the expert id.
+    const int64_t dmax = a.H - 1;
+    const int64_t d1r = w0 + (1 / a.np) * nw;
+    const int e_a = down_expert(sel, a, 0, G), e_b = down_expert(sel, a, 1 % a.np, G);
+    const uint8_t* row_a = down_row_e(D, shD, a, w0 < dmax ? w0 : dmax, 0, G, e_a);
+    const uint8_t* row_b = down_row_e(D, shD, a, d1r < dmax ? d1r : dmax, 1 % a.np, G, e_b);
+
+    // Activation staging: each thread owns at most two units (the launcher guarantees
+    // units <= 2 * blockDim.x).  Their loads are issued before the weight loads so that
+    // waiting for them does not wait for the weight stream (vector loads complete in order).
+    uint32_t xs0[32], xs1[32];
+    const int u0 = threadIdx.x, u1 = threadIdx.x + blockDim.x;
+    auto unit_geo = [&](int u, int& sl, int& seg, int& ls) {
+        sl = u / (NSEG * 32);
         const int rem = u - sl * NSEG * 32;
-        const int seg = rem >> 5, ls = rem & 31;
-        const Geo g2 = make_geo(ls);
+        seg = rem >> 5;
+        ls = rem & 31;
+    };
+    {
+        // buffer loads over h[nslots][I]: an invalid unit reads past the end and gets 0
+        const __amdgpu_buffer_rsrc_t hr = buf_rsrc(hbuf, (uint32_t)(a.nslots * a.I * 2));
+        auto unit_load = [&](int u, uint32_t (&xs)[32]) {
+            int sl, seg, ls;
+            unit_geo(u, sl, seg, ls);
+            const Geo gg = make_geo(ls);
+            const bool valid = u < units && seg * kSegBlocks + gg.bs < a.nsb;
+            const uint32_t off = valid ? 2u * (uint32_t)(sl * a.I + (seg * kSegBlocks + gg.bs) * QK_K + 64 * gg.g)
+                                       : 0x7FFFFFF0u;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint4 v = buf_load16(hr, off + 16u * i);
+                xs[4 * i] = v.x;
+                xs[4 * i + 1] = v.y;
+                xs[4 * i + 2] = v.z;
+                xs[4 * i + 3] = v.w;
+            }
+        };
+        unit_load(u0, xs0);
+        unit_load(u1, xs1);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the activation loads ahead of the weight loads
+
+    // Unconditional loads (rows clamped into range) keep the activation wait static.
+    DownBuf<NSEG> ba, bb;
+    down_load(ba, row_a, G, blkc);
+    down_load(bb, row_b, G, blkc);
+
+    auto stage = [&](int u, const uint32_t (&xs)[32]) {
+        int sl, seg, ls;
+        unit_geo(u, sl, seg, ls);
         Act A;
-        act_load(A, hbuf + (int64_t)sl * a.I, seg, g2, seg * kSegBlocks + g2.bs < a.nsb);
+        act_from_natural(A, xs);
         const int base = (u >> 5) * 256;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             lxa[base + i * 32 + ls] = make_uint4(A.xa[4 * i], A.xa[4 * i + 1], A.xa[4 * i + 2], A.xa[4 * i + 3]);
         lsum[u] = make_float2(A.alo, A.ahi);
-    }
+    };
+    if (u0 < units) stage(u0, xs0);
+    if (u1 < units) stage(u1, xs1);
     __syncthreads();
 
     float facc = 0.f;
@@ -471,7 +561,7 @@ __global__ __launch_bounds__(256) void k_down_rows(const uint8_t* __restrict__ D
         }
         if (u + 2 < nunits) {
             const int64_t r2 = (u + 2) / a.np;
-            down_load(cur, D, shD, sel, a, w0 + r2 * nw, (int)(u + 2 - r2 * a.np), G, blkc);
+            down_load(cur, down_row(D, shD, sel, a, w0 + r2 * nw, (int)(u + 2 - r2 * a.np), G), G, blkc);
         }
         const float tot = half_sum_dpp(svalid ? part : 0.f);
         const float v0 = __shfl(tot, 31, 64);
@@ -555,7 +645,7 @@ hipError_t run_rows(const Items& items, const Epi& epi, const uint16_t* X, int64
     const int nsb = (int)(K / QK_K);
     const int nseg = (nsb + kSegBlocks - 1) / kSegBlocks;
     int64_t nwg = (npairs + kRowWaves - 1) / kRowWaves;
-    const int64_t cap = (int64_t)AIPU_ROW_WG_PER_CU * device_cu_count();
+    const int64_t cap = (int64_t)kRowWgPerCu * device_cu_count();
     if (nwg > cap) nwg = cap;
     const dim3 grid((unsigned)nwg), block(kRowWaves * 64);
     switch (nseg) {
@@ -664,6 +754,7 @@ hipError_t launch_moe_down_fast(const uint8_t* D, const uint8_t* shD, const int3
     const int64_t lds = moe_down_lds_bytes(nslots, I);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     const int waves = 4;
+    if ((int64_t)nslots * nseg * 32 > 2 * 64 * waves) return hipErrorInvalidValue;   // <= 2 staging units per thread
     int64_t nwg = (H + waves - 1) / waves;
     const int64_t cap = (int64_t)AIPU_DOWN_WG_PER_CU * device_cu_count();
     if (nwg > cap) nwg = cap;

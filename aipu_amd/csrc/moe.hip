@@ -159,8 +159,11 @@ hipError_t launch_swiglu_expert(int type, const void* wg, const void* wu, const 
     const uint8_t* U = (const uint8_t*)wu;
     const uint8_t* D = (const uint8_t*)wd;
     if (mode == AIPU_MODE_FAST && type == T_Q4_K) {
-        AIPU_TRY(launch_moe_gateup_fast(G, U, G, U, nullptr, 0, 1, 1, H, I, x, h, st));
-        return launch_moe_down_fast(D, D, nullptr, nullptr, 0, 1, 1, H, I, h, y, 1, st);
+        // No routing: the expert runs as the shared slot.  The kernels still read one
+        // (ignored) expert id, so they get the workspace's id slot rather than a null pointer.
+        const int32_t* no_sel = (const int32_t*)(ws + L.sel);
+        AIPU_TRY(launch_moe_gateup_fast(G, U, G, U, no_sel, 0, 1, 1, H, I, x, h, st));
+        return launch_moe_down_fast(D, D, no_sel, nullptr, 0, 1, 1, H, I, h, y, 1, st);
     }
     uint16_t* g = (uint16_t*)(ws + L.g);
     uint16_t* u = (uint16_t*)(ws + L.u);

@@ -84,13 +84,15 @@ __device__ __forceinline__ void act_from_natural(Act& A, const uint32_t (&xs)[32
         A.xa[4 * i + 2] = perm(xs[17 + 2 * i], xs[16 + 2 * i], 0x05040100u);  // a[32+4i], a[34+4i]
         A.xa[4 * i + 3] = perm(xs[17 + 2 * i], xs[16 + 2 * i], 0x07060302u);  // a[33+4i], a[35+4i]
     }
+    // sub-block sums with dot2 against (1.0, 1.0): each product is exact, fp32 adds round
+    const uint32_t ones = 0x3F803F80u;
     float lo0 = 0.f, lo1 = 0.f, hi0 = 0.f, hi1 = 0.f;
 #pragma unroll
     for (int n = 0; n < 16; n += 2) {
-        lo0 += bf16_to_f32(xs[n] & 0xFFFFu) + bf16_to_f32(xs[n] >> 16);
-        lo1 += bf16_to_f32(xs[n + 1] & 0xFFFFu) + bf16_to_f32(xs[n + 1] >> 16);
-        hi0 += bf16_to_f32(xs[16 + n] & 0xFFFFu) + bf16_to_f32(xs[16 + n] >> 16);
-        hi1 += bf16_to_f32(xs[17 + n] & 0xFFFFu) + bf16_to_f32(xs[17 + n] >> 16);
+        lo0 = dot2(xs[n], ones, lo0);
+        lo1 = dot2(xs[n + 1], ones, lo1);
+        hi0 = dot2(xs[16 + n], ones, hi0);
+        hi1 = dot2(xs[17 + n], ones, hi1);
     }
     A.alo = lo0 + lo1;
     A.ahi = hi0 + hi1;
@@ -103,24 +105,30 @@ __device__ __forceinline__ void act_zero(Act& A) {
     A.ahi = 0.f;
 }
 
-// Load the lane's activations for segment `seg` of activation row `xrow` (K bf16).
-__device__ __forceinline__ void act_load(Act& A, const uint16_t* __restrict__ xrow, int seg, const Geo& G,
-                                         bool valid) {
-    if (!valid) {
-        act_zero(A);
-        return;
-    }
+// The 64 natural-order activations a lane owns in segment `seg` of activation row `xrow`
+// (K bf16), as 32 dwords; zeros when `valid` is false.
+// The loads are issued unconditionally (from `xsafe`, any 16-B aligned address with 64
+// readable bf16, when !valid) and masked afterwards: a branch around them would make the
+// compiler wait for every earlier vector load where the paths join.
+__device__ __forceinline__ void act_load_natural(uint32_t (&xs)[32], const uint16_t* __restrict__ xrow, int seg,
+                                                 const Geo& G, bool valid, const uint16_t* xsafe) {
     const int64_t k0 = (int64_t)(seg * kSegBlocks + G.bs) * QK_K + 64 * G.g;
-    const uint4* p = (const uint4*)(xrow + k0);
-    uint32_t xs[32];
+    const uint4* p = (const uint4*)(valid ? xrow + k0 : xsafe);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint4 v = p[i];
-        xs[4 * i + 0] = v.x;
-        xs[4 * i + 1] = v.y;
-        xs[4 * i + 2] = v.z;
-        xs[4 * i + 3] = v.w;
+        xs[4 * i + 0] = valid ? v.x : 0u;
+        xs[4 * i + 1] = valid ? v.y : 0u;
+        xs[4 * i + 2] = valid ? v.z : 0u;
+        xs[4 * i + 3] = valid ? v.w : 0u;
     }
+}
+
+// Load the lane's activations for segment `seg` of activation row `xrow` (K bf16).
+__device__ __forceinline__ void act_load(Act& A, const uint16_t* __restrict__ xrow, int seg, const Geo& G,
+                                         bool valid) {
+    uint32_t xs[32];
+    act_load_natural(xs, xrow, seg, G, valid, xrow);
     act_from_natural(A, xs);
 }
 

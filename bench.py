@@ -253,7 +253,7 @@ def bench_prefill(dev, torch, M=512, K=6144, N=16384, reps=3):
     return dict(M=M, K=K, N=N, ms=ms, tflops=fl / (ms * 1e-3) / 1e12, flop=fl)
 
 
-def cpu_baseline(budget_s=8.0):
+def cpu_baseline(budget_s=12.0):
     """Time the repo's CPU restatement of the reference's path on this host (1 core)."""
     import numpy as np
 
@@ -297,10 +297,96 @@ def cpu_baseline(budget_s=8.0):
     )
 
 
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_gemv_q4k_6144.json")
+HEADLINE_KERNEL = "k_rows"
+COPY_BYTES = 256 << 20
+
+
+def bench_copy(torch, reps=20):
+    """Calibration for the HBM byte counters: a plain device copy of COPY_BYTES (torch routes a
+    same-dtype contiguous copy to the runtime's copy kernel, which reads COPY_BYTES and writes
+    COPY_BYTES per dispatch)."""
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return dict(bytes_read=COPY_BYTES, bytes_written=COPY_BYTES, reps=reps)
+
+
+def _pmc_rows(d):
+    import csv
+    import glob
+    rows = []
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    return rows
+
+
+def summarize_traffic(fetch_dir, write_dir, out=TRAFFIC_JSON):
+    """HBM bytes per launch of the headline kernel from two rocprofv3 --pmc runs (FETCH_SIZE,
+    then WRITE_SIZE; each over `bench.py --only gemv` followed by `--only copy`), with each
+    counter scaled by what it reads for the copy kernel of known size."""
+    import statistics
+
+    def per(rows, counter, pred):
+        v = [float(r["Counter_Value"]) for r in rows if r["Counter_Name"] == counter and pred(r["Kernel_Name"])]
+        return statistics.median(v) if v else None
+
+    res = {}
+    for counter, d, key in (("FETCH_SIZE", fetch_dir, "bytes_read"), ("WRITE_SIZE", write_dir, "bytes_written")):
+        rows = _pmc_rows(d)
+        k = per(rows, counter, lambda n: HEADLINE_KERNEL in n)
+        c = per(rows, counter, lambda n: "copyBuffer" in n)
+        if k is None or c is None:
+            raise SystemExit(f"{counter}: no samples for the headline kernel or the copy kernel in {d}")
+        scale = COPY_BYTES / (c * 1024.0)     # bytes per counted KiB, from the copy of known size
+        res[counter] = dict(kib_per_dispatch=k, copy_kib_per_dispatch=c, scale_bytes_per_kib=scale,
+                            bytes_per_launch=k * 1024.0 * scale)
+    tot = res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"]
+    summary = dict(kernel=HEADLINE_KERNEL, workload="Q4_K GEMV M=1 K=N=6144, cold (rotated weights)",
+                   bytes_per_launch=tot, algorithmic_bytes=q4k_bytes(6144, 6144) + 4 * 6144,
+                   counters=res, note="median over the dispatches of one run; calibration kernel = the runtime's "
+                                      f"device copy (__amd_rocclr_copyBuffer) of {COPY_BYTES} bytes")
+    with open(out, "w") as f:
+        json.dump(summary, f, indent=1)
+    print(json.dumps(summary))
+    return summary
+
+
+def _short_kernel(name):
+    """`void aipu::(anonymous namespace)::k_rows<3, ...>(...)` -> `k_rows<3, ...>`."""
+    n = name.split("(")[0] if not name.startswith("void ") else name[5:]
+    n = n.replace("aipu::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+    depth, out = 0, ""
+    for ch in n:
+        if ch == "(" and depth == 0:
+            break
+        depth += ch == "<"
+        depth -= ch == ">"
+        out += ch
+    return out[:110]
+
+
+def trace_summary(d, command):
+    """Markdown summary of a `rocprofv3 --kernel-trace --stats --output-format csv` directory."""
+    import csv
+    import glob
+    f = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)
+    if not f:
+        raise SystemExit(f"no kernel_stats.csv under {d}")
+    rows = list(csv.DictReader(open(f[0])))
+    lines = [f"Command: `{command}`", "", "| kernel | calls | avg ns | min ns | max ns | % time |", "|---|---|---|---|---|---|"]
+    for r in rows[:12]:
+        lines.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']):.0f} | {r['MinNs']} | "
+                     f"{r['MaxNs']} | {float(r['Percentage']):.1f} |")
+    print("\n".join(lines))
+
+
 def load_traffic():
-    p = os.path.join(ROOT, "profiles", "traffic_gemv_q4k_6144.json")
-    if os.path.exists(p):
-        with open(p) as f:
+    if os.path.exists(TRAFFIC_JSON):
+        with open(TRAFFIC_JSON) as f:
             return json.load(f)
     return None
 
@@ -315,9 +401,20 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of one HIP graph")
-    ap.add_argument("--only", choices=["gemv", "moe", "stream"], default=None,
-                    help="run one measurement only (for kernel tracing)")
+    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy"], default=None,
+                    help="run one measurement only (for kernel tracing / counter runs)")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
+                    help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into "
+                         "profiles/traffic_gemv_q4k_6144.json and exit (no GPU needed)")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_DIR", "COMMAND"), default=None,
+                    help="print a markdown table of a rocprofv3 --stats csv directory and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(*args.trace_summary)
+        return
+    if args.traffic:
+        summarize_traffic(*args.traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU sharding is a design "
               f"note in DESIGN.md, not a measured configuration.", file=sys.stderr)
@@ -332,6 +429,9 @@ def main():
     torch.cuda.init()
     rot = 0.3e9 if args.quick else 1.05e9
 
+    if args.only == "copy":
+        print(json.dumps(bench_copy(torch)))
+        return
     if args.only == "moe":
         print(json.dumps(bench_moe(dev, torch, args.moe_steps)))
         return
