@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "libaipu_q4k.so")
 OBJDIR = os.path.join(ROOT, "_build", "obj")
 ARCH = "gfx950"
 
-SOURCES = ["abi.hip", "elementwise.hip", "router.hip", "gemv_ref.hip", "gemv_fast.hip", "moe.hip", "tiles.hip",
+SOURCES = ["abi.hip", "elementwise.hip", "router.hip", "gemv_ref.hip", "gemv_fast.hip", "moe.hip", "tiles.hip", "gemv_mfma.hip",
            "prefill.hip"]
 
 HIPCC_FLAGS = [

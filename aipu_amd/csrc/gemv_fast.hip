@@ -709,7 +709,9 @@ hipError_t gemv_stream_mc(const uint8_t* W, int64_t N, int64_t K, const uint16_t
 hipError_t launch_gemv_fast(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
                             float* y_f32, hipStream_t st) {
     switch (type) {
-        case T_Q4_K: return gemv_stream_mc<T_Q4_K, 4>((const uint8_t*)w, N, K, x, M, y, y_f32, st);
+        case T_Q4_K:
+            if (gemv_mfma_supported(N, K, M)) return launch_gemv_mfma(w, N, K, x, M, y, y_f32, N, st);
+            return gemv_stream_mc<T_Q4_K, 4>((const uint8_t*)w, N, K, x, M, y, y_f32, st);
         case T_BF16: return gemv_stream_mc<T_BF16, 2>((const uint8_t*)w, N, K, x, M, y, y_f32, st);
         default: return hipErrorInvalidValue;
     }

@@ -1,0 +1,1064 @@
+// Matrix-core Q4_K GEMV kernels (tolerance mode): the plain GEMV for M = 1..8 activation
+// rows, and the MoE expert legs (gate/up with the fused h = bf16(silu(g) * u) epilogue, and
+// down with the slot-ordered combine).  The per-tile arithmetic is in mfma_gemv.hpp.
+//
+// Workgroup.  A workgroup owns T tiles of 16 rows (T = 1 plain, 2 gate/up, nslots down) and
+// splits each tile's K into KP equal parts of bpk blocks; wave w computes part w % KP of
+// tile w / KP, so W = T * KP waves.  The activations are staged once per workgroup in LDS
+// in the MFMA operand order.  Per-wave partial sums are reduced across the wave's four
+// K-groups with two cross-lane adds, then across the KP parts in fixed order through LDS,
+// so every result is deterministic.
+//
+// Memory order.  Every thread issues its activation loads first, then the wave's first PD
+// blocks of weights (buffer loads, streaming cache policy), and only then waits for the
+// activations: vector loads return in order, so the staging never waits for the weight
+// stream.  The block loop is software pipelined PD deep; loads that fall past the wave's
+// blocks or past the tile's valid rows use an out-of-range buffer offset, which reads zero
+// without a memory access, so every load is unconditional and the waits are static.
+#include "common.hpp"
+#include "glm_act.hpp"
+#include "launch.hpp"
+#include "mfma_gemv.hpp"
+
+namespace aipu {
+
+using namespace mg;
+
+namespace {
+
+constexpr int kXL = 8;          // activation pieces (16 B) staged per thread, at most
+constexpr int kMaxW = 8;        // waves per workgroup
+constexpr int64_t kMaxLds = 64 * 1024;
+
+struct TileRef {
+    const uint8_t* base;   // row 0 of the tile
+    int nvalid;            // rows of the tile that exist (the rest read as zero)
+    int act;               // which staged activation the tile multiplies
+};
+
+// ------------------------------------------------------------------ problems
+// Plain GEMV: tile = 16 consecutive rows of W, activation rows x[M][K].
+template <int MR>
+struct ProbPlain {
+    const uint8_t* W;
+    int64_t N, rb;
+    uint16_t* Y;
+    float* Yf;
+    int64_t ystride;   // N of the full output (tiles of a mixed call write a column slice)
+    int M;
+    __device__ TileRef tile(int wg, int) const {
+        const int64_t r0 = (int64_t)wg * kTR;
+        const int64_t nv = N - r0;
+        return TileRef{W + r0 * rb, (int)(nv < kTR ? nv : kTR), 0};
+    }
+    __device__ void finish(int wg, const float* red, int KP, int tid) const {
+        if (tid >= kTR * MR) return;
+        const int n = tid / MR, r = tid % MR;
+        const int64_t row = (int64_t)wg * kTR + n;
+        if (r >= M || row >= N) return;
+        float v = 0.f;
+        for (int k = 0; k < KP; ++k) v += red[(k * kTR + n) * MR + r];
+        Y[r * ystride + row] = (uint16_t)bf16_rne(v);
+        if (Yf) Yf[r * ystride + row] = v;
+    }
+};
+
+__device__ __forceinline__ int routed_expert(const int32_t* sel, int s, int E) {
+    const int e = sel[s];
+    return e < 0 ? 0 : (e >= E ? E - 1 : e);
+}
+
+// MoE gate/up: workgroup (slot, 16-row tile of I); tile 0 = gate rows, tile 1 = up rows of
+// the slot's expert (slot topk = the shared expert).  h[slot][i] = bf16(silu(g) * u).
+struct ProbGateUp {
+    const uint8_t *G, *U, *shG, *shU;
+    const int32_t* sel;
+    int topk, E, itiles;
+    int64_t rb, ebytes;
+    uint16_t* h;
+    int64_t I;
+    __device__ TileRef tile(int wg, int t) const {
+        const int s = wg / itiles, it = wg - s * itiles;
+        const uint8_t* base;
+        if (s < topk) base = (t ? U : G) + (int64_t)routed_expert(sel, s, E) * ebytes;
+        else base = t ? shU : shG;
+        return TileRef{base + (int64_t)it * kTR * rb, kTR, 0};
+    }
+    __device__ void finish(int wg, const float* red, int KP, int tid) const {
+        if (tid >= kTR) return;
+        const int s = wg / itiles, it = wg - s * itiles;
+        float g = 0.f, u = 0.f;
+        for (int k = 0; k < KP; ++k) {
+            g += red[k * kTR + tid];
+            u += red[(KP + k) * kTR + tid];
+        }
+        const uint32_t gb = bf16_rne(g), ub = bf16_rne(u);
+        h[(int64_t)s * I + (int64_t)it * kTR + tid] =
+            (uint16_t)bf16_rne(bf16_to_f32(glm_silu_bf16(gb)) * bf16_to_f32(ub));
+    }
+};
+
+// MoE down: workgroup = 16-row tile of H; tile s = slot s (its expert's rows, against
+// h[s]).  The slots are combined in slot order
+//     facc = f32(facc + f32(w_s * bf16(y_s)))   (tools/glm_model_q4k_ref.py:799-809)
+// with w = 1 for the shared slot; passthrough (one expert, no routing) writes bf16(y_0).
+struct ProbDown {
+    const uint8_t *D, *shD;
+    const int32_t* sel;
+    const uint16_t* selw;
+    int topk, nslots, E, passthrough;
+    int64_t H, rb, ebytes;
+    uint16_t* Y;
+    __device__ TileRef tile(int wg, int t) const {
+        const int64_t d0 = (int64_t)wg * kTR;
+        const uint8_t* base = t < topk ? D + (int64_t)routed_expert(sel, t, E) * ebytes : shD;
+        const int64_t nv = H - d0;
+        return TileRef{base + d0 * rb, (int)(nv < kTR ? nv : kTR), t};
+    }
+    __device__ void finish(int wg, const float* red, int KP, int tid) const {
+        if (tid >= kTR) return;
+        const int64_t d = (int64_t)wg * kTR + tid;
+        if (d >= H) return;
+        float facc = 0.f;
+        for (int s = 0; s < nslots; ++s) {
+            float ys = 0.f;
+            for (int k = 0; k < KP; ++k) ys += red[(s * KP + k) * kTR + tid];
+            if (passthrough) {
+                Y[d] = (uint16_t)bf16_rne(ys);
+                return;
+            }
+            const float yb = bf16_to_f32(bf16_rne(ys));
+            const float p = s < topk ? bf16_to_f32(selw[s]) * yb : yb;
+            facc = facc + p;
+        }
+        Y[d] = (uint16_t)bf16_rne(facc);
+    }
+};
+
+// ------------------------------------------------------------------ kernel
+struct Plan {
+    int KP, bpk, PD, W, nact;
+    int64_t lds;
+};
+
+template <int MR>
+__device__ __forceinline__ void lds_sums(const uint8_t* smem, uint32_t off, float (&lo)[MR], float (&hi)[MR]) {
+    if constexpr (MR == 1) {
+        const float2 v = *(const float2*)(smem + off);
+        lo[0] = v.x;
+        hi[0] = v.y;
+    } else if constexpr (MR == 2) {
+        const float4 v = *(const float4*)(smem + off);
+        lo[0] = v.x;
+        lo[1] = v.y;
+        hi[0] = v.z;
+        hi[1] = v.w;
+    } else {
+        const float4 a = *(const float4*)(smem + off);
+        const float4 b = *(const float4*)(smem + off + 16);
+        lo[0] = a.x;
+        lo[1] = a.y;
+        lo[2] = a.z;
+        lo[3] = a.w;
+        hi[0] = b.x;
+        hi[1] = b.y;
+        hi[2] = b.z;
+        hi[3] = b.w;
+    }
+}
+
+__device__ __forceinline__ u32x4_t lds128(const uint8_t* smem, uint32_t off) {
+    const uint4 v = *(const uint4*)(smem + off);
+    return u32x4_t{v.x, v.y, v.z, v.w};
+}
+
+template <int MR, int PD, class Prob>
+__global__ __launch_bounds__(kMaxW * 64) void k_mfma_gemv(Prob pb, const uint16_t* __restrict__ X, int64_t xstride,
+                                                          uint32_t xbytes, int K, int M, int nact, int KP, int bpk) {
+    static_assert(MR == 1 || MR == 2 || MR == 4, "MR must be 1, 2 or 4");
+    using L = ActLayout<MR>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nthr = blockDim.x;
+    const int nsb = K / QK_K;
+    const int wg = blockIdx.x;
+    const uint32_t abytes = (uint32_t)nsb * L::kEntriesPerBlock * 16;   // A entries of one activation
+    const uint32_t aoff0 = L::kZeroBytes;
+    const uint32_t soff0 = aoff0 + (uint32_t)nact * abytes;
+    const uint32_t sbytes = (uint32_t)nsb * L::kSumsPerBlock * 4;
+    float* red = (float*)(smem + soff0 + (uint32_t)nact * sbytes);
+
+    // ---- 1. activation loads: piece q = (act*MR + m) * ppr + p, 8 bf16 at position 8p
+    const int ppr = nsb * 32;
+    const int total = nact * MR * ppr;
+    const float inv_ppr = 1.0f / (float)ppr;
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, xbytes);
+    uint4 xv[kXL];
+#pragma unroll
+    for (int i = 0; i < kXL; ++i) {
+        const int q = tid + i * nthr;
+        const int rowid = (int)(((float)q + 0.5f) * inv_ppr);
+        const int p = q - rowid * ppr;
+        const int a = rowid / MR, m = rowid - a * MR;
+        const bool valid = q < total && m < M;
+        const uint32_t off = valid ? 2u * (uint32_t)((int64_t)a * xstride + (int64_t)m * K + 8 * p) : kOOB;
+        xv[i] = buf_load16(xr, off);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. the wave's tile and its first PD blocks of weights
+    const int tt = w / KP, kp = w - tt * KP;
+    const TileRef tr = pb.tile(wg, tt);
+    const int64_t rb = (int64_t)nsb * 144;
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
+    const int n = lane & 15, g = lane >> 4;
+    const uint32_t row_off = (uint32_t)(n * rb);   // rows >= nvalid land out of range -> zeros
+    const int kb0 = kp * bpk;
+    Raw buf[PD];
+#pragma unroll
+    for (int j = 0; j < PD; ++j) buf[j] = raw_load(wr, row_off + (uint32_t)(kb0 + j) * 144u, g);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 3. stage: zero region, permuted activations, sub-block sums
+    for (int i = tid; i < L::kZeroBytes / 16; i += nthr) ((uint4*)smem)[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kXL; ++i) {
+        const int q = tid + i * nthr;
+        const int rowid = (int)(((float)q + 0.5f) * inv_ppr);
+        const int p = q - rowid * ppr;
+        const int a = rowid / MR, m = rowid - a * MR;
+        // sum of the piece's 8 activations, then of the 4 pieces of its sub-block (a quad)
+        const uint32_t ones = 0x3F803F80u;
+        float s = 0.f;
+        s = dot2(xv[i].x, ones, s);
+        s = dot2(xv[i].y, ones, s);
+        s = dot2(xv[i].z, ones, s);
+        s = dot2(xv[i].w, ones, s);
+        s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));
+        s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));
+        if (q < total) {
+            const int b = p >> 5, gg = (p >> 3) & 3, t = p & 7;
+            const uint32_t e = (uint32_t)((b * 8 + t) * 4 + gg) * MR + m;
+            *(u32x4_t*)(smem + aoff0 + (uint32_t)a * abytes + 16u * e) = act_perm(xv[i]);
+            if ((p & 3) == 0) {
+                const int h = (p >> 2) & 1;
+                ((float*)(smem + soff0 + (uint32_t)a * sbytes))[((b * 4 + gg) * 2 + h) * MR + m] = s;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 4. block loop
+    const int mm = n - 4 * g;
+    const bool diag = mm >= 0 && mm < MR;
+    const uint32_t alane = diag ? aoff0 + (uint32_t)tr.act * abytes + 16u * (uint32_t)(g * MR + mm) : 0u;
+    const uint32_t ablk = diag ? (uint32_t)L::kEntriesPerBlock * 16u : 0u;
+    const uint32_t slane = soff0 + (uint32_t)tr.act * sbytes + 4u * (uint32_t)(g * 2 * MR);
+    const HdrSel hs = hdr_sel(g);
+    const CodeK ck = code_k();
+    float acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+    // Accumulator rows r >= MR multiply all-zero activation rows and stay 0; only rows < MR
+    // are re-seeded per block.
+    f32x4_t dlo = {0.f, 0.f, 0.f, 0.f}, dhi = {0.f, 0.f, 0.f, 0.f};
+
+    for (int s0 = 0; s0 < bpk; s0 += PD) {
+#pragma unroll
+        for (int j = 0; j < PD; ++j) {
+            const int b = kb0 + s0 + j;
+            const Raw& R = buf[j];
+            const uint32_t ab = alane + ablk * (uint32_t)b;
+            u32x4_t A[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) A[t] = lds128(smem, ab + 16u * (uint32_t)(t * 4 * MR));
+            float alo[MR], ahi[MR];
+            lds_sums<MR>(smem, slane + 4u * (uint32_t)(b * 8 * MR), alo, ahi);
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                dlo[r] = -kCodeBiasF * alo[r];
+                dhi[r] = -kCodeBiasF * ahi[r];
+            }
+            const uint32_t qd[8] = {R.q0.x, R.q0.y, R.q0.z, R.q0.w, R.q1.x, R.q1.y, R.q1.z, R.q1.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                dlo = mfma(A[t], codes_lo(qd[2 * t], qd[2 * t + 1], ck), dlo);
+                dhi = mfma(A[4 + t], codes_hi(qd[2 * t], qd[2 * t + 1], ck), dhi);
+            }
+            const Hdr H = hdr_decode(R.h, hs);
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                const float t1 = __builtin_fmaf(H.sc1, dhi[r], H.sc0 * dlo[r]);
+                const float v = __builtin_fmaf(H.m1, ahi[r], H.m0 * alo[r]);
+                acc[r] = __builtin_fmaf(H.d, t1, acc[r]);
+                acc[r] = __builtin_fmaf(-H.dm, v, acc[r]);
+            }
+            // refill this slot right away (the loads must not sink to the end of the group)
+            const int sn = s0 + j + PD;
+            buf[j] = raw_load(wr, sn < bpk ? row_off + (uint32_t)(kb0 + sn) * 144u : kOOB, g);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // ---- 5. reduce over the four K-groups (lanes n, n+16, n+32, n+48), then across parts
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        acc[r] += __shfl_xor(acc[r], 16, 64);
+        acc[r] += __shfl_xor(acc[r], 32, 64);
+    }
+    if (lane < kTR) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r) red[(w * kTR + lane) * MR + r] = acc[r];
+    }
+    __syncthreads();
+    pb.finish(wg, red, KP, tid);
+}
+
+// LDS reads of one block step.  Written as asm because the direct-to-LDS loads of the other
+// ring slots are still in flight and the compiler cannot prove that these reads do not
+// alias them (it would wait for every outstanding load); the ordering is established by
+// the explicit vmcnt wait and the barrier before them.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+struct StepIn {
+    u32x4_t h, q0, q1;
+    f32x2_t as;
+};
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Header, qs chunk and sub-block sums of one lane (all lanes).
+__device__ __forceinline__ void step_reads(uint32_t ah, uint32_t aq0, uint32_t aq1, uint32_t asum, StepIn& o) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %5\n\t"
+        "ds_read_b128 %2, %6\n\t"
+        "ds_read_b64 %3, %7"
+        : "=&v"(o.h), "=&v"(o.q0), "=&v"(o.q1), "=&v"(o.as)
+        : "v"(ah), "v"(aq0), "v"(aq1), "v"(asum));
+}
+
+// The 8 activation operands of a block, read on the lanes in `mask` only (the diagonal
+// lanes of the block-diagonal A); every other lane keeps its register contents, which stay
+// zero for the whole kernel.  This moves 64 B per read instead of a 1 KB broadcast of zeros.
+__device__ __forceinline__ void a_reads(u32x4_t (&A)[8], uint32_t aa, uint64_t mask) {
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %8, exec\n\t"
+        "s_and_b64 exec, exec, %10\n\t"
+        "ds_read_b128 %0, %9\n\t"
+        "ds_read_b128 %1, %9 offset:64\n\t"
+        "ds_read_b128 %2, %9 offset:128\n\t"
+        "ds_read_b128 %3, %9 offset:192\n\t"
+        "ds_read_b128 %4, %9 offset:256\n\t"
+        "ds_read_b128 %5, %9 offset:320\n\t"
+        "ds_read_b128 %6, %9 offset:384\n\t"
+        "ds_read_b128 %7, %9 offset:448\n\t"
+        "s_mov_b64 exec, %8"
+        : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]),
+          "=&s"(saved)
+        : "v"(aa), "s"(mask));
+}
+
+// Wait for the LDS reads above; the operands are tied so that no use moves above the wait.
+__device__ __forceinline__ void lds_wait(StepIn& a, StepIn& b, u32x4_t (&A)[8], u32x4_t (&B)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a.h), "+v"(a.q0), "+v"(a.q1), "+v"(a.as), "+v"(b.h), "+v"(b.q0), "+v"(b.q1), "+v"(b.as),
+                   "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]),
+                   "+v"(B[0]), "+v"(B[1]), "+v"(B[2]), "+v"(B[3]), "+v"(B[4]), "+v"(B[5]), "+v"(B[6]), "+v"(B[7]));
+}
+
+__device__ __forceinline__ void a_wait(u32x4_t (&A)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]));
+}
+
+// Diagonal lanes of the block-diagonal activation operand: lane 16g + 4g + m for m < MR.
+__host__ __device__ constexpr uint64_t diag_mask(int mr) {
+    uint64_t m = 0;
+    for (int g = 0; g < 4; ++g)
+        for (int r = 0; r < mr; ++r) m |= 1ull << (20 * g + r);
+    return m;
+}
+
+// ------------------------------------------------------- single-row kernel (M = 1)
+// Each wave is self-contained: it stages the activations of its own BPK = GS * NG blocks
+// and streams its 16 rows of weights group by group (GS blocks per group) into its own LDS
+// slice with direct-to-LDS buffer loads, 16 contiguous bytes per lane, so every load
+// instruction covers ~1 KB of consecutive row bytes and no byte is fetched twice.  A group
+// is copied from LDS into registers before the next group's loads are issued into the same
+// slice, so the next group's memory latency overlaps this group's arithmetic.  No barrier
+// precedes the block loop; the one barrier is the final reduction across the K parts.
+template <int GS>
+struct Dma {
+    static constexpr int kPieces = 16 * 9 * GS;            // 16-B pieces of 16 rows x GS blocks
+    static constexpr int kInsts = (kPieces + 63) / 64;     // 64 lanes x 16 B per instruction
+    static constexpr int kBytes = kInsts * 1024;           // LDS slice (the tail lanes write zeros)
+};
+
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, kNT);
+}
+
+// s_waitcnt immediates (gfx9 layout: vmcnt[3:0] expcnt[6:4] lgkmcnt[11:8] vmcnt_hi[15:14])
+constexpr int kWaitVm0 = 0x0F70;    // vmcnt(0)
+constexpr int kWaitLgkm0 = 0xC07F;  // lgkmcnt(0)
+
+template <int GS>
+__device__ __forceinline__ void dma_group(__amdgpu_buffer_rsrc_t wr, uint8_t* slice, int64_t rb, int blk0, int lane) {
+#pragma unroll
+    for (int i = 0; i < Dma<GS>::kInsts; ++i) {
+        const int j = 64 * i + lane;
+        const int row = j / (9 * GS), within = j - row * (9 * GS);
+        const uint32_t off = j < Dma<GS>::kPieces ? (uint32_t)(row * rb + (int64_t)blk0 * 144 + 16 * within) : kOOB;
+        lds_dma16(wr, slice + 1024 * i, off);
+    }
+}
+
+template <int GS, int XI, class Prob>
+__global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb, const uint16_t* __restrict__ X, int64_t xstride,
+                                                      uint32_t xbytes, int K, int KP, int NG) {
+    // Separate LDS objects for the direct-to-LDS weight slices (dynamic) and for everything
+    // the waves write themselves (static), so the compiler can see that the staging writes
+    // do not alias weight loads still in flight and does not make them wait for those.
+    constexpr int kBpkMax = 2 * XI;             // activation pieces per wave <= 64 * XI
+    constexpr uint32_t kActWave = kBpkMax * 544;
+    __shared__ __align__(16) uint8_t s_act[kMaxW * kActWave];
+    __shared__ float red[kMaxW * kTR];
+    extern __shared__ __align__(16) uint8_t s_w[];
+    const int BPK = GS * NG;
+    const int XP = BPK * 32;
+    const uint32_t kA = (uint32_t)BPK * 512;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nsb = K / QK_K;
+    const int wg = blockIdx.x;
+    uint8_t* wA = s_act + (uint32_t)w * kActWave;
+    float* wS = (float*)(wA + kA);
+    uint8_t* wW = s_w + (uint32_t)w * Dma<GS>::kBytes;
+
+    const int tt = w / KP, kp = w - tt * KP;
+    const TileRef tr = pb.tile(wg, tt);
+    const int kb0 = kp * BPK;
+    const int64_t rb = (int64_t)nsb * 144;
+
+    // 1. this wave's activations, then 2. its first group of weights
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, xbytes);
+    const uint32_t xbase = 2u * (uint32_t)((int64_t)tr.act * xstride + (int64_t)kb0 * QK_K);
+    uint4 xv[XI];
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const int q = lane + 64 * i;
+        xv[i] = buf_load16(xr, q < XP ? xbase + 16u * q : kOOB);
+    }
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
+    dma_group<GS>(wr, wW, rb, kb0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. stage: A entries, sums
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const int q = lane + 64 * i;
+        const uint32_t ones = 0x3F803F80u;
+        float sm = 0.f;
+        sm = dot2(xv[i].x, ones, sm);
+        sm = dot2(xv[i].y, ones, sm);
+        sm = dot2(xv[i].z, ones, sm);
+        sm = dot2(xv[i].w, ones, sm);
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+        if (q < XP) {
+            const int bb = q >> 5, gg = (q >> 3) & 3, t = q & 7;
+            *(u32x4_t*)(wA + 16u * (uint32_t)((bb * 8 + t) * 4 + gg)) = act_perm(xv[i]);
+            if ((q & 3) == 0) wS[(bb * 4 + gg) * 2 + ((q >> 2) & 1)] = sm;
+        }
+    }
+
+    // 4. block loop
+    const int n = lane & 15, g = lane >> 4;
+    u32x4_t A[8];   // block-diagonal activation operands: off-diagonal lanes stay zero
+#pragma unroll
+    for (int t = 0; t < 8; ++t) A[t] = u32x4_t{0u, 0u, 0u, 0u};
+    const HdrSel hs = hdr_sel(g);
+    const CodeK ck = code_k();
+    const uint32_t rrow = (uint32_t)n * (144u * GS);
+    float acc = 0.f;
+    f32x4_t dlo = {0.f, 0.f, 0.f, 0.f}, dhi = {0.f, 0.f, 0.f, 0.f};
+    for (int gi = 0; gi < NG; ++gi) {
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);    // this group's weights are in LDS
+        Raw R[GS];
+#pragma unroll
+        for (int bb = 0; bb < GS; ++bb) {
+            const uint8_t* p = wW + rrow + 144u * bb;
+            R[bb].h = *(const uint4*)p;
+            R[bb].q0 = *(const uint4*)(p + 16 + 32 * g);
+            R[bb].q1 = *(const uint4*)(p + 32 + 32 * g);
+        }
+        if (gi + 1 < NG) {
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // the slice has been read: refill it
+            dma_group<GS>(wr, wW, rb, kb0 + (gi + 1) * GS, lane);
+        }
+#pragma unroll
+        for (int bb = 0; bb < GS; ++bb) {
+            const int b = gi * GS + bb;   // block index within this wave's part
+            a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
+            a_wait(A);
+            const float2 as = *(const float2*)(wS + (b * 4 + g) * 2);
+            dlo[0] = -kCodeBiasF * as.x;
+            dhi[0] = -kCodeBiasF * as.y;
+            const uint32_t qd[8] = {R[bb].q0.x, R[bb].q0.y, R[bb].q0.z, R[bb].q0.w,
+                                    R[bb].q1.x, R[bb].q1.y, R[bb].q1.z, R[bb].q1.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                dlo = mfma(A[t], codes_lo(qd[2 * t], qd[2 * t + 1], ck), dlo);
+                dhi = mfma(A[4 + t], codes_hi(qd[2 * t], qd[2 * t + 1], ck), dhi);
+            }
+            const Hdr H = hdr_decode(R[bb].h, hs);
+            const float t1 = __builtin_fmaf(H.sc1, dhi[0], H.sc0 * dlo[0]);
+            const float v = __builtin_fmaf(H.m1, as.y, H.m0 * as.x);
+            acc = __builtin_fmaf(H.d, t1, acc);
+            acc = __builtin_fmaf(-H.dm, v, acc);
+        }
+    }
+
+    // 5. reduce over the four K-groups, then across the K parts
+    acc += __shfl_xor(acc, 16, 64);
+    acc += __shfl_xor(acc, 32, 64);
+    if (lane < kTR) red[w * kTR + lane] = acc;
+    __syncthreads();
+    pb.finish(wg, red, KP, tid);
+}
+
+// ------------------------------------------------------------ phased kernel (M = 1)
+// A workgroup of 4 waves streams a sequence of phases.  A phase is 16 rows x 8 Q4_K blocks
+// of one tile (16 runs of 1152 contiguous row bytes = 9 whole cache lines each) against one
+// activation; wave w computes blocks w and w + 4 of the phase as soon as the phase has
+// landed, so the arithmetic follows the memory stream and the tail after the last byte is
+// two blocks per wave.  Phases go through a ring of three LDS slots (weights by
+// direct-to-LDS loads, activations staged by the threads in the MFMA operand order).
+//
+// Slot layout: 16-B piece c (0..71) of tile row n sits at slot 72n + (c ^ ((n >> 1) & 7)),
+// which puts the 16 rows' copies of any piece in 16 different bank quads (conflict-free
+// 16-lane reads) while every load instruction still covers one contiguous run of slots.
+constexpr int kPhB = 8;                      // blocks per phase
+constexpr int kPhWaves = 4;                  // waves per workgroup
+constexpr int kPhBpw = kPhB / kPhWaves;      // blocks per wave per phase
+constexpr int kPhaseW = 16 * 72 * 16;        // weight bytes of a phase slot (18 KB)
+constexpr int kPhaseInst = 16 * 72 / 64;     // 18 load instructions per phase
+constexpr int kPhIpw = (kPhaseInst + kPhWaves - 1) / kPhWaves;   // 5 per wave (2 spare in all)
+constexpr int kRing = 3;
+constexpr int kMaxTiles = 8;
+
+struct PhaseRef {
+    const uint8_t* lo;   // tile rows 0..7 start here (row stride rb)
+    const uint8_t* hi;   // tile rows 8..15
+    int nlo, nhi;        // valid rows in each half
+    int blk0, nb;        // first block of the phase and its block count (<= kPhB)
+    int act;             // activation index
+    int tile;            // which accumulator (tile) the phase feeds
+    bool last;           // last phase of its tile
+};
+
+// Plain GEMV as phases: one tile of 16 rows, phase p = blocks [8p, 8p + 8).
+struct PhPlain {
+    const uint8_t* W;
+    int64_t N, rb;
+    int nsb;
+    uint16_t* Y;
+    float* Yf;
+    int64_t ystride;
+    __device__ void setup(int) {}
+    __device__ int nphase() const { return (nsb + kPhB - 1) / kPhB; }
+    __device__ PhaseRef phase(int wg, int p) const {
+        const int64_t r0 = (int64_t)wg * kTR;
+        const int64_t nv = N - r0;
+        const int nvalid = (int)(nv < kTR ? nv : kTR);
+        PhaseRef f;
+        f.lo = W + r0 * rb;
+        f.hi = f.lo + 8 * rb;
+        f.nlo = nvalid < 8 ? nvalid : 8;
+        f.nhi = nvalid > 8 ? nvalid - 8 : 0;
+        f.blk0 = p * kPhB;
+        f.nb = nsb - f.blk0 < kPhB ? nsb - f.blk0 : kPhB;
+        f.act = 0;
+        f.tile = 0;
+        f.last = p == nphase() - 1;
+        return f;
+    }
+    __device__ void finish(int wg, const float* red, int tid) const {   // red[tile][wave][16]
+        if (tid >= kTR) return;
+        const int64_t row = (int64_t)wg * kTR + tid;
+        if (row >= N) return;
+        float v = 0.f;
+        for (int k = 0; k < kPhWaves; ++k) v += red[k * kTR + tid];
+        Y[row] = (uint16_t)bf16_rne(v);
+        if (Yf) Yf[row] = v;
+    }
+};
+
+// MoE gate/up as phases: the 16 tile rows are gate rows i0..i0+7 (0..7) and up rows
+// i0..i0+7 (8..15) of the slot's expert; h[slot][i0 + n] = bf16(silu(g_n) * u_n).
+struct PhGateUp {
+    const uint8_t *G, *U, *shG, *shU;
+    const int32_t* sel;
+    int topk, E, itiles, nsb;
+    int64_t rb, ebytes, I;
+    uint16_t* h;
+    int eid;   // expert of this workgroup's slot (set up once per workgroup)
+    __device__ void setup(int wg) {
+        const int s = wg / itiles;
+        eid = s < topk ? __builtin_amdgcn_readfirstlane(routed_expert(sel, s, E)) : 0;
+    }
+    __device__ int nphase() const { return (nsb + kPhB - 1) / kPhB; }
+    __device__ PhaseRef phase(int wg, int p) const {
+        const int s = wg / itiles, it = wg - s * itiles;
+        const uint8_t *g, *u;
+        if (s < topk) {
+            const int64_t eo = (int64_t)eid * ebytes;
+            g = G + eo;
+            u = U + eo;
+        } else {
+            g = shG;
+            u = shU;
+        }
+        PhaseRef f;
+        f.lo = g + (int64_t)it * 8 * rb;
+        f.hi = u + (int64_t)it * 8 * rb;
+        f.nlo = 8;
+        f.nhi = 8;
+        f.blk0 = p * kPhB;
+        f.nb = nsb - f.blk0 < kPhB ? nsb - f.blk0 : kPhB;
+        f.act = 0;
+        f.tile = 0;
+        f.last = p == nphase() - 1;
+        return f;
+    }
+    __device__ void finish(int wg, const float* red, int tid) const {
+        if (tid >= 8) return;
+        const int s = wg / itiles, it = wg - s * itiles;
+        float g = 0.f, u = 0.f;
+        for (int k = 0; k < kPhWaves; ++k) {
+            g += red[k * kTR + tid];
+            u += red[k * kTR + 8 + tid];
+        }
+        const uint32_t gb = bf16_rne(g), ub = bf16_rne(u);
+        h[(int64_t)s * I + (int64_t)it * 8 + tid] = (uint16_t)bf16_rne(bf16_to_f32(glm_silu_bf16(gb)) * bf16_to_f32(ub));
+    }
+};
+
+// MoE down as phases: tile s = slot s (16 rows of H of its expert, K = I), phases walk
+// the slots in order (and each slot's K in chunks of 8 blocks); the finish combines the
+// slots in slot order as in tools/glm_model_q4k_ref.py:799-809.
+struct PhDown {
+    const uint8_t *D, *shD;
+    const int32_t* sel;
+    const uint16_t* selw;
+    int topk, nslots, E, passthrough, nsb;
+    int64_t H, rb, ebytes;
+    uint16_t* Y;
+    int eid[kMaxTiles];   // experts of the slots (set up once per workgroup)
+    __device__ void setup(int) {
+#pragma unroll
+        for (int s = 0; s < kMaxTiles; ++s)
+            eid[s] = s < topk ? __builtin_amdgcn_readfirstlane(routed_expert(sel, s, E)) : 0;
+    }
+    __device__ int pps() const { return (nsb + kPhB - 1) / kPhB; }
+    __device__ int nphase() const { return nslots * pps(); }
+    __device__ PhaseRef phase(int wg, int p) const {
+        const int q = pps();
+        const int s = p / q, pk = p - s * q;
+        const int64_t d0 = (int64_t)wg * kTR;
+        const int64_t nv = H - d0;
+        const int nvalid = (int)(nv < kTR ? nv : kTR);
+        int e = 0;
+#pragma unroll
+        for (int k = 0; k < kMaxTiles; ++k) e = k == s ? eid[k] : e;
+        const uint8_t* base = s < topk ? D + (int64_t)e * ebytes : shD;
+        PhaseRef f;
+        f.lo = base + d0 * rb;
+        f.hi = f.lo + 8 * rb;
+        f.nlo = nvalid < 8 ? nvalid : 8;
+        f.nhi = nvalid > 8 ? nvalid - 8 : 0;
+        f.blk0 = pk * kPhB;
+        f.nb = nsb - f.blk0 < kPhB ? nsb - f.blk0 : kPhB;
+        f.act = s;
+        f.tile = s;
+        f.last = pk == q - 1;
+        return f;
+    }
+    __device__ void finish(int wg, const float* red, int tid) const {
+        if (tid >= kTR) return;
+        const int64_t d = (int64_t)wg * kTR + tid;
+        if (d >= H) return;
+        float facc = 0.f;
+        for (int s = 0; s < nslots; ++s) {
+            float ys = 0.f;
+            for (int k = 0; k < kPhWaves; ++k) ys += red[(s * kPhWaves + k) * kTR + tid];
+            if (passthrough) {
+                Y[d] = (uint16_t)bf16_rne(ys);
+                return;
+            }
+            const float yb = bf16_to_f32(bf16_rne(ys));
+            const float pr = s < topk ? bf16_to_f32(selw[s]) * yb : yb;
+            facc = facc + pr;
+        }
+        Y[d] = (uint16_t)bf16_rne(facc);
+    }
+};
+
+// Issue one phase into a ring slot: the activation piece of this thread (M = 1: 8 blocks x
+// 32 pieces = 256 pieces, one per thread), then this wave's weight-load instructions
+// (instructions w, w + 4, ... of the phase's 18; the spare ones read out of range, which
+// writes zeros into the slot's tail).  A phase past the end (nb <= 0) loads nothing but
+// still issues the same instructions, so every wave's count of outstanding loads is the
+// same at every point and all waits are static.  Offsets are computed in 32 bits and
+// selected without branches (a branch would let the compiler move loads between blocks).
+__device__ __forceinline__ uint4 phase_issue(const PhaseRef& f, __amdgpu_buffer_rsrc_t xr, int64_t xstride, int tid,
+                                             int w, int lane, int64_t rb, uint8_t* wslot) {
+    const int q = tid;
+    const uint32_t xo = 2u * ((uint32_t)(f.act * xstride) + (uint32_t)f.blk0 * QK_K + 8u * (uint32_t)q);
+    const uint4 xv = buf_load16(xr, q < 32 * f.nb ? xo : kOOB);
+    const uint32_t rb32 = (uint32_t)rb;
+    const __amdgpu_buffer_rsrc_t rlo = buf_rsrc(f.lo, (uint32_t)f.nlo * rb32);
+    const __amdgpu_buffer_rsrc_t rhi = buf_rsrc(f.hi, (uint32_t)f.nhi * rb32);
+    const uint32_t b0 = (uint32_t)f.blk0 * 144u;
+    const int climit = 9 * f.nb;
+#pragma unroll
+    for (int k = 0; k < kPhIpw; ++k) {
+        const int i = w + kPhWaves * k;
+        const int sl = 64 * i + lane;        // destination slot
+        const int n = sl / 72, cs = sl - n * 72;
+        const int c = cs ^ ((n >> 1) & 7);   // source piece of row n
+        const uint32_t o = (uint32_t)(n & 7) * rb32 + b0 + 16u * (uint32_t)c;
+        const uint32_t off = (i < kPhaseInst && c < climit) ? o : kOOB;
+        lds_dma16(i < 9 ? rlo : rhi, wslot + 1024 * (i < kPhaseInst ? i : kPhaseInst), off);
+    }
+    return xv;
+}
+
+struct PhaseCtx {
+    int tid, w, lane, n, g, sw, P, wg;
+    uint32_t rowb;
+    int64_t rb, xstride;
+    __amdgpu_buffer_rsrc_t xr;
+    HdrSel hs;
+    CodeK ck;
+};
+
+template <class Prob>
+__device__ __forceinline__ PhaseRef phase_or_empty(const Prob& pb, int wg, int p, int P) {
+    PhaseRef f = pb.phase(wg, p < P ? p : P - 1);
+    if (p >= P) f.nb = 0;
+    return f;
+}
+
+// Block (ws row base, block index b within the phase) -> this lane's partial dot product.
+__device__ __forceinline__ float block_dot(const StepIn& in, const u32x4_t (&A)[8], const PhaseCtx& c) {
+    f32x4_t dlo = {-kCodeBiasF * in.as.x, 0.f, 0.f, 0.f};
+    f32x4_t dhi = {-kCodeBiasF * in.as.y, 0.f, 0.f, 0.f};
+    const uint32_t qd[8] = {in.q0.x, in.q0.y, in.q0.z, in.q0.w, in.q1.x, in.q1.y, in.q1.z, in.q1.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        dlo = mfma(A[t], codes_lo(qd[2 * t], qd[2 * t + 1], c.ck), dlo);
+        dhi = mfma(A[4 + t], codes_hi(qd[2 * t], qd[2 * t + 1], c.ck), dhi);
+    }
+    const Hdr H = hdr_decode(make_uint4(in.h.x, in.h.y, in.h.z, in.h.w), c.hs);
+    const float t1 = __builtin_fmaf(H.sc1, dhi[0], H.sc0 * dlo[0]);
+    const float v = __builtin_fmaf(H.m1, in.as.y, H.m0 * in.as.x);
+    return __builtin_fmaf(H.d, t1, -(H.dm * v));
+}
+
+template <class Prob>
+__device__ __forceinline__ void phase_step(const Prob& pb, const PhaseCtx& c, int p, uint4& xv, uint8_t* wslot,
+                                           uint8_t* act, float* red, float& acc, u32x4_t (&A)[8], u32x4_t (&B)[8]) {
+    const PhaseRef f = phase_or_empty(pb, c.wg, p, c.P);
+    float* sums = (float*)(act + kPhB * 512);
+    {   // stage this phase's activation piece (thread tid = piece q of the phase)
+        const uint4 x = xv;
+        const uint32_t ones = 0x3F803F80u;
+        float sm = 0.f;
+        sm = dot2(x.x, ones, sm);
+        sm = dot2(x.y, ones, sm);
+        sm = dot2(x.z, ones, sm);
+        sm = dot2(x.w, ones, sm);
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+        const int q = c.tid;
+        const int bb = q >> 5, gg = (q >> 3) & 3, t = q & 7;
+        *(u32x4_t*)(act + 16u * (uint32_t)((bb * 8 + t) * 4 + gg)) = act_perm(x);
+        if ((q & 3) == 0) sums[(bb * 4 + gg) * 2 + ((q >> 2) & 1)] = sm;
+    }
+    // this wave's loads of the phase have landed: loads complete in order and exactly the
+    // next two phases' 1 + kPhIpw loads each were issued after them
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * (1 + kPhIpw)));   // vmcnt(12)
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_s_barrier();
+
+    // blocks w and w + 4 of the phase (both past the end contribute zero)
+    const int b0 = c.w, b1 = c.w + kPhWaves;
+    const uint8_t* ws = wslot + c.rowb;
+    StepIn i0, i1;
+    step_reads(lds_addr(ws + 16 * ((9 * b0) ^ c.sw)), lds_addr(ws + 16 * ((9 * b0 + 1 + 2 * c.g) ^ c.sw)),
+               lds_addr(ws + 16 * ((9 * b0 + 2 + 2 * c.g) ^ c.sw)), lds_addr(sums + (b0 * 4 + c.g) * 2), i0);
+    step_reads(lds_addr(ws + 16 * ((9 * b1) ^ c.sw)), lds_addr(ws + 16 * ((9 * b1 + 1 + 2 * c.g) ^ c.sw)),
+               lds_addr(ws + 16 * ((9 * b1 + 2 + 2 * c.g) ^ c.sw)), lds_addr(sums + (b1 * 4 + c.g) * 2), i1);
+    a_reads(A, lds_addr(act + (uint32_t)b0 * 512u + 16u * (uint32_t)c.g), diag_mask(1));
+    a_reads(B, lds_addr(act + (uint32_t)b1 * 512u + 16u * (uint32_t)c.g), diag_mask(1));
+    lds_wait(i0, i1, A, B);
+    const float v0 = block_dot(i0, A, c);
+    const float v1 = block_dot(i1, B, c);
+    acc += (b0 < f.nb ? v0 : 0.f) + (b1 < f.nb ? v1 : 0.f);
+
+    if (f.last && p < c.P) {   // flush this tile's partial sums (reduced over the four K-groups)
+        float a = acc;
+        a += __shfl_xor(a, 16, 64);
+        a += __shfl_xor(a, 32, 64);
+        if (c.lane < kTR) red[(f.tile * kPhWaves + c.w) * kTR + c.lane] = a;
+        acc = 0.f;
+    }
+    // refill this slot with phase p + kRing once every wave is done with it (always issued,
+    // empty past the last phase)
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_s_barrier();
+    xv = phase_issue(phase_or_empty(pb, c.wg, p + kRing, c.P), c.xr, c.xstride, c.tid, c.w, c.lane, c.rb, wslot);
+}
+
+template <class Prob>
+__global__ __launch_bounds__(kPhWaves * 64) void k_phase(Prob pb0, const uint16_t* __restrict__ X, int64_t xstride,
+                                                        uint32_t xbytes, int nsb) {
+    __shared__ __align__(16) uint8_t s_w0[kPhaseW + 2048];   // + tail for the spare loads
+    __shared__ __align__(16) uint8_t s_w1[kPhaseW + 2048];
+    __shared__ __align__(16) uint8_t s_w2[kPhaseW + 2048];
+    __shared__ __align__(16) uint8_t s_a0[kPhB * 544];
+    __shared__ __align__(16) uint8_t s_a1[kPhB * 544];
+    __shared__ __align__(16) uint8_t s_a2[kPhB * 544];
+    __shared__ float s_red[kMaxTiles * kPhWaves * kTR];   // [tile][wave][row]
+    Prob pb = pb0;
+    pb.setup(blockIdx.x);   // routed expert ids, read once before any weight load is issued
+    PhaseCtx c;
+    c.tid = threadIdx.x;
+    c.lane = c.tid & 63;
+    c.w = __builtin_amdgcn_readfirstlane(c.tid >> 6);
+    c.wg = blockIdx.x;
+    c.rb = (int64_t)nsb * 144;
+    c.xstride = xstride;
+    c.P = pb.nphase();
+    c.xr = buf_rsrc(X, xbytes);
+    c.n = c.lane & 15;
+    c.g = c.lane >> 4;
+    c.sw = (c.n >> 1) & 7;
+    c.rowb = 16u * (uint32_t)(72 * c.n);
+    c.hs = hdr_sel(c.g);
+    c.ck = code_k();
+
+    // issue the first kRing phases (phases past the end load nothing)
+    uint4 x0 = phase_issue(phase_or_empty(pb, c.wg, 0, c.P), c.xr, xstride, c.tid, c.w, c.lane, c.rb, s_w0);
+    uint4 x1 = phase_issue(phase_or_empty(pb, c.wg, 1, c.P), c.xr, xstride, c.tid, c.w, c.lane, c.rb, s_w1);
+    uint4 x2 = phase_issue(phase_or_empty(pb, c.wg, 2, c.P), c.xr, xstride, c.tid, c.w, c.lane, c.rb, s_w2);
+
+    float acc = 0.f;
+    u32x4_t A[8], B[8];   // block-diagonal activation operands: off-diagonal lanes stay zero
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        A[t] = u32x4_t{0u, 0u, 0u, 0u};
+        B[t] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    // all three ring steps run every round (a step past the last phase is empty), so the
+    // outstanding-load count is the same at every iteration and the waits stay static
+    for (int p = 0; p < c.P; p += kRing) {
+        phase_step(pb, c, p, x0, s_w0, s_a0, s_red, acc, A, B);
+        phase_step(pb, c, p + 1, x1, s_w1, s_a1, s_red, acc, A, B);
+        phase_step(pb, c, p + 2, x2, s_w2, s_a2, s_red, acc, A, B);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_s_barrier();
+    pb.finish(c.wg, s_red, c.tid);
+}
+
+template <class Prob>
+hipError_t run_phase(const Prob& pb, unsigned nwg, const uint16_t* X, int64_t xstride, int64_t xbytes, int nsb,
+                     hipStream_t st) {
+    hipLaunchKernelGGL((k_phase<Prob>), dim3(nwg), dim3(kPhWaves * 64), 0, st, pb, X, xstride, (uint32_t)xbytes,
+                       nsb);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ planning
+int pick_pd(int bpk) {
+    for (int pd = 4; pd >= 2; --pd)
+        if (bpk % pd == 0) return pd;
+    return 1;
+}
+
+// T tiles per workgroup, nact staged activations of MR rows.  Returns false when the shape
+// does not fit the kernel's staging or LDS limits.
+bool make_plan(int nsb, int T, int nact, int MR, int kp_max, Plan& p) {
+    int best = 0;
+    for (int kp = 1; kp <= kp_max && kp * T <= kMaxW; ++kp)
+        if (nsb % kp == 0) best = kp;
+    if (best == 0) return false;
+    p.KP = best;
+    p.bpk = nsb / best;
+    p.PD = pick_pd(p.bpk);
+    p.W = T * best;
+    p.nact = nact;
+    const int64_t ent = 8LL * 4 * MR;
+    p.lds = ent * 16 + (int64_t)nact * nsb * (ent * 16 + 8LL * MR * 4) + (int64_t)p.W * kTR * MR * 4;
+    const int64_t pieces = (int64_t)nact * MR * nsb * 32;
+    return p.lds <= kMaxLds && pieces <= (int64_t)kXL * 64 * p.W;
+}
+
+template <int MR, class Prob>
+hipError_t run_mfma(const Prob& pb, const Plan& pl, unsigned nwg, const uint16_t* X, int64_t xstride,
+                    int64_t xbytes, int K, int M, hipStream_t st) {
+    const dim3 grid(nwg), block(64 * pl.W);
+    const size_t lds = (size_t)pl.lds;
+#define AIPU_LAUNCH(PDV)                                                                                         \
+    hipLaunchKernelGGL((k_mfma_gemv<MR, PDV, Prob>), grid, block, lds, st, pb, X, xstride, (uint32_t)xbytes, K, M, \
+                       pl.nact, pl.KP, pl.bpk)
+    switch (pl.PD) {
+        case 1: AIPU_LAUNCH(1); break;
+        case 2: AIPU_LAUNCH(2); break;
+        case 3: AIPU_LAUNCH(3); break;
+        default: AIPU_LAUNCH(4); break;
+    }
+#undef AIPU_LAUNCH
+    return hipGetLastError();
+}
+
+// Single-row plan: T tiles per workgroup, each split into KP parts of BPK = GS * NG blocks.
+struct Plan1 {
+    int KP, GS, NG, XI, W;
+    int64_t lds;   // dynamic LDS (the weight slices)
+};
+
+constexpr int64_t kMaxLds1 = 80 * 1024;   // two workgroups per CU
+
+int dma_bytes(int gs) { return ((16 * 9 * gs + 63) / 64) * 1024; }
+// static LDS of k_gemv1<GS, XI>: zero region, activation slices, reduction
+int64_t static_lds1(int xi) { return (int64_t)kMaxW * 2 * xi * 544 + kMaxW * kTR * 4; }
+
+bool make_plan1(int nsb, int T, int kp_max, Plan1& p) {
+    for (int kp = (kp_max < kMaxW / T ? kp_max : kMaxW / T); kp >= 1; --kp) {
+        if (nsb % kp) continue;
+        const int bpk = nsb / kp;
+        const int xi_need = (bpk * 32 + 63) / 64;
+        const int xi = xi_need <= 2 ? 2 : (xi_need <= 4 ? 4 : (xi_need <= 8 ? 8 : 0));
+        if (xi == 0) continue;
+        for (int gs = 3; gs >= 1; --gs) {
+            if (bpk % gs) continue;
+            const int W = T * kp;
+            const int64_t lds = (int64_t)W * dma_bytes(gs);
+            if (lds + static_lds1(xi) > kMaxLds1) continue;
+            p = Plan1{kp, gs, bpk / gs, xi, W, lds};
+            return true;
+        }
+    }
+    return false;
+}
+
+template <class Prob>
+hipError_t run1(const Prob& pb, const Plan1& pl, unsigned nwg, const uint16_t* X, int64_t xstride, int64_t xbytes,
+                int K, hipStream_t st) {
+    const dim3 grid(nwg), block(64 * pl.W);
+    const size_t lds = (size_t)pl.lds;
+#define AIPU_L1(GSV, XIV)                                                                                             \
+    hipLaunchKernelGGL((k_gemv1<GSV, XIV, Prob>), grid, block, lds, st, pb, X, xstride, (uint32_t)xbytes, K, pl.KP, \
+                       pl.NG)
+#define AIPU_L1X(GSV)                        \
+    switch (pl.XI) {                         \
+        case 2: AIPU_L1(GSV, 2); break;      \
+        case 4: AIPU_L1(GSV, 4); break;      \
+        default: AIPU_L1(GSV, 8); break;     \
+    }
+    switch (pl.GS) {
+        case 1: AIPU_L1X(1); break;
+        case 2: AIPU_L1X(2); break;
+        default: AIPU_L1X(3); break;
+    }
+#undef AIPU_L1X
+#undef AIPU_L1
+    return hipGetLastError();
+}
+
+template <int MR>
+hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int M, uint16_t* y, float* yf,
+                      int64_t ystride, hipStream_t st) {
+    const int nsb = (int)(K / QK_K);
+    const ProbPlain<MR> pb{W, N, row_bytes(T_Q4_K, K), y, yf, ystride, M};
+    const unsigned nwg = (unsigned)((N + kTR - 1) / kTR);
+    Plan1 p1;
+    if (MR == 1 && make_plan1(nsb, 1, kMaxW, p1)) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
+    Plan pl;
+    if (!make_plan(nsb, 1, 1, MR, kMaxW, pl)) return hipErrorInvalidValue;
+    return run_mfma<MR>(pb, pl, nwg, x, 0, (int64_t)M * K * 2, (int)K, M, st);
+}
+
+}  // namespace
+
+// Whether the matrix-core GEMV serves this shape (Q4_K, any M, the staging limits).
+bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M) {
+    if (N < 1 || K < QK_K || K % QK_K != 0 || M < 1) return false;
+    if (N * row_bytes(T_Q4_K, K) >= (int64_t)1 << 40) return false;
+    Plan pl;
+    const int mr = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
+    return K <= (1 << 20) && make_plan((int)(K / QK_K), 1, 1, mr, kMaxW, pl);
+}
+
+// y[M][N] (row stride ystride) = x[M][K] . W^T, in passes of at most 4 activation rows.
+hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
+                            float* y_f32, int64_t ystride, hipStream_t st) {
+    const uint8_t* W = (const uint8_t*)w;
+    for (int64_t m0 = 0; m0 < M; m0 += 4) {
+        const int mr = (int)(M - m0 < 4 ? M - m0 : 4);
+        const uint16_t* xm = x + m0 * K;
+        uint16_t* ym = y + m0 * ystride;
+        float* yfm = y_f32 ? y_f32 + m0 * ystride : nullptr;
+        hipError_t e;
+        if (mr == 1) e = plain_pass<1>(W, N, K, xm, 1, ym, yfm, ystride, st);
+        else if (mr == 2) e = plain_pass<2>(W, N, K, xm, 2, ym, yfm, ystride, st);
+        else e = plain_pass<4>(W, N, K, xm, mr, ym, yfm, ystride, st);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
+                                  const int32_t* sel, int topk, int nslots, int64_t E, int64_t H, int64_t I,
+                                  const uint16_t* x, uint16_t* h, hipStream_t st) {
+    const int nsb = (int)(H / QK_K);
+    if (I % kTR != 0) return hipErrorInvalidValue;
+    const int64_t rb = row_bytes(T_Q4_K, H);
+    const ProbGateUp pb{G, U, shG, shU, sel, topk, (int)E, (int)(I / kTR), rb, rb * I, h, I};
+    const unsigned nwg = (unsigned)(nslots * (I / kTR));
+    Plan1 p1;
+    if (make_plan1(nsb, 2, 4, p1)) return run1(pb, p1, nwg, x, 0, H * 2, (int)H, st);
+    Plan pl;
+    if (!make_plan(nsb, 2, 1, 1, 4, pl)) return hipErrorInvalidValue;
+    return run_mfma<1>(pb, pl, nwg, x, 0, H * 2, (int)H, 1, st);
+}
+
+hipError_t launch_moe_down_mfma(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
+                                int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h, uint16_t* y,
+                                int passthrough, hipStream_t st) {
+    const int nsb = (int)(I / QK_K);
+    const int64_t rb = row_bytes(T_Q4_K, I);
+    const ProbDown pb{D, shD, sel, selw, topk, nslots, (int)E, passthrough, H, rb, rb * H, y};
+    const unsigned nwg = (unsigned)((H + kTR - 1) / kTR);
+    const int kpmax = kMaxW / nslots > 0 ? kMaxW / nslots : 1;
+    Plan1 p1;
+    if (nslots <= kMaxW && make_plan1(nsb, nslots, kpmax, p1))
+        return run1(pb, p1, nwg, h, I, (int64_t)nslots * I * 2, (int)I, st);
+    Plan pl;
+    if (!make_plan(nsb, nslots, nslots, 1, kpmax, pl)) return hipErrorInvalidValue;
+    return run_mfma<1>(pb, pl, nwg, h, I, (int64_t)nslots * I * 2, (int)I, 1, st);
+}
+
+bool moe_mfma_supported(int nslots, int64_t H, int64_t I) {
+    Plan p1, p2;
+    return I % kTR == 0 && make_plan((int)(H / QK_K), 2, 1, 1, 4, p1) &&
+           make_plan((int)(I / QK_K), nslots, nslots, 1, kMaxW / nslots > 0 ? kMaxW / nslots : 1, p2);
+}
+
+}  // namespace aipu

@@ -45,6 +45,18 @@ hipError_t launch_gemv_fast(int type, const void* w, int64_t N, int64_t K, const
 hipError_t launch_gemv_tiles(const aipu_tile_desc* tiles, int n_tiles, int64_t N, int64_t K, const uint16_t* x,
                              int64_t M, uint16_t* y, float* y_f32, int mode, hipStream_t st);
 
+// gemv_mfma.hip -- matrix-core Q4_K GEMV (tolerance mode)
+bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M);
+hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
+                            float* y_f32, int64_t ystride, hipStream_t st);
+bool moe_mfma_supported(int nslots, int64_t H, int64_t I);
+hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
+                                  const int32_t* sel, int topk, int nslots, int64_t E, int64_t H, int64_t I,
+                                  const uint16_t* x, uint16_t* h, hipStream_t st);
+hipError_t launch_moe_down_mfma(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
+                                int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h, uint16_t* y,
+                                int passthrough, hipStream_t st);
+
 // moe.hip
 struct MoeArgs {
     int router_type;

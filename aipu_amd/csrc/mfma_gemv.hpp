@@ -1,0 +1,162 @@
+// Matrix-core Q4_K GEMV core for gfx950 (tolerance mode), M = 1..4 activation rows per pass.
+//
+// Tile.  One wave computes a 16-row tile of the weight matrix over a range of Q4_K blocks
+// with v_mfma_f32_16x16x32_bf16 (D[i][n] = sum_k A[i][k] B[k][n]; lane l supplies
+// A[l%16][8(l/16)..+7] and B[8(l/16)..+7][l%16], and holds D[4(l/16)+r][l%16], r = 0..3).
+//   B (weights): lane l = 16g + n owns output row n of the tile and the 32-byte qs chunk g of
+//     each block (bytes 32g..32g+31), i.e. sub-block 2g in the low nibbles and sub-block
+//     2g+1 in the high nibbles.  Four MFMAs (t = 0..3) cover the low nibbles, four (t = 4..7)
+//     the high nibbles, 8 bytes per MFMA.
+//   A (activations): block diagonal.  Row i = 4g + m of A carries activation row m (m < MR)
+//     on K-group g only, so D[4g + m][n] accumulates sub-block (2g + h) of row n against
+//     activation row m, for all four chunks g at once, and lane 16g + n finds exactly the
+//     sums of its own row and chunk in its D registers (r = m).  All other A entries are 0.
+//   Codes: a nibble q at bits 0..3 (or 16..19) of a qs dword becomes the bf16 pattern
+//     0x4300 | q, which is exactly 128 + q, with one and-or per two codes (plus one shift per
+//     pair not already at bits 0..3); the products (128 + q) * a are exact and the MFMA
+//     accumulates in fp32.  The accumulator starts at -128 * sum(a) of the sub-block, so it
+//     ends at sum(q * a).
+//   Epilogue per block and lane: acc += d * (sc_lo * S_lo + sc_hi * S_hi)
+//                                        - dmin * (m_lo * A_lo + m_hi * A_hi),
+//     the factorised form of sum_k a_k * (d*sc*q_k - dmin*m) (tools/q4k_ref.py:53-59).
+//
+// Lane -> K order.  Within the 8 bytes of one MFMA the code pairs are built in byte order
+// (0,2) (1,3) (4,6) (5,7); the activations are staged in LDS in the same order, so the
+// products line up.  Activation piece p (8 consecutive bf16 starting at 8p) belongs to
+// block p / 32, chunk (p / 8) % 4 and MFMA t = p % 8.
+#pragma once
+
+#include "common.hpp"
+
+namespace aipu {
+namespace mg {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kTR = 16;                  // output rows per tile
+constexpr uint32_t kNT = 2;              // buffer-load cache policy: streaming (nt)
+constexpr uint32_t kOOB = 0xF0000000u;   // buffer offset that reads as zero without a memory access
+constexpr uint32_t kCodeMask = 0x000F000Fu;
+constexpr uint32_t kCodeBias = 0x43004300u;   // bf16 128.0 in both halves
+constexpr float kCodeBiasF = 128.0f;
+
+__device__ __forceinline__ f32x4_t mfma(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// (v & mask) | bias in one v_and_or_b32: gfx9 VOP3 encodings take no literal and read at
+// most one scalar operand, so the mask comes from an SGPR and the bias from a VGPR that the
+// caller keeps live (CodeK).
+struct CodeK {
+    uint32_t mask;   // wave-uniform (SGPR)
+    uint32_t bias;   // VGPR
+};
+
+__device__ __forceinline__ CodeK code_k() {
+    CodeK k;
+    k.mask = __builtin_amdgcn_readfirstlane(kCodeMask);
+    k.bias = kCodeBias;
+    return k;
+}
+
+__device__ __forceinline__ uint32_t c16(uint32_t v, const CodeK& k) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(k.mask), "v"(k.bias));
+    return r;
+}
+
+// B operands (128 + q codes) of the low-nibble and high-nibble MFMAs over qs dwords x0, x1:
+// element pairs (byte 0, byte 2), (1, 3), (4, 6), (5, 7) of the 8 bytes.
+__device__ __forceinline__ u32x4_t codes_lo(uint32_t x0, uint32_t x1, const CodeK& k) {
+    return u32x4_t{c16(x0, k), c16(x0 >> 8, k), c16(x1, k), c16(x1 >> 8, k)};
+}
+__device__ __forceinline__ u32x4_t codes_hi(uint32_t x0, uint32_t x1, const CodeK& k) {
+    return u32x4_t{c16(x0 >> 4, k), c16(x0 >> 12, k), c16(x1 >> 4, k), c16(x1 >> 12, k)};
+}
+
+// 8 natural-order bf16 (w0 = a0|a1<<16 ...) -> the MFMA element order (a0,a2)(a1,a3)(a4,a6)(a5,a7).
+__device__ __forceinline__ u32x4_t act_perm(const uint4& v) {
+    return u32x4_t{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                   __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+}
+
+__device__ __forceinline__ uint4 wload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// One lane's bytes of one block: the 16-B header and its 32-B qs chunk.
+struct Raw {
+    uint4 h, q0, q1;
+};
+
+__device__ __forceinline__ Raw raw_load(__amdgpu_buffer_rsrc_t r, uint32_t off, int g) {
+    Raw x;
+    x.h = wload(r, off);
+    x.q0 = wload(r, off + 16u + 32u * g);
+    x.q1 = wload(r, off + 32u + 32u * g);
+    return x;
+}
+
+// Scale/min of sub-blocks 2g and 2g+1 from the 12 packed bytes (header dwords y, z, w),
+// following get_scale_min_k4 (tools/q4k_ref.py:27-37):
+//   j < 4 : sc = s[j] & 63,                      m = s[j+4] & 63
+//   j >= 4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4,  m = (s[j+4] >> 4) | (s[j] >> 6) << 4
+// Sub-blocks 2g, 2g+1 read bytes jb = 2(g&1), jb+1 of each dword.
+struct HdrSel {
+    uint32_t selB, selC, mC, mC4, mB2, mB;
+};
+
+__device__ __forceinline__ HdrSel hdr_sel(int g) {
+    HdrSel s;
+    const bool lowj = g < 2;
+    const bool jb2 = (g & 1) != 0;
+    s.selB = jb2 ? 0x07060302u : 0x05040100u;
+    s.selC = jb2 ? 0x03020302u : 0x01000100u;
+    s.mC = lowj ? 0u : 0x00000F0Fu;
+    s.mC4 = lowj ? 0u : 0x0F0F0000u;
+    s.mB2 = lowj ? 0u : 0x30303030u;
+    s.mB = lowj ? 0x3F3F3F3Fu : 0u;
+    return s;
+}
+
+struct Hdr {
+    float d, dm, sc0, sc1, m0, m1;
+};
+
+__device__ __forceinline__ Hdr hdr_decode(const uint4& h, const HdrSel& S) {
+    Hdr H;
+    H.d = f16_to_f32(h.x);
+    H.dm = f16_to_f32(h.x >> 16);
+    const uint32_t B = __builtin_amdgcn_perm(h.z, h.y, S.selB);
+    const uint32_t C = __builtin_amdgcn_perm(h.w, h.w, S.selC);
+    const uint32_t R = (C & S.mC) | ((C >> 4) & S.mC4) | ((B >> 2) & S.mB2) | (B & S.mB);
+    H.sc0 = (float)(R & 0xFFu);
+    H.sc1 = (float)((R >> 8) & 0xFFu);
+    H.m0 = (float)((R >> 16) & 0xFFu);
+    H.m1 = (float)(R >> 24);
+    return H;
+}
+
+// LDS layout of one staged activation (M_pad = MR rows, nsb blocks):
+//   A entries (16 B): [b][t][g][m]  at index (b*8 + t)*4*MR + g*MR + m
+//   sums (fp32):      [b][g][h][m]  at index ((b*4 + g)*2 + h)*MR + m
+// and a zero region of 8*4*MR entries that the off-diagonal lanes read.
+template <int MR>
+struct ActLayout {
+    static constexpr int kEntriesPerBlock = 8 * 4 * MR;
+    static constexpr int kSumsPerBlock = 8 * MR;
+    __host__ __device__ static int64_t bytes(int nsb) { return (int64_t)nsb * (kEntriesPerBlock * 16 + kSumsPerBlock * 4); }
+    static constexpr int kZeroBytes = kEntriesPerBlock * 16;
+};
+
+}  // namespace mg
+}  // namespace aipu

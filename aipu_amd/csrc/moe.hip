@@ -124,6 +124,11 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
             AIPU_TRY(hipGetLastError());
         }
     }
+    if (fast && moe_mfma_supported(nslots, a.H, a.I)) {
+        AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, sel, a.topk, nslots, a.E, a.H,
+                                        a.I, a.x, h, st));
+        return launch_moe_down_mfma(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y, 0, st);
+    }
     if (fast) {
         AIPU_TRY(launch_moe_gateup_fast(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, sel, a.topk, nslots, a.E, a.H,
                                         a.I, a.x, h, st));
@@ -162,6 +167,10 @@ hipError_t launch_swiglu_expert(int type, const void* wg, const void* wu, const 
         // No routing: the expert runs as the shared slot.  The kernels still read one
         // (ignored) expert id, so they get the workspace's id slot rather than a null pointer.
         const int32_t* no_sel = (const int32_t*)(ws + L.sel);
+        if (moe_mfma_supported(1, H, I)) {
+            AIPU_TRY(launch_moe_gateup_mfma(G, U, G, U, no_sel, 0, 1, 1, H, I, x, h, st));
+            return launch_moe_down_mfma(D, D, no_sel, nullptr, 0, 1, 1, H, I, h, y, 1, st);
+        }
         AIPU_TRY(launch_moe_gateup_fast(G, U, G, U, no_sel, 0, 1, 1, H, I, x, h, st));
         return launch_moe_down_fast(D, D, no_sel, nullptr, 0, 1, 1, H, I, h, y, 1, st);
     }

@@ -14,6 +14,13 @@ hipError_t launch_gemv_tiles(const aipu_tile_desc* tiles, int n_tiles, int64_t N
     // kernels express by running once per activation row.
     for (int t = 0; t < n_tiles; ++t) {
         const aipu_tile_desc& d = tiles[t];
+        if (mode == AIPU_MODE_FAST && d.ggml_type == T_Q4_K && gemv_mfma_supported(d.nrows, K, M)) {
+            // the matrix-core GEMV writes all M rows of the tile's column slice directly
+            const hipError_t e = launch_gemv_mfma(d.w, d.nrows, K, x, M, y + d.row0,
+                                                  y_f32 ? y_f32 + d.row0 : nullptr, N, st);
+            if (e != hipSuccess) return e;
+            continue;
+        }
         for (int64_t m = 0; m < M; ++m) {
             hipError_t e;
             uint16_t* ym = y + m * N + d.row0;
