@@ -19,6 +19,7 @@
 #include "glm_act.hpp"
 #include "launch.hpp"
 #include "mfma_gemv.hpp"
+#include "route.hpp"
 
 namespace aipu {
 
@@ -46,6 +47,8 @@ struct ProbPlain {
     float* Yf;
     int64_t ystride;   // N of the full output (tiles of a mixed call write a column slice)
     int M;
+    static constexpr bool kRoutes = false;
+    __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ TileRef tile(int wg, int) const {
         const int64_t r0 = (int64_t)wg * kTR;
         const int64_t nv = N - r0;
@@ -70,17 +73,39 @@ __device__ __forceinline__ int routed_expert(const int32_t* sel, int s, int E) {
 
 // MoE gate/up: workgroup (slot, 16-row tile of I); tile 0 = gate rows, tile 1 = up rows of
 // the slot's expert (slot topk = the shared expert).  h[slot][i] = bf16(silu(g) * u).
+// With route.logits set, every workgroup first computes the routing decision itself from
+// the router logits (route.hpp) -- no workgroup waits for another -- and workgroup 0
+// publishes it for the down leg and the caller.
 struct ProbGateUp {
     const uint8_t *G, *U, *shG, *shU;
-    const int32_t* sel;
+    MoeRoute route;
     int topk, E, itiles;
     int64_t rb, ebytes;
     uint16_t* h;
     int64_t I;
+    int eid;   // expert of this workgroup's slot (setup)
+    static constexpr bool kRoutes = true;
+    __device__ void setup(int wg, uint32_t* keys, uint32_t* win, int32_t* sel, uint16_t* selw) {
+        const int s = wg / itiles;
+        if (route.logits) {
+            // workgroup 0 also forms the slot weights and publishes the decision
+            route_workgroup(route.logits, E, topk, route.scale_bits, keys, win, sel, selw, wg == 0);
+            if (wg == 0 && (int)threadIdx.x < topk) {
+                route.sel_pub[threadIdx.x] = sel[threadIdx.x];
+                route.selw_pub[threadIdx.x] = selw[threadIdx.x];
+                if (route.sel_api) route.sel_api[threadIdx.x] = sel[threadIdx.x];
+                if (route.selw_api) route.selw_api[threadIdx.x] = selw[threadIdx.x];
+            }
+            const int e = s < topk ? (int)(0xFFFFu - (win[s] & 0xFFFFu)) : 0;
+            eid = __builtin_amdgcn_readfirstlane(e < 0 ? 0 : (e >= E ? E - 1 : e));
+        } else {
+            eid = s < topk ? __builtin_amdgcn_readfirstlane(routed_expert(route.sel, s, E)) : 0;
+        }
+    }
     __device__ TileRef tile(int wg, int t) const {
         const int s = wg / itiles, it = wg - s * itiles;
         const uint8_t* base;
-        if (s < topk) base = (t ? U : G) + (int64_t)routed_expert(sel, s, E) * ebytes;
+        if (s < topk) base = (t ? U : G) + (int64_t)eid * ebytes;
         else base = t ? shU : shG;
         return TileRef{base + (int64_t)it * kTR * rb, kTR, 0};
     }
@@ -109,6 +134,8 @@ struct ProbDown {
     int topk, nslots, E, passthrough;
     int64_t H, rb, ebytes;
     uint16_t* Y;
+    static constexpr bool kRoutes = false;
+    __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ TileRef tile(int wg, int t) const {
         const int64_t d0 = (int64_t)wg * kTR;
         const uint8_t* base = t < topk ? D + (int64_t)routed_expert(sel, t, E) * ebytes : shD;
@@ -173,7 +200,7 @@ __device__ __forceinline__ u32x4_t lds128(const uint8_t* smem, uint32_t off) {
 }
 
 template <int MR, int PD, class Prob>
-__global__ __launch_bounds__(kMaxW * 64) void k_mfma_gemv(Prob pb, const uint16_t* __restrict__ X, int64_t xstride,
+__global__ __launch_bounds__(kMaxW * 64) void k_mfma_gemv(Prob pb0, const uint16_t* __restrict__ X, int64_t xstride,
                                                           uint32_t xbytes, int K, int M, int nact, int KP, int bpk) {
     static_assert(MR == 1 || MR == 2 || MR == 4, "MR must be 1, 2 or 4");
     using L = ActLayout<MR>;
@@ -207,6 +234,14 @@ __global__ __launch_bounds__(kMaxW * 64) void k_mfma_gemv(Prob pb, const uint16_
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. the wave's tile and its first PD blocks of weights
+    Prob pb = pb0;
+    if constexpr (Prob::kRoutes) {
+        __shared__ uint32_t r_keys[kRouteMaxE];
+        __shared__ uint32_t r_win[kRouteMaxTopk];
+        __shared__ int32_t r_sel[kRouteMaxTopk];
+        __shared__ uint16_t r_selw[kRouteMaxTopk];
+        pb.setup(wg, r_keys, r_win, r_sel, r_selw);
+    }
     const int tt = w / KP, kp = w - tt * KP;
     const TileRef tr = pb.tile(wg, tt);
     const int64_t rb = (int64_t)nsb * 144;
@@ -314,30 +349,8 @@ __global__ __launch_bounds__(kMaxW * 64) void k_mfma_gemv(Prob pb, const uint16_
     pb.finish(wg, red, KP, tid);
 }
 
-// LDS reads of one block step.  Written as asm because the direct-to-LDS loads of the other
-// ring slots are still in flight and the compiler cannot prove that these reads do not
-// alias them (it would wait for every outstanding load); the ordering is established by
-// the explicit vmcnt wait and the barrier before them.
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-struct StepIn {
-    u32x4_t h, q0, q1;
-    f32x2_t as;
-};
-
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// Header, qs chunk and sub-block sums of one lane (all lanes).
-__device__ __forceinline__ void step_reads(uint32_t ah, uint32_t aq0, uint32_t aq1, uint32_t asum, StepIn& o) {
-    asm volatile(
-        "ds_read_b128 %0, %4\n\t"
-        "ds_read_b128 %1, %5\n\t"
-        "ds_read_b128 %2, %6\n\t"
-        "ds_read_b64 %3, %7"
-        : "=&v"(o.h), "=&v"(o.q0), "=&v"(o.q1), "=&v"(o.as)
-        : "v"(ah), "v"(aq0), "v"(aq1), "v"(asum));
 }
 
 // The 8 activation operands of a block, read on the lanes in `mask` only (the diagonal
@@ -362,14 +375,7 @@ __device__ __forceinline__ void a_reads(u32x4_t (&A)[8], uint32_t aa, uint64_t m
         : "v"(aa), "s"(mask));
 }
 
-// Wait for the LDS reads above; the operands are tied so that no use moves above the wait.
-__device__ __forceinline__ void lds_wait(StepIn& a, StepIn& b, u32x4_t (&A)[8], u32x4_t (&B)[8]) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(a.h), "+v"(a.q0), "+v"(a.q1), "+v"(a.as), "+v"(b.h), "+v"(b.q0), "+v"(b.q1), "+v"(b.as),
-                   "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]),
-                   "+v"(B[0]), "+v"(B[1]), "+v"(B[2]), "+v"(B[3]), "+v"(B[4]), "+v"(B[5]), "+v"(B[6]), "+v"(B[7]));
-}
-
+// Wait for the reads above; the operands are tied so that no use moves above the wait.
 __device__ __forceinline__ void a_wait(u32x4_t (&A)[8]) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]));
@@ -418,7 +424,7 @@ __device__ __forceinline__ void dma_group(__amdgpu_buffer_rsrc_t wr, uint8_t* sl
 }
 
 template <int GS, int XI, class Prob>
-__global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb, const uint16_t* __restrict__ X, int64_t xstride,
+__global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* __restrict__ X, int64_t xstride,
                                                       uint32_t xbytes, int K, int KP, int NG) {
     // Separate LDS objects for the direct-to-LDS weight slices (dynamic) and for everything
     // the waves write themselves (static), so the compiler can see that the staging writes
@@ -438,6 +444,14 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb, const uint16_t* _
     float* wS = (float*)(wA + kA);
     uint8_t* wW = s_w + (uint32_t)w * Dma<GS>::kBytes;
 
+    Prob pb = pb0;
+    if constexpr (Prob::kRoutes) {   // routing decision (before any weight address is known)
+        __shared__ uint32_t r_keys[kRouteMaxE];
+        __shared__ uint32_t r_win[kRouteMaxTopk];
+        __shared__ int32_t r_sel[kRouteMaxTopk];
+        __shared__ uint16_t r_selw[kRouteMaxTopk];
+        pb.setup(wg, r_keys, r_win, r_sel, r_selw);
+    }
     const int tt = w / KP, kp = w - tt * KP;
     const TileRef tr = pb.tile(wg, tt);
     const int kb0 = kp * BPK;
@@ -528,360 +542,6 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb, const uint16_t* _
     if (lane < kTR) red[w * kTR + lane] = acc;
     __syncthreads();
     pb.finish(wg, red, KP, tid);
-}
-
-// ------------------------------------------------------------ phased kernel (M = 1)
-// A workgroup of 4 waves streams a sequence of phases.  A phase is 16 rows x 8 Q4_K blocks
-// of one tile (16 runs of 1152 contiguous row bytes = 9 whole cache lines each) against one
-// activation; wave w computes blocks w and w + 4 of the phase as soon as the phase has
-// landed, so the arithmetic follows the memory stream and the tail after the last byte is
-// two blocks per wave.  Phases go through a ring of three LDS slots (weights by
-// direct-to-LDS loads, activations staged by the threads in the MFMA operand order).
-//
-// Slot layout: 16-B piece c (0..71) of tile row n sits at slot 72n + (c ^ ((n >> 1) & 7)),
-// which puts the 16 rows' copies of any piece in 16 different bank quads (conflict-free
-// 16-lane reads) while every load instruction still covers one contiguous run of slots.
-constexpr int kPhB = 8;                      // blocks per phase
-constexpr int kPhWaves = 4;                  // waves per workgroup
-constexpr int kPhBpw = kPhB / kPhWaves;      // blocks per wave per phase
-constexpr int kPhaseW = 16 * 72 * 16;        // weight bytes of a phase slot (18 KB)
-constexpr int kPhaseInst = 16 * 72 / 64;     // 18 load instructions per phase
-constexpr int kPhIpw = (kPhaseInst + kPhWaves - 1) / kPhWaves;   // 5 per wave (2 spare in all)
-constexpr int kRing = 3;
-constexpr int kMaxTiles = 8;
-
-struct PhaseRef {
-    const uint8_t* lo;   // tile rows 0..7 start here (row stride rb)
-    const uint8_t* hi;   // tile rows 8..15
-    int nlo, nhi;        // valid rows in each half
-    int blk0, nb;        // first block of the phase and its block count (<= kPhB)
-    int act;             // activation index
-    int tile;            // which accumulator (tile) the phase feeds
-    bool last;           // last phase of its tile
-};
-
-// Plain GEMV as phases: one tile of 16 rows, phase p = blocks [8p, 8p + 8).
-struct PhPlain {
-    const uint8_t* W;
-    int64_t N, rb;
-    int nsb;
-    uint16_t* Y;
-    float* Yf;
-    int64_t ystride;
-    __device__ void setup(int) {}
-    __device__ int nphase() const { return (nsb + kPhB - 1) / kPhB; }
-    __device__ PhaseRef phase(int wg, int p) const {
-        const int64_t r0 = (int64_t)wg * kTR;
-        const int64_t nv = N - r0;
-        const int nvalid = (int)(nv < kTR ? nv : kTR);
-        PhaseRef f;
-        f.lo = W + r0 * rb;
-        f.hi = f.lo + 8 * rb;
-        f.nlo = nvalid < 8 ? nvalid : 8;
-        f.nhi = nvalid > 8 ? nvalid - 8 : 0;
-        f.blk0 = p * kPhB;
-        f.nb = nsb - f.blk0 < kPhB ? nsb - f.blk0 : kPhB;
-        f.act = 0;
-        f.tile = 0;
-        f.last = p == nphase() - 1;
-        return f;
-    }
-    __device__ void finish(int wg, const float* red, int tid) const {   // red[tile][wave][16]
-        if (tid >= kTR) return;
-        const int64_t row = (int64_t)wg * kTR + tid;
-        if (row >= N) return;
-        float v = 0.f;
-        for (int k = 0; k < kPhWaves; ++k) v += red[k * kTR + tid];
-        Y[row] = (uint16_t)bf16_rne(v);
-        if (Yf) Yf[row] = v;
-    }
-};
-
-// MoE gate/up as phases: the 16 tile rows are gate rows i0..i0+7 (0..7) and up rows
-// i0..i0+7 (8..15) of the slot's expert; h[slot][i0 + n] = bf16(silu(g_n) * u_n).
-struct PhGateUp {
-    const uint8_t *G, *U, *shG, *shU;
-    const int32_t* sel;
-    int topk, E, itiles, nsb;
-    int64_t rb, ebytes, I;
-    uint16_t* h;
-    int eid;   // expert of this workgroup's slot (set up once per workgroup)
-    __device__ void setup(int wg) {
-        const int s = wg / itiles;
-        eid = s < topk ? __builtin_amdgcn_readfirstlane(routed_expert(sel, s, E)) : 0;
-    }
-    __device__ int nphase() const { return (nsb + kPhB - 1) / kPhB; }
-    __device__ PhaseRef phase(int wg, int p) const {
-        const int s = wg / itiles, it = wg - s * itiles;
-        const uint8_t *g, *u;
-        if (s < topk) {
-            const int64_t eo = (int64_t)eid * ebytes;
-            g = G + eo;
-            u = U + eo;
-        } else {
-            g = shG;
-            u = shU;
-        }
-        PhaseRef f;
-        f.lo = g + (int64_t)it * 8 * rb;
-        f.hi = u + (int64_t)it * 8 * rb;
-        f.nlo = 8;
-        f.nhi = 8;
-        f.blk0 = p * kPhB;
-        f.nb = nsb - f.blk0 < kPhB ? nsb - f.blk0 : kPhB;
-        f.act = 0;
-        f.tile = 0;
-        f.last = p == nphase() - 1;
-        return f;
-    }
-    __device__ void finish(int wg, const float* red, int tid) const {
-        if (tid >= 8) return;
-        const int s = wg / itiles, it = wg - s * itiles;
-        float g = 0.f, u = 0.f;
-        for (int k = 0; k < kPhWaves; ++k) {
-            g += red[k * kTR + tid];
-            u += red[k * kTR + 8 + tid];
-        }
-        const uint32_t gb = bf16_rne(g), ub = bf16_rne(u);
-        h[(int64_t)s * I + (int64_t)it * 8 + tid] = (uint16_t)bf16_rne(bf16_to_f32(glm_silu_bf16(gb)) * bf16_to_f32(ub));
-    }
-};
-
-// MoE down as phases: tile s = slot s (16 rows of H of its expert, K = I), phases walk
-// the slots in order (and each slot's K in chunks of 8 blocks); the finish combines the
-// slots in slot order as in tools/glm_model_q4k_ref.py:799-809.
-struct PhDown {
-    const uint8_t *D, *shD;
-    const int32_t* sel;
-    const uint16_t* selw;
-    int topk, nslots, E, passthrough, nsb;
-    int64_t H, rb, ebytes;
-    uint16_t* Y;
-    int eid[kMaxTiles];   // experts of the slots (set up once per workgroup)
-    __device__ void setup(int) {
-#pragma unroll
-        for (int s = 0; s < kMaxTiles; ++s)
-            eid[s] = s < topk ? __builtin_amdgcn_readfirstlane(routed_expert(sel, s, E)) : 0;
-    }
-    __device__ int pps() const { return (nsb + kPhB - 1) / kPhB; }
-    __device__ int nphase() const { return nslots * pps(); }
-    __device__ PhaseRef phase(int wg, int p) const {
-        const int q = pps();
-        const int s = p / q, pk = p - s * q;
-        const int64_t d0 = (int64_t)wg * kTR;
-        const int64_t nv = H - d0;
-        const int nvalid = (int)(nv < kTR ? nv : kTR);
-        int e = 0;
-#pragma unroll
-        for (int k = 0; k < kMaxTiles; ++k) e = k == s ? eid[k] : e;
-        const uint8_t* base = s < topk ? D + (int64_t)e * ebytes : shD;
-        PhaseRef f;
-        f.lo = base + d0 * rb;
-        f.hi = f.lo + 8 * rb;
-        f.nlo = nvalid < 8 ? nvalid : 8;
-        f.nhi = nvalid > 8 ? nvalid - 8 : 0;
-        f.blk0 = pk * kPhB;
-        f.nb = nsb - f.blk0 < kPhB ? nsb - f.blk0 : kPhB;
-        f.act = s;
-        f.tile = s;
-        f.last = pk == q - 1;
-        return f;
-    }
-    __device__ void finish(int wg, const float* red, int tid) const {
-        if (tid >= kTR) return;
-        const int64_t d = (int64_t)wg * kTR + tid;
-        if (d >= H) return;
-        float facc = 0.f;
-        for (int s = 0; s < nslots; ++s) {
-            float ys = 0.f;
-            for (int k = 0; k < kPhWaves; ++k) ys += red[(s * kPhWaves + k) * kTR + tid];
-            if (passthrough) {
-                Y[d] = (uint16_t)bf16_rne(ys);
-                return;
-            }
-            const float yb = bf16_to_f32(bf16_rne(ys));
-            const float pr = s < topk ? bf16_to_f32(selw[s]) * yb : yb;
-            facc = facc + pr;
-        }
-        Y[d] = (uint16_t)bf16_rne(facc);
-    }
-};
-
-// Issue one phase into a ring slot: the activation piece of this thread (M = 1: 8 blocks x
-// 32 pieces = 256 pieces, one per thread), then this wave's weight-load instructions
-// (instructions w, w + 4, ... of the phase's 18; the spare ones read out of range, which
-// writes zeros into the slot's tail).  A phase past the end (nb <= 0) loads nothing but
-// still issues the same instructions, so every wave's count of outstanding loads is the
-// same at every point and all waits are static.  Offsets are computed in 32 bits and
-// selected without branches (a branch would let the compiler move loads between blocks).
-__device__ __forceinline__ uint4 phase_issue(const PhaseRef& f, __amdgpu_buffer_rsrc_t xr, int64_t xstride, int tid,
-                                             int w, int lane, int64_t rb, uint8_t* wslot) {
-    const int q = tid;
-    const uint32_t xo = 2u * ((uint32_t)(f.act * xstride) + (uint32_t)f.blk0 * QK_K + 8u * (uint32_t)q);
-    const uint4 xv = buf_load16(xr, q < 32 * f.nb ? xo : kOOB);
-    const uint32_t rb32 = (uint32_t)rb;
-    const __amdgpu_buffer_rsrc_t rlo = buf_rsrc(f.lo, (uint32_t)f.nlo * rb32);
-    const __amdgpu_buffer_rsrc_t rhi = buf_rsrc(f.hi, (uint32_t)f.nhi * rb32);
-    const uint32_t b0 = (uint32_t)f.blk0 * 144u;
-    const int climit = 9 * f.nb;
-#pragma unroll
-    for (int k = 0; k < kPhIpw; ++k) {
-        const int i = w + kPhWaves * k;
-        const int sl = 64 * i + lane;        // destination slot
-        const int n = sl / 72, cs = sl - n * 72;
-        const int c = cs ^ ((n >> 1) & 7);   // source piece of row n
-        const uint32_t o = (uint32_t)(n & 7) * rb32 + b0 + 16u * (uint32_t)c;
-        const uint32_t off = (i < kPhaseInst && c < climit) ? o : kOOB;
-        lds_dma16(i < 9 ? rlo : rhi, wslot + 1024 * (i < kPhaseInst ? i : kPhaseInst), off);
-    }
-    return xv;
-}
-
-struct PhaseCtx {
-    int tid, w, lane, n, g, sw, P, wg;
-    uint32_t rowb;
-    int64_t rb, xstride;
-    __amdgpu_buffer_rsrc_t xr;
-    HdrSel hs;
-    CodeK ck;
-};
-
-template <class Prob>
-__device__ __forceinline__ PhaseRef phase_or_empty(const Prob& pb, int wg, int p, int P) {
-    PhaseRef f = pb.phase(wg, p < P ? p : P - 1);
-    if (p >= P) f.nb = 0;
-    return f;
-}
-
-// Block (ws row base, block index b within the phase) -> this lane's partial dot product.
-__device__ __forceinline__ float block_dot(const StepIn& in, const u32x4_t (&A)[8], const PhaseCtx& c) {
-    f32x4_t dlo = {-kCodeBiasF * in.as.x, 0.f, 0.f, 0.f};
-    f32x4_t dhi = {-kCodeBiasF * in.as.y, 0.f, 0.f, 0.f};
-    const uint32_t qd[8] = {in.q0.x, in.q0.y, in.q0.z, in.q0.w, in.q1.x, in.q1.y, in.q1.z, in.q1.w};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        dlo = mfma(A[t], codes_lo(qd[2 * t], qd[2 * t + 1], c.ck), dlo);
-        dhi = mfma(A[4 + t], codes_hi(qd[2 * t], qd[2 * t + 1], c.ck), dhi);
-    }
-    const Hdr H = hdr_decode(make_uint4(in.h.x, in.h.y, in.h.z, in.h.w), c.hs);
-    const float t1 = __builtin_fmaf(H.sc1, dhi[0], H.sc0 * dlo[0]);
-    const float v = __builtin_fmaf(H.m1, in.as.y, H.m0 * in.as.x);
-    return __builtin_fmaf(H.d, t1, -(H.dm * v));
-}
-
-template <class Prob>
-__device__ __forceinline__ void phase_step(const Prob& pb, const PhaseCtx& c, int p, uint4& xv, uint8_t* wslot,
-                                           uint8_t* act, float* red, float& acc, u32x4_t (&A)[8], u32x4_t (&B)[8]) {
-    const PhaseRef f = phase_or_empty(pb, c.wg, p, c.P);
-    float* sums = (float*)(act + kPhB * 512);
-    {   // stage this phase's activation piece (thread tid = piece q of the phase)
-        const uint4 x = xv;
-        const uint32_t ones = 0x3F803F80u;
-        float sm = 0.f;
-        sm = dot2(x.x, ones, sm);
-        sm = dot2(x.y, ones, sm);
-        sm = dot2(x.z, ones, sm);
-        sm = dot2(x.w, ones, sm);
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
-        const int q = c.tid;
-        const int bb = q >> 5, gg = (q >> 3) & 3, t = q & 7;
-        *(u32x4_t*)(act + 16u * (uint32_t)((bb * 8 + t) * 4 + gg)) = act_perm(x);
-        if ((q & 3) == 0) sums[(bb * 4 + gg) * 2 + ((q >> 2) & 1)] = sm;
-    }
-    // this wave's loads of the phase have landed: loads complete in order and exactly the
-    // next two phases' 1 + kPhIpw loads each were issued after them
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * (1 + kPhIpw)));   // vmcnt(12)
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    __builtin_amdgcn_s_barrier();
-
-    // blocks w and w + 4 of the phase (both past the end contribute zero)
-    const int b0 = c.w, b1 = c.w + kPhWaves;
-    const uint8_t* ws = wslot + c.rowb;
-    StepIn i0, i1;
-    step_reads(lds_addr(ws + 16 * ((9 * b0) ^ c.sw)), lds_addr(ws + 16 * ((9 * b0 + 1 + 2 * c.g) ^ c.sw)),
-               lds_addr(ws + 16 * ((9 * b0 + 2 + 2 * c.g) ^ c.sw)), lds_addr(sums + (b0 * 4 + c.g) * 2), i0);
-    step_reads(lds_addr(ws + 16 * ((9 * b1) ^ c.sw)), lds_addr(ws + 16 * ((9 * b1 + 1 + 2 * c.g) ^ c.sw)),
-               lds_addr(ws + 16 * ((9 * b1 + 2 + 2 * c.g) ^ c.sw)), lds_addr(sums + (b1 * 4 + c.g) * 2), i1);
-    a_reads(A, lds_addr(act + (uint32_t)b0 * 512u + 16u * (uint32_t)c.g), diag_mask(1));
-    a_reads(B, lds_addr(act + (uint32_t)b1 * 512u + 16u * (uint32_t)c.g), diag_mask(1));
-    lds_wait(i0, i1, A, B);
-    const float v0 = block_dot(i0, A, c);
-    const float v1 = block_dot(i1, B, c);
-    acc += (b0 < f.nb ? v0 : 0.f) + (b1 < f.nb ? v1 : 0.f);
-
-    if (f.last && p < c.P) {   // flush this tile's partial sums (reduced over the four K-groups)
-        float a = acc;
-        a += __shfl_xor(a, 16, 64);
-        a += __shfl_xor(a, 32, 64);
-        if (c.lane < kTR) red[(f.tile * kPhWaves + c.w) * kTR + c.lane] = a;
-        acc = 0.f;
-    }
-    // refill this slot with phase p + kRing once every wave is done with it (always issued,
-    // empty past the last phase)
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    __builtin_amdgcn_s_barrier();
-    xv = phase_issue(phase_or_empty(pb, c.wg, p + kRing, c.P), c.xr, c.xstride, c.tid, c.w, c.lane, c.rb, wslot);
-}
-
-template <class Prob>
-__global__ __launch_bounds__(kPhWaves * 64) void k_phase(Prob pb0, const uint16_t* __restrict__ X, int64_t xstride,
-                                                        uint32_t xbytes, int nsb) {
-    __shared__ __align__(16) uint8_t s_w0[kPhaseW + 2048];   // + tail for the spare loads
-    __shared__ __align__(16) uint8_t s_w1[kPhaseW + 2048];
-    __shared__ __align__(16) uint8_t s_w2[kPhaseW + 2048];
-    __shared__ __align__(16) uint8_t s_a0[kPhB * 544];
-    __shared__ __align__(16) uint8_t s_a1[kPhB * 544];
-    __shared__ __align__(16) uint8_t s_a2[kPhB * 544];
-    __shared__ float s_red[kMaxTiles * kPhWaves * kTR];   // [tile][wave][row]
-    Prob pb = pb0;
-    pb.setup(blockIdx.x);   // routed expert ids, read once before any weight load is issued
-    PhaseCtx c;
-    c.tid = threadIdx.x;
-    c.lane = c.tid & 63;
-    c.w = __builtin_amdgcn_readfirstlane(c.tid >> 6);
-    c.wg = blockIdx.x;
-    c.rb = (int64_t)nsb * 144;
-    c.xstride = xstride;
-    c.P = pb.nphase();
-    c.xr = buf_rsrc(X, xbytes);
-    c.n = c.lane & 15;
-    c.g = c.lane >> 4;
-    c.sw = (c.n >> 1) & 7;
-    c.rowb = 16u * (uint32_t)(72 * c.n);
-    c.hs = hdr_sel(c.g);
-    c.ck = code_k();
-
-    // issue the first kRing phases (phases past the end load nothing)
-    uint4 x0 = phase_issue(phase_or_empty(pb, c.wg, 0, c.P), c.xr, xstride, c.tid, c.w, c.lane, c.rb, s_w0);
-    uint4 x1 = phase_issue(phase_or_empty(pb, c.wg, 1, c.P), c.xr, xstride, c.tid, c.w, c.lane, c.rb, s_w1);
-    uint4 x2 = phase_issue(phase_or_empty(pb, c.wg, 2, c.P), c.xr, xstride, c.tid, c.w, c.lane, c.rb, s_w2);
-
-    float acc = 0.f;
-    u32x4_t A[8], B[8];   // block-diagonal activation operands: off-diagonal lanes stay zero
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        A[t] = u32x4_t{0u, 0u, 0u, 0u};
-        B[t] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-    // all three ring steps run every round (a step past the last phase is empty), so the
-    // outstanding-load count is the same at every iteration and the waits stay static
-    for (int p = 0; p < c.P; p += kRing) {
-        phase_step(pb, c, p, x0, s_w0, s_a0, s_red, acc, A, B);
-        phase_step(pb, c, p + 1, x1, s_w1, s_a1, s_red, acc, A, B);
-        phase_step(pb, c, p + 2, x2, s_w2, s_a2, s_red, acc, A, B);
-    }
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    __builtin_amdgcn_s_barrier();
-    pb.finish(c.wg, s_red, c.tid);
-}
-
-template <class Prob>
-hipError_t run_phase(const Prob& pb, unsigned nwg, const uint16_t* X, int64_t xstride, int64_t xbytes, int nsb,
-                     hipStream_t st) {
-    hipLaunchKernelGGL((k_phase<Prob>), dim3(nwg), dim3(kPhWaves * 64), 0, st, pb, X, xstride, (uint32_t)xbytes,
-                       nsb);
-    return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ planning
@@ -1024,18 +684,24 @@ hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t*
     return hipSuccess;
 }
 
+bool moe_route_in_kernel(int64_t E, int topk) {
+    return E >= 1 && E <= kRouteMaxE && topk >= 1 && topk <= kRouteMaxTopk && topk <= E;
+}
+
 hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
-                                  const int32_t* sel, int topk, int nslots, int64_t E, int64_t H, int64_t I,
+                                  const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
                                   const uint16_t* x, uint16_t* h, hipStream_t st) {
     const int nsb = (int)(H / QK_K);
     if (I % kTR != 0) return hipErrorInvalidValue;
+    if (route.logits && !moe_route_in_kernel(E, topk)) return hipErrorInvalidValue;
     const int64_t rb = row_bytes(T_Q4_K, H);
-    const ProbGateUp pb{G, U, shG, shU, sel, topk, (int)E, (int)(I / kTR), rb, rb * I, h, I};
+    const ProbGateUp pb{G, U, shG, shU, route, topk, (int)E, (int)(I / kTR), rb, rb * I, h, I, 0};
     const unsigned nwg = (unsigned)(nslots * (I / kTR));
     Plan1 p1;
-    if (make_plan1(nsb, 2, 4, p1)) return run1(pb, p1, nwg, x, 0, H * 2, (int)H, st);
+    if (make_plan1(nsb, 2, 4, p1) && p1.W * 64 >= (route.logits ? (int)((E + 7) & ~7) : 0))
+        return run1(pb, p1, nwg, x, 0, H * 2, (int)H, st);
     Plan pl;
-    if (!make_plan(nsb, 2, 1, 1, 4, pl)) return hipErrorInvalidValue;
+    if (!make_plan(nsb, 2, 1, 1, 4, pl) || pl.W * 64 < (route.logits ? (int)((E + 7) & ~7) : 0)) return hipErrorInvalidValue;
     return run_mfma<1>(pb, pl, nwg, x, 0, H * 2, (int)H, 1, st);
 }
 

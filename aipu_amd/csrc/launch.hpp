@@ -19,13 +19,13 @@ hipError_t launch_rsqrt(const float* x, int64_t n, float* y, hipStream_t st);
 hipError_t launch_stream_read(const void* p, int64_t bytes, uint32_t* sink, hipStream_t st);
 
 // router.hip
-hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t scale_bits,
-                              int32_t* sel_idx, uint16_t* sel_w, uint16_t* gates, hipStream_t st);
-// bf16 router GEMV + tail in one launch; `counter` is a workspace word that must be 0 on
-// entry (the kernel leaves it 0).  sel2/selw2 (nullable) receive a copy of the routing.
-hipError_t launch_router_bf16_fused(const uint16_t* W, const uint16_t* x, int64_t K, int E, int topk,
-                                    uint32_t scale_bits, uint16_t* logits, uint32_t* counter, int32_t* sel,
-                                    uint16_t* selw, int32_t* sel2, uint16_t* selw2, hipStream_t st);
+// Router tail (one wave): routing of E bf16 logits; sel2/selw2 (nullable) receive a copy.
+hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t scale_bits, int32_t* sel_idx,
+                              uint16_t* sel_w, uint16_t* gates, hipStream_t st, int32_t* sel2 = nullptr,
+                              uint16_t* selw2 = nullptr);
+// bf16 router GEMV: logits[e] = bf16(W[e] . x), one workgroup per expert.
+hipError_t launch_router_bf16_logits(const uint16_t* W, const uint16_t* x, int64_t K, int E, uint16_t* logits,
+                                     hipStream_t st);
 
 // gemv_ref.hip -- bit-exact reference order
 hipError_t launch_gemv_ref(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
@@ -50,8 +50,21 @@ bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M);
 hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
                             float* y_f32, int64_t ystride, hipStream_t st);
 bool moe_mfma_supported(int nslots, int64_t H, int64_t I);
+// Routing source of the gate/up leg: either `sel` (expert ids already decided) or, when
+// `logits` is set, the kernel routes from the logits itself and workgroup 0 publishes the
+// decision to sel_pub/selw_pub (and the optional API copies sel_api/selw_api).
+struct MoeRoute {
+    const int32_t* sel;
+    const uint16_t* logits;
+    uint32_t scale_bits;
+    int32_t* sel_pub;
+    uint16_t* selw_pub;
+    int32_t* sel_api;
+    uint16_t* selw_api;
+};
+bool moe_route_in_kernel(int64_t E, int topk);
 hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
-                                  const int32_t* sel, int topk, int nslots, int64_t E, int64_t H, int64_t I,
+                                  const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
                                   const uint16_t* x, uint16_t* h, hipStream_t st);
 hipError_t launch_moe_down_mfma(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
                                 int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h, uint16_t* y,

@@ -73,15 +73,6 @@ __global__ void k_combine(const uint16_t* __restrict__ ys, const uint16_t* __res
     }
 }
 
-__global__ void k_copy_sel(const int32_t* __restrict__ sel, const uint16_t* __restrict__ selw, int topk,
-                           int32_t* __restrict__ sel_out, uint16_t* __restrict__ selw_out) {
-    const int i = threadIdx.x;
-    if (i < topk) {
-        if (sel_out) sel_out[i] = sel[i];
-        if (selw_out) selw_out[i] = selw[i];
-    }
-}
-
 inline int blocks_for(int64_t n) {
     int64_t b = (n + 255) / 256;
     return (int)(b < 1 ? 1 : (b > 4096 ? 4096 : b));
@@ -108,24 +99,28 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
     const int nslots = a.topk + (has_shared ? 1 : 0);
     const bool fast = a.mode == AIPU_MODE_FAST && a.type == T_Q4_K;
 
-    // 1-2. router logits (bf16) and router tail
-    if (a.mode == AIPU_MODE_FAST && a.router_type == T_BF16) {
-        AIPU_TRY(launch_router_bf16_fused((const uint16_t*)a.router_w, a.x, a.H, (int)a.E, a.topk, a.scale_bits,
-                                          logits, (uint32_t*)(ws + L.counter), sel, selw, a.sel_idx_out,
-                                          a.sel_w_out, st));
-    } else {
-        if (a.mode == AIPU_MODE_FAST && a.router_type == T_Q4_K)
-            AIPU_TRY(launch_gemv_fast(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
-        else
-            AIPU_TRY(launch_gemv_ref(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
-        AIPU_TRY(launch_router_tail(logits, (int)a.E, a.topk, a.scale_bits, sel, selw, nullptr, st));
-        if (a.sel_idx_out || a.sel_w_out) {
-            hipLaunchKernelGGL(k_copy_sel, dim3(1), dim3(64), 0, st, sel, selw, a.topk, a.sel_idx_out, a.sel_w_out);
-            AIPU_TRY(hipGetLastError());
-        }
+    // 1. router logits
+    if (a.mode == AIPU_MODE_FAST && a.router_type == T_BF16)
+        AIPU_TRY(launch_router_bf16_logits((const uint16_t*)a.router_w, a.x, a.H, (int)a.E, logits, st));
+    else if (a.mode == AIPU_MODE_FAST && a.router_type == T_Q4_K)
+        AIPU_TRY(launch_gemv_fast(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
+    else
+        AIPU_TRY(launch_gemv_ref(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
+
+    // 2-3. fast path: the gate/up kernel routes from the logits in every workgroup and
+    // publishes the decision for the down kernel (no separate router-tail launch)
+    if (fast && moe_mfma_supported(nslots, a.H, a.I) && moe_route_in_kernel(a.E, a.topk)) {
+        const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};
+        AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
+                                        a.I, a.x, h, st));
+        return launch_moe_down_mfma(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y, 0, st);
     }
+    // 2. router tail (one wave), then the experts
+    AIPU_TRY(launch_router_tail(logits, (int)a.E, a.topk, a.scale_bits, sel, selw, nullptr, st, a.sel_idx_out,
+                                a.sel_w_out));
     if (fast && moe_mfma_supported(nslots, a.H, a.I)) {
-        AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, sel, a.topk, nslots, a.E, a.H,
+        const MoeRoute route{sel, nullptr, 0u, nullptr, nullptr, nullptr, nullptr};
+        AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
                                         a.I, a.x, h, st));
         return launch_moe_down_mfma(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y, 0, st);
     }
@@ -168,7 +163,8 @@ hipError_t launch_swiglu_expert(int type, const void* wg, const void* wu, const 
         // (ignored) expert id, so they get the workspace's id slot rather than a null pointer.
         const int32_t* no_sel = (const int32_t*)(ws + L.sel);
         if (moe_mfma_supported(1, H, I)) {
-            AIPU_TRY(launch_moe_gateup_mfma(G, U, G, U, no_sel, 0, 1, 1, H, I, x, h, st));
+            const MoeRoute route{no_sel, nullptr, 0u, nullptr, nullptr, nullptr, nullptr};
+            AIPU_TRY(launch_moe_gateup_mfma(G, U, G, U, route, 0, 1, 1, H, I, x, h, st));
             return launch_moe_down_mfma(D, D, no_sel, nullptr, 0, 1, 1, H, I, h, y, 1, st);
         }
         AIPU_TRY(launch_moe_gateup_fast(G, U, G, U, no_sel, 0, 1, 1, H, I, x, h, st));

@@ -1,0 +1,97 @@
+// MoE routing decision shared by the router tail kernel and the in-kernel routing of the
+// gate/up leg (tools/glm_model_q4k_ref.py:663-699):
+//   gate = glm_sigmoid(logit) (bf16); experts ordered by (fp32 order key of the gate,
+//   descending; expert index, ascending); the first topk win; s = balanced +0-padded fp32
+//   add tree over the winners' gates in slot order; rs = f32(f32(rsqrt(s)^2) * SCALE);
+//   sel_w = bf16(gate * rs).
+// Because the gates are bf16, the fp32 order key of a gate is the 16-bit order key of its
+// bf16 pattern followed by 16 zero bits, so one 32-bit key (key16 << 16 | 0xFFFF - e)
+// orders experts exactly as the reference's (key, -e) sort, ties included, and all keys
+// are distinct.
+#pragma once
+
+#include "common.hpp"
+#include "glm_act.hpp"
+
+namespace aipu {
+
+constexpr int kRouteMaxE = 512;    // in-kernel routing (one key per thread, rank by counting)
+constexpr int kRouteMaxTopk = 32;
+
+__device__ __forceinline__ uint32_t bf16_order_key(uint32_t b) {
+    return (b & 0x8000u) ? (~b & 0xFFFFu) : (b ^ 0x8000u);
+}
+
+__device__ __forceinline__ uint32_t key_to_bf16(uint32_t k16) {
+    return (k16 & 0x8000u) ? (k16 ^ 0x8000u) : (~k16 & 0xFFFFu);
+}
+
+__device__ __forceinline__ uint32_t route_key(uint32_t logit_bits, int e) {
+    return (bf16_order_key(glm_sigmoid_bf16(logit_bits)) << 16) | (0xFFFFu - (uint32_t)e);
+}
+
+// Slot weights from the winners' keys in slot order (one thread): the balanced fp32 add
+// tree over the gates (padded with +0 to a power of two >= 2), rs = rsqrt(s)^2 * scale.
+// The tree is written with compile-time trip counts so the nodes stay in registers.
+__device__ __forceinline__ void route_weights(const uint32_t* win, int topk, uint32_t scale_bits, int32_t* sel,
+                                              uint16_t* selw) {
+    float node[kRouteMaxTopk];
+#pragma unroll
+    for (int i = 0; i < kRouteMaxTopk; ++i) node[i] = i < topk ? bf16_to_f32(key_to_bf16(win[i] >> 16)) : 0.0f;
+    int npow = 2;
+    while (npow < topk) npow <<= 1;
+#pragma unroll
+    for (int n = kRouteMaxTopk; n > 1; n >>= 1) {
+        if (n <= npow) {
+#pragma unroll
+            for (int i = 0; i < n / 2; ++i) node[i] = node[2 * i] + node[2 * i + 1];
+        }
+    }
+    const float rr = glm_rsqrt(node[0]);
+    const float rr2 = rr * rr;
+    const float rs = rr2 * __uint_as_float(scale_bits);
+    for (int i = 0; i < topk; ++i) {
+        const float g = bf16_to_f32(key_to_bf16(win[i] >> 16));
+        sel[i] = (int32_t)(0xFFFFu - (win[i] & 0xFFFFu));
+        selw[i] = (uint16_t)bf16_rne(g * rs);
+    }
+}
+
+// The routing decision computed by one workgroup (all threads call it; E <= kRouteMaxE and
+// E rounded up to 8 <= the thread count, topk <= kRouteMaxTopk; keys holds >= that many).  An expert's rank is the number of larger
+// keys (all keys are distinct), so the top-k need no sort; with at least 2E threads two
+// threads count one key's rank over half the keys each.  Afterwards win[0..topk) holds the
+// winners' keys in slot order; with `weights`, sel / selw (LDS) are filled too.
+__device__ __forceinline__ void route_workgroup(const uint16_t* logits, int E, int topk, uint32_t scale_bits,
+                                                uint32_t* keys, uint32_t* win, int32_t* sel, uint16_t* selw,
+                                                bool weights) {
+    const int t = threadIdx.x, nthr = blockDim.x;
+    if (t < E) keys[t] = route_key(logits[t], t);
+    else if (t < ((E + 7) & ~7)) keys[t] = 0u;
+    __syncthreads();
+    const bool two = 2 * E <= nthr;
+    const int k = two ? t >> 1 : t;
+    if (k < E) {
+        const uint32_t my = keys[k];
+        // keys are padded with zeros to a multiple of 8 (zero is below every key), so each
+        // half is a whole number of 16-B reads; the reads are unrolled so that they overlap
+        const int e8 = (E + 7) & ~7;
+        const int half = two ? e8 / 2 : e8;
+        const uint4* kp = (const uint4*)(keys + (two ? (t & 1) * half : 0));
+        int rank = 0;
+#pragma unroll 8
+        for (int j = 0; j < half / 4; ++j) {
+            const uint4 k4 = kp[j];
+            rank += (k4.x > my) + (k4.y > my) + (k4.z > my) + (k4.w > my);
+        }
+        if (two) rank += __shfl_xor(rank, 1, 64);
+        if (rank < topk && (!two || (t & 1) == 0)) win[rank] = my;
+    }
+    __syncthreads();
+    if (weights) {
+        if (t == 0) route_weights(win, topk, scale_bits, sel, selw);
+        __syncthreads();
+    }
+}
+
+}  // namespace aipu
