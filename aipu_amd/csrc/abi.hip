@@ -78,9 +78,13 @@ int check_gemv(int type, const void* w, int64_t N, int64_t K, const void* x, int
     return AIPU_OK;
 }
 
-// Fast streaming kernels exist for Q4_K and bf16 weights; the other types are served by
-// the exact kernel (whose results trivially satisfy the fast-mode tolerance).
-bool has_fast(int type) { return type == aipu::T_Q4_K || type == aipu::T_BF16; }
+// Fast kernels exist for every type: Q4_K on the matrix cores, bf16 in the streaming
+// kernel, Q6_K / Q8_0 / F16 in the mixed-type kernel (K up to its staging limit; larger K
+// is served by the exact kernel, whose results trivially satisfy the fast-mode tolerance).
+bool has_fast(int type, int64_t K) {
+    if (type == aipu::T_Q4_K || type == aipu::T_BF16) return true;
+    return aipu::gemv_mixed_supported(type, K);
+}
 
 }  // namespace
 
@@ -131,7 +135,7 @@ int aipu_gemv(int ggml_type, const void* w, int64_t N, int64_t K, const uint16_t
               float* y_f32, int mode, void* stream) {
     int rc = check_gemv(ggml_type, w, N, K, x, M, y, y_f32, mode);
     if (rc) return rc;
-    if (mode == AIPU_MODE_FAST && has_fast(ggml_type))
+    if (mode == AIPU_MODE_FAST && has_fast(ggml_type, K))
         return hip_status(aipu::launch_gemv_fast(ggml_type, w, N, K, x, M, y, y_f32, S(stream)), "aipu_gemv");
     return hip_status(aipu::launch_gemv_ref(ggml_type, w, N, K, x, M, y, y_f32, S(stream)), "aipu_gemv");
 }

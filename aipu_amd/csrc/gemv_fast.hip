@@ -713,6 +713,18 @@ hipError_t launch_gemv_fast(int type, const void* w, int64_t N, int64_t K, const
             if (gemv_mfma_supported(N, K, M)) return launch_gemv_mfma(w, N, K, x, M, y, y_f32, N, st);
             return gemv_stream_mc<T_Q4_K, 4>((const uint8_t*)w, N, K, x, M, y, y_f32, st);
         case T_BF16: return gemv_stream_mc<T_BF16, 2>((const uint8_t*)w, N, K, x, M, y, y_f32, st);
+        case T_Q6_K:
+        case T_Q8_0:
+        case T_F16: {
+            // one tile covering all N rows, one launch per activation row
+            if (!gemv_mixed_supported(type, K)) return hipErrorInvalidValue;
+            const aipu_tile_desc d{type, 0, w, 0, N};
+            for (int64_t m = 0; m < M; ++m) {
+                const hipError_t e = launch_gemv_mixed(&d, 1, K, x + m * K, y + m * N, y_f32 ? y_f32 + m * N : nullptr, st);
+                if (e != hipSuccess) return e;
+            }
+            return hipSuccess;
+        }
         default: return hipErrorInvalidValue;
     }
 }

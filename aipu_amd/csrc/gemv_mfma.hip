@@ -349,46 +349,6 @@ __global__ __launch_bounds__(kMaxW * 64) void k_mfma_gemv(Prob pb0, const uint16
     pb.finish(wg, red, KP, tid);
 }
 
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// The 8 activation operands of a block, read on the lanes in `mask` only (the diagonal
-// lanes of the block-diagonal A); every other lane keeps its register contents, which stay
-// zero for the whole kernel.  This moves 64 B per read instead of a 1 KB broadcast of zeros.
-__device__ __forceinline__ void a_reads(u32x4_t (&A)[8], uint32_t aa, uint64_t mask) {
-    uint64_t saved;
-    asm volatile(
-        "s_mov_b64 %8, exec\n\t"
-        "s_and_b64 exec, exec, %10\n\t"
-        "ds_read_b128 %0, %9\n\t"
-        "ds_read_b128 %1, %9 offset:64\n\t"
-        "ds_read_b128 %2, %9 offset:128\n\t"
-        "ds_read_b128 %3, %9 offset:192\n\t"
-        "ds_read_b128 %4, %9 offset:256\n\t"
-        "ds_read_b128 %5, %9 offset:320\n\t"
-        "ds_read_b128 %6, %9 offset:384\n\t"
-        "ds_read_b128 %7, %9 offset:448\n\t"
-        "s_mov_b64 exec, %8"
-        : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]),
-          "=&s"(saved)
-        : "v"(aa), "s"(mask));
-}
-
-// Wait for the reads above; the operands are tied so that no use moves above the wait.
-__device__ __forceinline__ void a_wait(u32x4_t (&A)[8]) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]));
-}
-
-// Diagonal lanes of the block-diagonal activation operand: lane 16g + 4g + m for m < MR.
-__host__ __device__ constexpr uint64_t diag_mask(int mr) {
-    uint64_t m = 0;
-    for (int g = 0; g < 4; ++g)
-        for (int r = 0; r < mr; ++r) m |= 1ull << (20 * g + r);
-    return m;
-}
-
 // ------------------------------------------------------- single-row kernel (M = 1)
 // Each wave is self-contained: it stages the activations of its own BPK = GS * NG blocks
 // and streams its 16 rows of weights group by group (GS blocks per group) into its own LDS
@@ -403,14 +363,6 @@ struct Dma {
     static constexpr int kInsts = (kPieces + 63) / 64;     // 64 lanes x 16 B per instruction
     static constexpr int kBytes = kInsts * 1024;           // LDS slice (the tail lanes write zeros)
 };
-
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t off) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, kNT);
-}
-
-// s_waitcnt immediates (gfx9 layout: vmcnt[3:0] expcnt[6:4] lgkmcnt[11:8] vmcnt_hi[15:14])
-constexpr int kWaitVm0 = 0x0F70;    // vmcnt(0)
-constexpr int kWaitLgkm0 = 0xC07F;  // lgkmcnt(0)
 
 template <int GS>
 __device__ __forceinline__ void dma_group(__amdgpu_buffer_rsrc_t wr, uint8_t* slice, int64_t rb, int blk0, int lane) {
@@ -519,20 +471,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
             a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
             a_wait(A);
             const float2 as = *(const float2*)(wS + (b * 4 + g) * 2);
-            dlo[0] = -kCodeBiasF * as.x;
-            dhi[0] = -kCodeBiasF * as.y;
-            const uint32_t qd[8] = {R[bb].q0.x, R[bb].q0.y, R[bb].q0.z, R[bb].q0.w,
-                                    R[bb].q1.x, R[bb].q1.y, R[bb].q1.z, R[bb].q1.w};
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                dlo = mfma(A[t], codes_lo(qd[2 * t], qd[2 * t + 1], ck), dlo);
-                dhi = mfma(A[4 + t], codes_hi(qd[2 * t], qd[2 * t + 1], ck), dhi);
-            }
-            const Hdr H = hdr_decode(R[bb].h, hs);
-            const float t1 = __builtin_fmaf(H.sc1, dhi[0], H.sc0 * dlo[0]);
-            const float v = __builtin_fmaf(H.m1, as.y, H.m0 * as.x);
-            acc = __builtin_fmaf(H.d, t1, acc);
-            acc = __builtin_fmaf(-H.dm, v, acc);
+            acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
         }
     }
 

@@ -45,6 +45,12 @@ hipError_t launch_gemv_fast(int type, const void* w, int64_t N, int64_t K, const
 hipError_t launch_gemv_tiles(const aipu_tile_desc* tiles, int n_tiles, int64_t N, int64_t K, const uint16_t* x,
                              int64_t M, uint16_t* y, float* y_f32, int mode, hipStream_t st);
 
+// gemv_mixed.hip -- one-launch GEMV over tiles of Q4_K / Q6_K / Q8_0 / F16 / BF16 rows
+// (tolerance mode, one activation row per launch)
+bool gemv_mixed_supported(int type, int64_t K);
+hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K, const uint16_t* x, uint16_t* y,
+                             float* y_f32, hipStream_t st);
+
 // gemv_mfma.hip -- matrix-core Q4_K GEMV (tolerance mode)
 bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M);
 hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,

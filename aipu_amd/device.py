@@ -119,9 +119,12 @@ def gemv_tiles(tiles, N, K, x, mode="fast", out=None, out_f32=False):
         _need_cuda(w)
         arr[i] = TileDesc(int(t), 0, w.data_ptr(), int(r0), int(nr))
     y = out if out is not None else torch.zeros((M, N), dtype=torch.bfloat16, device=x.device)
-    yf = torch.zeros((M, N), dtype=torch.float32, device=x.device) if out_f32 else None
+    if isinstance(out_f32, torch.Tensor):   # caller-provided fp32 output (rows outside tiles kept)
+        yf = out_f32
+    else:
+        yf = torch.zeros((M, N), dtype=torch.float32, device=x.device) if out_f32 else None
     call("aipu_gemv_tiles", arr, len(tiles), N, K, _ptr(x), M, _ptr(y), _ptr(yf), _mode(mode), _stream(x))
-    return (y, yf) if out_f32 else y
+    return (y, yf) if yf is not None else y
 
 
 def glm_silu(x):

@@ -401,7 +401,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of one HIP graph")
-    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1"], default=None,
                     help="run one measurement only (for kernel tracing / counter runs)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
                     help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into "
@@ -434,6 +434,15 @@ def main():
         return
     if args.only == "moe":
         print(json.dumps(bench_moe(dev, torch, args.moe_steps)))
+        return
+    if args.only == "tiles":
+        print(json.dumps(bench_tiles(dev, torch)))
+        return
+    if args.only == "prefill":
+        print(json.dumps(bench_prefill(dev, torch)))
+        return
+    if args.only == "c1":
+        print(json.dumps({f"m{M}": bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, label="C1") for M in (2, 4, 8)}))
         return
     if args.only == "stream":
         r = bench_stream_read(dev, torch)

@@ -174,6 +174,55 @@ def test_gemv_fast_tolerance(N, K, M):
     assert np.array_equal(u32(h_f32(yf2)), u32(h_f32(yf)))
 
 
+# Q6_K / Q8_0 / F16 through the mixed-type kernel: shapes where some waves own no blocks
+# (K = 256, 768), odd block counts (1280), the largest staged K (15360; larger K is served by
+# the exact kernel), ragged row counts and several activation rows.
+TYPE_FAST_CASES = [(256, 6144, 1), (37, 768, 1), (100, 256, 2), (300, 1280, 1), (64, 15360, 1), (513, 2048, 3)]
+
+
+@pytest.mark.parametrize("t", [qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16])
+@pytest.mark.parametrize("N,K,M", TYPE_FAST_CASES)
+def test_gemv_fast_types_tolerance(t, N, K, M):
+    note(f"gemv fast type={t} N={N} K={K} M={M}")
+    rng = np.random.default_rng(t * 1000 + N + K + M)
+    raw = qo.random_weights(rng, t, N, K)
+    x = qo.random_bf16(rng, (M, K))
+    wd = d_u8(raw)
+    y, yf = dev.gemv(t, wd, N, K, d_bf16(x), mode="fast", out_f32=True)
+    acc, _ = co.gemv_ref(t, raw, N, K, x)
+    w = qo.dequant_matrix(t, raw, N, K)
+    xf = qo.bf16_bits_to_f32(x)
+    ok, worst = qo.tolerance_gate(w, xf, h_f32(yf), rel=1e-5)
+    note(f"  worst |delta| = {worst:.4f} of the 1e-5*sum|a*w| bound")
+    assert ok, f"tolerance gate exceeded: worst {worst:.3f} of the 1e-5*sum|a*w| bound"
+    ok, max_ulp, n_cancelled = qo.bf16_parity(h_bits(y), acc, w, xf)
+    assert ok, f"bf16 outputs: {max_ulp} ulp on well-conditioned outputs ({n_cancelled} cancelled sums)"
+    y2, yf2 = dev.gemv(t, wd, N, K, d_bf16(x), mode="fast", out_f32=True)
+    assert np.array_equal(u32(h_f32(yf2)), u32(h_f32(yf)))
+
+
+@pytest.mark.parametrize("t", [qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16])
+def test_gemv_fast_types_detect_corruption(t):
+    """Must-fail twin per type: one changed weight in row 3 moves that output past the gate."""
+    note(f"gemv fast type={t} corruption twin")
+    rng = np.random.default_rng(40 + t)
+    N, K = 32, 1024
+    raw = qo.random_weights(rng, t, N, K)
+    x = qo.random_bf16(rng, (1, K))
+    w = qo.dequant_matrix(t, raw, N, K)
+    bad = raw.copy()
+    rb = raw.size // N
+    if t == qo.GGML_F16:
+        bad[3 * rb + 2 * 100:3 * rb + 2 * 100 + 2] = np.asarray(qo.f32_to_f16_bits(np.array([3.0], np.float32)), np.uint16).view(np.uint8)
+    elif t == qo.GGML_Q8_0:
+        bad[3 * rb + 2 + 7] ^= 0x40
+    else:
+        bad[3 * rb + 128 + 5] ^= 0x30          # qh bits of one position
+    _, yf = dev.gemv(t, d_u8(bad), N, K, d_bf16(x), mode="fast", out_f32=True)
+    ok, _ = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
+    assert not ok
+
+
 def test_gemv_fast_bf16_router_shape():
     note("gemv fast BF16 256x6144")
     rng = np.random.default_rng(11)

@@ -206,6 +206,52 @@ def test_mixed_tiles(mode):
         assert qo.bf16_parity(h_bits(y), acc, w, qo.bf16_bits_to_f32(x))[0]
 
 
+def test_mixed_tiles_c3_full_shape():
+    """BASELINE config 3 at its own size: K = N = 6144, 24 tiles of 256 rows, one launch."""
+    note("tiles fast C3 K=6144")
+    rng = np.random.default_rng(34)
+    K, rows = 6144, 256
+    types = [Q4K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16] * 6
+    raws = [qo.random_weights(rng, t, rows, K) for t in types]
+    tiles = [(t, d_u8(r), i * rows, rows) for i, (t, r) in enumerate(zip(types, raws))]
+    N = rows * len(types)
+    x = qo.random_bf16(rng, (1, K))
+    y, yf = dev.gemv_tiles(tiles, N, K, d_bf16(x), mode="fast", out_f32=True)
+    acc = np.concatenate([co.gemv_ref(t, r, rows, K, x)[0] for t, r in zip(types, raws)], axis=1)
+    w = np.concatenate([qo.dequant_matrix(t, r, rows, K) for t, r in zip(types, raws)])
+    ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
+    note(f"  worst |delta| = {worst:.4f} of the 1e-5*sum|a*w| bound")
+    assert ok, worst
+    assert qo.bf16_parity(h_bits(y), acc, w, qo.bf16_bits_to_f32(x))[0]
+
+
+def test_mixed_tiles_ragged_fast():
+    """Tiles of odd row counts, out of order, with uncovered rows that must stay untouched."""
+    note("tiles fast ragged")
+    rng = np.random.default_rng(35)
+    K = 1280
+    spec = [(qo.GGML_F16, 200, 37), (Q4K, 0, 16), (qo.GGML_Q6_K, 20, 100), (qo.GGML_Q8_0, 120, 1),
+            (qo.GGML_Q6_K, 121, 17), (Q4K, 250, 33)]
+    N = 300
+    raws = [qo.random_weights(rng, t, n, K) for t, _, n in spec]
+    tiles = [(t, d_u8(r), r0, n) for (t, r0, n), r in zip(spec, raws)]
+    x = qo.random_bf16(rng, (1, K))
+    y = torch.full((1, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    yf = torch.full((1, N), -3.0, dtype=torch.float32, device="cuda")
+    dev.gemv_tiles(tiles, N, K, d_bf16(x), mode="fast", out=y, out_f32=yf)
+    got_f, got_y = h_f32(yf)[0], h_bits(y)[0]
+    covered = np.zeros(N, bool)
+    for (t, r0, n), r in zip(spec, raws):
+        covered[r0:r0 + n] = True
+        w = qo.dequant_matrix(t, r, n, K)
+        acc, _ = co.gemv_ref(t, r, n, K, x)
+        ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), got_f[None, r0:r0 + n])
+        assert ok, (t, r0, n, worst)
+        assert qo.bf16_parity(got_y[None, r0:r0 + n], acc, w, qo.bf16_bits_to_f32(x))[0], (t, r0, n)
+    assert np.all(got_f[~covered] == np.float32(-3.0))
+    assert np.all(got_y[~covered] == qo.bf16_round_bits(np.float32(7.0)))
+
+
 # --------------------------------------------------- reference-interface mirrors
 def test_q4k_ref_mirror_selftest():
     """The reference's own self-test (tools/q4k_ref.py:150-182) run through the GPU mirror."""
