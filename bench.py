@@ -298,7 +298,7 @@ def cpu_baseline(budget_s=12.0):
 
 
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_gemv_q4k_6144.json")
-HEADLINE_KERNEL = "k_rows"
+HEADLINE_KERNEL = "k_gemv1"
 COPY_BYTES = 256 << 20
 
 
@@ -356,7 +356,7 @@ def summarize_traffic(fetch_dir, write_dir, out=TRAFFIC_JSON):
 
 
 def _short_kernel(name):
-    """`void aipu::(anonymous namespace)::k_rows<3, ...>(...)` -> `k_rows<3, ...>`."""
+    """`void aipu::(anonymous namespace)::k_gemv1<3, ...>(...)` -> `k_gemv1<3, ...>`."""
     n = name.split("(")[0] if not name.startswith("void ") else name[5:]
     n = n.replace("aipu::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
     depth, out = 0, ""
