@@ -21,8 +21,7 @@ TYPE_Q6_K = 14
 TYPE_BF16 = 30
 MODE_FAST = 0
 MODE_REF = 1
-PREFILL_EXACT3 = 0
-PREFILL_BF16X2 = 1
+PREFILL_CODES = 0
 MAX_TILES = 64
 
 STATUS = {
@@ -81,7 +80,8 @@ SIGNATURES = {
     "aipu_swiglu_expert": (_I, [_I, _P, _P, _P, _I64, _I64, _P, _P, _P, _I, _P, _I64, _P]),
     "aipu_moe_swiglu_decode": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _U32, _P, _P, _P,
                                     _P, _I, _P, _I64, _P]),
-    "aipu_gemm_prefill": (_I, [_I, _P, _I64, _I64, _P, _I64, _P, _I, _P]),
+    "aipu_gemm_prefill_workspace_bytes": (_I64, [_I64, _I64]),
+    "aipu_gemm_prefill": (_I, [_I, _P, _I64, _I64, _P, _I64, _P, _P, _I, _P, _I64, _P]),
     "aipu_stream_read": (_I, [_P, _I64, _P, _P]),
 }
 

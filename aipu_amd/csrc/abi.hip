@@ -274,14 +274,28 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
     return hip_status(aipu::launch_moe_decode(a, S(stream)), "aipu_moe_swiglu_decode");
 }
 
+int64_t aipu_gemm_prefill_workspace_bytes(int64_t M, int64_t K) {
+    if (M < 1 || K < aipu::QK_K || K % aipu::QK_K || M > (1LL << 31) || K > (1LL << 31)) return -1;
+    return aipu::prefill_workspace_bytes(M, K);
+}
+
 int aipu_gemm_prefill(int ggml_type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
-                      int precision, void* stream) {
+                      float* y_f32, int precision, void* workspace, int64_t ws_bytes, void* stream) {
     if (ggml_type != aipu::T_Q4_K) return fail(AIPU_ERR_TYPE, "prefill supports Q4_K weights");
-    int rc = check_gemv(ggml_type, w, N, K, x, M, y, nullptr, AIPU_MODE_FAST);
+    int rc = check_gemv(ggml_type, w, N, K, x, M, y, y_f32, AIPU_MODE_FAST);
     if (rc) return rc;
-    if (precision != AIPU_PREFILL_EXACT3 && precision != AIPU_PREFILL_BF16X2)
-        return fail(AIPU_ERR_ARG, "unknown prefill precision %d", precision);
-    return hip_status(aipu::launch_gemm_prefill(ggml_type, w, N, K, x, M, y, precision, S(stream)),
+    if (precision != AIPU_PREFILL_CODES) return fail(AIPU_ERR_ARG, "unknown prefill precision %d", precision);
+    if (!aligned(x, 16)) return fail(AIPU_ERR_ALIGN, "x must be 16-byte aligned");
+    if (M > (1LL << 24) || N > (1LL << 31) || K > (1LL << 24))
+        return fail(AIPU_ERR_SHAPE, "prefill shape out of range (M %lld, N %lld, K %lld)", (long long)M, (long long)N,
+                    (long long)K);
+    if (64 * (K / aipu::QK_K) * 144 >= (1LL << 32)) return fail(AIPU_ERR_SHAPE, "K too large for prefill");
+    const int64_t need = aipu::prefill_workspace_bytes(M, K);
+    if (!workspace || ws_bytes < need)
+        return fail(AIPU_ERR_WORKSPACE, "prefill workspace of %lld bytes needed, %lld given", (long long)need,
+                    (long long)ws_bytes);
+    if (!aligned(workspace, 256)) return fail(AIPU_ERR_ALIGN, "workspace must be 256-byte aligned");
+    return hip_status(aipu::launch_gemm_prefill(ggml_type, w, N, K, x, M, y, y_f32, precision, workspace, S(stream)),
                       "aipu_gemm_prefill");
 }
 

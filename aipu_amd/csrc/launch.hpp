@@ -103,9 +103,10 @@ hipError_t launch_swiglu_expert(int type, const void* wg, const void* wu, const 
                                 const uint16_t* x, uint16_t* y, uint16_t* h_out, int mode, void* ws,
                                 hipStream_t st);
 
-// prefill.hip
+// prefill.hip -- matrix-core prefill GEMM (tolerance mode); ws holds prefill_workspace_bytes(M, K)
+int64_t prefill_workspace_bytes(int64_t M, int64_t K);
 hipError_t launch_gemm_prefill(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
-                               uint16_t* y, int precision, hipStream_t st);
+                               uint16_t* y, float* y_f32, int precision, void* ws, hipStream_t st);
 
 int device_cu_count();
 

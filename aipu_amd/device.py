@@ -200,14 +200,27 @@ def moe_swiglu_decode(router_type, router_w, ggml_type, gate_exps, up_exps, down
     return y, sel, sw
 
 
-def gemm_prefill(ggml_type, w, N, K, x, precision=_lib.PREFILL_EXACT3, out=None):
-    """Prefill GEMM y[M,N] = bf16(x[M,K] . dequant(w)^T) (tolerance mode)."""
+def prefill_workspace(M, K, device):
+    """A workspace for gemm_prefill(M rows, K): reusable across calls of the same or smaller M."""
+    n = _lib.lib().aipu_gemm_prefill_workspace_bytes(M, K)
+    if n < 0:
+        raise ValueError(f"no prefill workspace for M={M}, K={K}")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def gemm_prefill(ggml_type, w, N, K, x, precision=_lib.PREFILL_CODES, out=None, workspace=None, out_f32=False):
+    """Prefill GEMM y[M,N] = bf16(x[M,K] . dequant(w)^T) on the matrix cores (tolerance mode).
+
+    With out_f32=True also returns the fp32 accumulators: (y, y_f32)."""
     _need_cuda(w, x)
     x = _bf16(x)
     M = x.shape[0]
     y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    call("aipu_gemm_prefill", ggml_type, _ptr(w), N, K, _ptr(x), M, _ptr(y), precision, _stream(x))
-    return y
+    yf = torch.empty((M, N), dtype=torch.float32, device=x.device) if out_f32 else None
+    ws = workspace if workspace is not None else prefill_workspace(M, K, x.device)
+    call("aipu_gemm_prefill", ggml_type, _ptr(w), N, K, _ptr(x), M, _ptr(y), _ptr(yf), precision, _ptr(ws),
+         ws.numel(), _stream(x))
+    return (y, yf) if out_f32 else y
 
 
 def stream_read(buf, sink):

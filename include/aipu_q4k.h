@@ -151,17 +151,22 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
                            int32_t* sel_idx, uint16_t* sel_w, int mode, void* workspace,
                            int64_t ws_bytes, void* stream);
 
-/* Prefill GEMM for large M on the matrix cores: y[M][N] = bf16(x[M][K] . dequant(w)^T).
- * precision: AIPU_PREFILL_EXACT3 splits each exact fp32 weight into three bf16 terms
- * (w = hi + mid + lo exactly) and runs bf16 MFMA (fp32 accumulate); AIPU_PREFILL_BF16X2
- * keeps two terms (|w - hi - mid| <= 2^-16 |w|).  Both are tolerance-mode paths (the
- * summation order differs from the reference); use aipu_gemv(..., AIPU_MODE_REF) for the
- * bit-exact order.  Types: Q4_K.  No counterpart in the reference beyond M independent
- * matmul_q4k_col rows (tools/q4k_ref.py:86-92). */
-#define AIPU_PREFILL_EXACT3 0
-#define AIPU_PREFILL_BF16X2 1
+/* Prefill GEMM for large M on the matrix cores: y[M][N] = bf16(x[M][K] . dequant(w)^T),
+ * tolerance mode (|acc - exact| <= 1e-5 * sum|a*w|; the summation order differs from the
+ * reference, use aipu_gemv(..., AIPU_MODE_REF) for the bit-exact order).  Types: Q4_K.
+ * y_f32 (nullable) receives the fp32 accumulators [M][N].
+ * precision must be AIPU_PREFILL_CODES: the products a * (sc*q) run on fp16 matrix-core
+ * instructions with exact integer codes sc*q and each activation row scaled by a power of
+ * two into fp16 range, the min term on bf16 instructions with exactly split sub-block sums,
+ * and d / dmin are applied in fp32 per super-block.  workspace: caller-owned device memory
+ * of at least aipu_gemm_prefill_workspace_bytes(M, K) bytes, 256-B aligned (any contents;
+ * it holds the staged activations).  x must be 16-B aligned.  No counterpart in the
+ * reference beyond M independent matmul_q4k_col rows (tools/q4k_ref.py:86-92). */
+#define AIPU_PREFILL_CODES 0
+int64_t aipu_gemm_prefill_workspace_bytes(int64_t M, int64_t K);
 int aipu_gemm_prefill(int ggml_type, const void* w, int64_t N, int64_t K, const uint16_t* x,
-                      int64_t M, uint16_t* y, int precision, void* stream);
+                      int64_t M, uint16_t* y, float* y_f32, int precision, void* workspace,
+                      int64_t ws_bytes, void* stream);
 
 /* Measurement utility with no counterpart in the reference: streams `bytes` (a multiple of
  * 16) from `p` with the same 16-B global loads the GEMV kernels use and folds them into

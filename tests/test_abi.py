@@ -123,8 +123,18 @@ def test_moe_validation():
 
 def test_prefill_validation():
     f = L().aipu_gemm_prefill
-    assert f(14, FAKE, 64, 256, FAKE, 512, FAKE, 0, S) == TYPE
-    assert f(12, FAKE, 64, 256, FAKE, 512, FAKE, 9, S) == ARG
+    wsb = L().aipu_gemm_prefill_workspace_bytes
+    need = wsb(512, 256)
+    assert need == 4 * 1 * 73728 + 512 * 4          # one 72 KB chunk per 128-row tile and super-block
+    assert wsb(513, 6144) == 5 * 24 * 73728 + 640 * 4
+    assert wsb(0, 256) < 0 and wsb(4, 100) < 0
+    assert f(14, FAKE, 64, 256, FAKE, 512, FAKE, NULL, 0, FAKE, need, S) == TYPE
+    assert f(12, FAKE, 64, 256, FAKE, 512, FAKE, NULL, 9, FAKE, need, S) == ARG
+    assert f(12, FAKE, 64, 300, FAKE, 512, FAKE, NULL, 0, FAKE, need, S) == SHAPE
+    assert f(12, FAKE, 64, 256, FAKE, 512, FAKE, NULL, 0, FAKE, need - 1, S) == WS
+    assert f(12, FAKE, 64, 256, FAKE, 512, FAKE, NULL, 0, NULL, need, S) == WS
+    assert f(12, FAKE, 64, 256, ctypes.c_void_p(0x100002), 512, FAKE, NULL, 0, FAKE, need, S) == ALIGN
+    assert f(12, FAKE, 64, 256, FAKE, 512, FAKE, NULL, 0, ctypes.c_void_p(0x100010), need, S) == ALIGN
 
 
 def test_python_api_rejects_host_tensors():
