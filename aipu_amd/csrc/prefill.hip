@@ -35,12 +35,13 @@
 // v_pk_fma_f16 with (sc, sc) and (-1024 sc, -1024 sc) leaves sc*q exactly; for the high
 // nibbles (v & 0x00F000F0) | 0x64006400 = 1024 + 16q goes with (sc/16) and -64 sc.
 //
-// Tiles.  Workgroup = 4 waves (one per SIMD, up to 512 registers each) over a 128 x 256
-// (M x N) output tile; wave w owns weight rows 64w..64w+63 of it (4 subtiles of 16) and all
-// 128 activation rows (8 subtiles): 32 accumulator tiles, plus 32 per-super-block tiles.
-// The activation chunk of super-block b+1 is copied into the other LDS stage and the
-// wave's weight blocks of b+1 are loaded into the other register set while b computes.
-// Workgroups sharing a weight tile are consecutive on one XCD (its L2 serves the re-reads).
+// Tiles.  Workgroup = 8 waves (two per SIMD) over a 128 x 256 (M x N) output tile; wave w
+// owns all 128 activation rows (8 subtiles of 16) and weight rows 32w..32w+31 (2 subtiles):
+// 16 accumulator tiles plus 16 per-super-block tiles, and each weight operand is built once
+// per workgroup.  The two halves of a super-block's activation chunk and the weight blocks
+// of the next super-block are copied into LDS while the current half computes; the barriers
+// wait only for the copies a phase needs.  Workgroups sharing a weight tile are consecutive
+// on one XCD (its L2 serves the re-reads).
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -50,14 +51,16 @@ namespace {
 
 constexpr int kBM = 128;                         // activation rows per workgroup
 constexpr int kBN = 256;                         // weight rows per workgroup
-constexpr int kWaves = 4;
-constexpr int kMS = kBM / 16;                    // 16-row activation subtiles per wave
-constexpr int kNS = kBN / kWaves / 16;           // 16-row weight subtiles per wave
-constexpr int kChunkA = 8 * kMS * 64 * 16;       // fp16 operands of one super-block
-constexpr int kChunkS = kMS * 64 * 16;           // sum operands
+constexpr int kWM = 1, kWN = 8;                  // waves along M and N
+constexpr int kWaves = kWM * kWN;                // 8 waves: two per SIMD
+constexpr int kMT = kBM / 16;                    // 16-row activation subtiles per workgroup tile
+constexpr int kMS = kMT / kWM;                   // ... per wave
+constexpr int kNS = kBN / kWN / 16;              // 16-row weight subtiles per wave
+constexpr int kChunkA = 8 * kMT * 64 * 16;       // fp16 operands of one super-block
+constexpr int kChunkS = kMT * 64 * 16;           // sum operands
 constexpr int kChunk = kChunkA + kChunkS;        // 73728 B
-constexpr int kDmaPerWave = kChunk / 1024 / kWaves;
-static_assert(kChunk % (1024 * kWaves) == 0, "chunk must split into whole 1 KB copies per wave");
+static_assert(kChunkA / 2 % (1024 * kWaves) == 0 && (kChunkA / 2 + kChunkS) % (1024 * kWaves) == 0,
+              "chunk halves must split into whole 1 KB copies per wave");
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -81,16 +84,17 @@ __device__ __forceinline__ void split3(float v, uint32_t& hi, uint32_t& mid, uin
 }
 
 // Row exponent e_m: the largest |x| of row m scaled by 2^-e_m lies in [2^14, 2^15).  Rows
-// that are all zero, hold inf/nan, or lie past M get e = 0.  One wave per row.
-__global__ __launch_bounds__(256) void k_prefill_rowexp(const uint16_t* __restrict__ X, int64_t K, int M, int Mpad,
+// that are all zero, hold inf/nan, or lie past M get e = 0.  One workgroup per row.
+__global__ __launch_bounds__(256) void k_prefill_rowexp(const uint16_t* __restrict__ X, int64_t K, int M,
                                                         int32_t* __restrict__ rexp) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= Mpad) return;
+    __shared__ uint32_t part[4];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     uint32_t mx = 0;
     if (row < M) {
         const uint16_t* xr = X + (int64_t)row * K;
-        for (int64_t k = (int64_t)lane * 8; k < K; k += 512) {
+#pragma unroll 4
+        for (int64_t k = (int64_t)tid * 8; k < K; k += 2048) {
             const uint4 v = *(const uint4*)(xr + k);
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -102,7 +106,10 @@ __global__ __launch_bounds__(256) void k_prefill_rowexp(const uint16_t* __restri
     }
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, s, 64));
-    if (lane == 0) {
+    if (lane == 0) part[tid >> 6] = mx;
+    __syncthreads();
+    if (tid == 0) {
+        mx = max(max(part[0], part[1]), max(part[2], part[3]));
         int e = 0;
         if (mx != 0 && mx < 0x7F80u) {
             int ex;
@@ -113,50 +120,56 @@ __global__ __launch_bounds__(256) void k_prefill_rowexp(const uint16_t* __restri
     }
 }
 
-// One workgroup per (super-block b, 128-row tile mt): writes chunk (mt, b).
+// Chunk (mt, b) of the workspace.  One thread per (row, sub-block s): it converts the 32
+// activations of the sub-block, writes them into the 8-byte halves of the eight operand
+// entries that carry them (sub-block s = 2c + hh sits in half hh of entries (t, g) with
+// (t < 4 ? 0 : 2) + (g >> 1) = c), and writes its exactly split sum into half s >> 2 of the
+// sum entry of lane group s & 3.  Rows past M get zeros.
 __global__ __launch_bounds__(256) void k_prefill_pack(const uint16_t* __restrict__ X, int64_t K, int M,
                                                       const int32_t* __restrict__ rexp, uint8_t* __restrict__ ws,
                                                       int nsb) {
     const int b = blockIdx.x, mt = blockIdx.y;
+    const int item = blockIdx.z * 256 + threadIdx.x;   // 0 .. kBM * 8 - 1
+    const int ml = item >> 3, s = item & 7;
+    const int i = ml >> 4, r = ml & 15;
+    const int m = mt * kBM + ml;
     uint8_t* chunk = ws + ((int64_t)mt * nsb + b) * kChunk;
-    for (int idx = threadIdx.x; idx < kChunkA / 16; idx += 256) {
-        const int t = idx / (kMS * 64), i = (idx / 64) % kMS, lane = idx & 63;
-        const int r = lane & 15, g = lane >> 4;
-        const int m = mt * kBM + i * 16 + r;
-        uint4 out = make_uint4(0, 0, 0, 0);
-        if (m < M) {
-            const int e = rexp[m];
-            const int c = (t < 4 ? 0 : 2) + (g >> 1);
-            const int64_t k0 = (int64_t)b * QK_K + 64 * c + 16 * (g & 1) + 4 * (t & 3);
-            const uint2 lo = *(const uint2*)(X + (int64_t)m * K + k0);        // x[k0 .. k0+3]
-            const uint2 hi = *(const uint2*)(X + (int64_t)m * K + k0 + 32);   // x[k0+32 .. k0+35]
-            out.x = f16_scaled(lo.x, e) | f16_scaled(lo.y, e) << 16;              // (k0, k0+2)
-            out.y = f16_scaled(lo.x >> 16, e) | f16_scaled(lo.y >> 16, e) << 16;  // (k0+1, k0+3)
-            out.z = f16_scaled(hi.x, e) | f16_scaled(hi.y, e) << 16;
-            out.w = f16_scaled(hi.x >> 16, e) | f16_scaled(hi.y >> 16, e) << 16;
-        }
-        *(uint4*)(chunk + (int64_t)idx * 16) = out;
-    }
-    for (int idx = threadIdx.x; idx < kChunkS / 16; idx += 256) {
-        const int i = idx / 64, lane = idx & 63;
-        const int r = lane & 15, g = lane >> 4;
-        const int m = mt * kBM + i * 16 + r;
-        uint32_t o[4] = {0, 0, 0, 0};
-        if (m < M) {
-            const int e = rexp[m];
+    uint32_t v[32];
+    float sum = 0.f;
+    if (m < M) {
+        const int e = rexp[m];
+        const uint4* src = (const uint4*)(X + (int64_t)m * K + (int64_t)b * QK_K + 32 * s);
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const uint16_t* p = X + (int64_t)m * K + (int64_t)b * QK_K + 32 * (g + 4 * q);
-                float s = 0.f;
-                for (int k = 0; k < 32; ++k) s += __half2float(__ushort_as_half((unsigned short)f16_scaled(p[k], e)));
-                uint32_t h, md, l;
-                split3(s, h, md, l);
-                o[2 * q] = h | md << 16;
-                o[2 * q + 1] = l;
+        for (int q = 0; q < 4; ++q) {
+            const uint4 x = src[q];
+            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                v[8 * q + 2 * k] = f16_scaled(w[k], e);
+                v[8 * q + 2 * k + 1] = f16_scaled(w[k] >> 16, e);
             }
         }
-        *(uint4*)(chunk + kChunkA + (int64_t)idx * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+#pragma unroll
+        for (int k = 0; k < 32; ++k) sum += __half2float(__ushort_as_half((unsigned short)v[k]));
+    } else {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) v[k] = 0;
     }
+    const int c = s >> 1, hh = s & 1;
+    const int t0 = c < 2 ? 0 : 4, gb = 2 * (c & 1);
+#pragma unroll
+    for (int g1 = 0; g1 < 2; ++g1) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const int base = 16 * g1 + 4 * tt;   // K offset inside the sub-block
+            const uint2 o = make_uint2(v[base] | v[base + 2] << 16, v[base + 1] | v[base + 3] << 16);
+            const int lane = 16 * (gb + g1) + r;
+            *(uint2*)(chunk + ((int64_t)((t0 + tt) * kMT + i) * 64 + lane) * 16 + 8 * hh) = o;
+        }
+    }
+    uint32_t h = 0, md = 0, l = 0;
+    if (m < M) split3(sum, h, md, l);
+    *(uint2*)(chunk + kChunkA + ((int64_t)i * 64 + 16 * (s & 3) + r) * 16 + 8 * (s >> 2)) = make_uint2(h | md << 16, l);
 }
 
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t off) {
@@ -176,16 +189,28 @@ __device__ __forceinline__ void dma_chunk(const uint8_t* ws, int64_t chunk_index
     }
 }
 
-// The wave's 64 weight rows of super-block b into its LDS slice, laid out [q][j][n] by
-// 16-B piece q of the block (0 = header, 1 + p = qs piece p), row 16j + n: a lane group
-// reading one piece of 16 rows touches 256 contiguous bytes.
-constexpr int kSliceB = 9 * kNS * 16 * 16;   // 9216 B per wave
+// The weight rows of wave column wn (kNS subtiles of 16), super-block b, into their LDS
+// slice, laid out [q][j][n] by 16-B piece q of the block (0 = header, 1 + p = qs piece p),
+// row 16j + n: a lane group reading one piece of 16 rows touches 256 contiguous bytes.
+// Ten pieces per row (piece 9, the first 16 B past the block, is never read) make a whole
+// number of 1 KB copies per wave, so every wave's copy count and waits are static.
+constexpr int kBpieces = 10;
+constexpr int kSliceB = kBpieces * kNS * 256;  // bytes per wave column
+constexpr int kBq = kSliceB / 1024;            // copies per wave per super-block
+static_assert(kSliceB % 1024 == 0, "weight slice must be whole 1 KB copies");
 __device__ __forceinline__ void dma_blocks(__amdgpu_buffer_rsrc_t wr, uint32_t rb, int b, uint8_t* slice, int lane) {
-    const int j = lane >> 4, n = lane & 15;
-    const uint32_t row_off = (uint32_t)(16 * j + n) * rb + (uint32_t)b * 144u;
 #pragma unroll
-    for (int q = 0; q < 9; ++q) dma16(wr, slice + q * 1024, row_off + 16u * (uint32_t)q);
+    for (int k = 0; k < kBq; ++k) {
+        const int p = 64 * k + lane;                     // piece index in the slice
+        const int q = p / (16 * kNS), row = p % (16 * kNS);
+        dma16(wr, slice + k * 1024, (uint32_t)row * rb + (uint32_t)b * 144u + 16u * (uint32_t)q);
+    }
 }
+
+// Workgroup barrier for LDS phases: waits for this wave's LDS reads and writes only.  The
+// direct-to-LDS copies a phase needs are waited for explicitly (vmcnt) before it, so copies
+// for later phases stay in flight across the barrier (__syncthreads would wait for all).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ uint4 lds_u4(const uint8_t* p) { return *(const uint4*)p; }
 
@@ -269,8 +294,8 @@ __device__ __forceinline__ uint32_t dword_of(const uint4& v, int i) {
 
 // Four MFMAs t = 4*half .. 4*half+3 of every accumulator tile.  sa = the half's operand
 // stage ([t][i][lane]), sb = the wave's weight slice.
-__device__ __forceinline__ void half_block(const uint8_t* sa, const uint8_t* sb, int half, int n, int g, int lane,
-                                           f4_t (&D1)[kMS][kNS]) {
+__device__ __forceinline__ void half_block(const uint8_t* sa, const uint8_t* sb, int half, int i0, int n, int g,
+                                           int lane, f4_t (&D1)[kMS][kNS]) {
     const f4_t zero = {0.f, 0.f, 0.f, 0.f};
     const CodeMask cm = code_mask();
     uint4 q[kNS];
@@ -287,7 +312,7 @@ __device__ __forceinline__ void half_block(const uint8_t* sa, const uint8_t* sb,
         for (int j = 0; j < kNS; ++j) B[j] = b_operand(dword_of(q[j], tt), ck[j], cm);
 #pragma unroll
         for (int i = 0; i < kMS; ++i) {
-            const h8_t A = __builtin_bit_cast(h8_t, lds_u4(sa + ((tt * kMS + i) * 64 + lane) * 16));
+            const h8_t A = __builtin_bit_cast(h8_t, lds_u4(sa + ((tt * kMT + i0 + i) * 64 + lane) * 16));
 #pragma unroll
             for (int j = 0; j < kNS; ++j)
                 D1[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], (half == 0 && tt == 0) ? zero : D1[i][j],
@@ -297,7 +322,7 @@ __device__ __forceinline__ void half_block(const uint8_t* sa, const uint8_t* sb,
 }
 
 // Min term and the per-super-block epilogue: acc += d * D1 - dmin * D2.
-__device__ __forceinline__ void block_epilogue(const uint8_t* ssum, const uint8_t* sb, int n, int g, int lane,
+__device__ __forceinline__ void block_epilogue(const uint8_t* ssum, const uint8_t* sb, int i0, int n, int g, int lane,
                                                const f4_t (&D1)[kMS][kNS], f4_t (&acc)[kMS][kNS]) {
     const f4_t zero = {0.f, 0.f, 0.f, 0.f};
     float d[kNS], dm[kNS];
@@ -311,7 +336,7 @@ __device__ __forceinline__ void block_epilogue(const uint8_t* ssum, const uint8_
     }
 #pragma unroll
     for (int i = 0; i < kMS; ++i) {
-        const bf8_t As = __builtin_bit_cast(bf8_t, lds_u4(ssum + (i * 64 + lane) * 16));
+        const bf8_t As = __builtin_bit_cast(bf8_t, lds_u4(ssum + ((i0 + i) * 64 + lane) * 16));
 #pragma unroll
         for (int j = 0; j < kNS; ++j) {
             const f4_t D2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(As, __builtin_bit_cast(bf8_t, bm[j]), zero, 0, 0, 0);
@@ -326,21 +351,22 @@ __device__ __forceinline__ void block_epilogue(const uint8_t* ssum, const uint8_
 
 constexpr int kA0 = kChunkA / 2;            // operands of t = 0..3
 constexpr int kA1 = kChunkA / 2 + kChunkS;  // operands of t = 4..7, then the sums
-constexpr int kWaitAll = 0x0F70;            // s_waitcnt vmcnt(0)
-constexpr int kWaitB = 0x0F70 | 9;          // vmcnt(9): the 9 weight-slice copies issued last may pend
+constexpr int kWaitAll = 0x0F70;            // s_waitcnt vmcnt(0); | n gives vmcnt(n), n < 16
 
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill_gemm(
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_prefill_gemm(
     const uint8_t* __restrict__ W, int64_t N, int nsb, const uint8_t* __restrict__ ws,
     const int32_t* __restrict__ rexp, int M, uint16_t* __restrict__ Y, float* __restrict__ Yf, int mtiles, int ntiles) {
     // Separate LDS objects per stage, so that reads of one stage are not ordered behind
     // direct-to-LDS copies still in flight into another.
     __shared__ __align__(16) uint8_t sA0[kA0];
     __shared__ __align__(16) uint8_t sA1[kA1];
-    __shared__ __align__(16) uint8_t sB0[kWaves * kSliceB];
-    __shared__ __align__(16) uint8_t sB1[kWaves * kSliceB];
+    __shared__ __align__(16) uint8_t sB0[kWN * kSliceB];
+    __shared__ __align__(16) uint8_t sB1[kWN * kSliceB];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar) for the copies
+    const int wn = w;
     const int n = lane & 15, g = lane >> 4;
+    const int i0 = 0;
 
     // workgroup -> tile: the XCD of a workgroup is wg % 8; workgroups that share a weight
     // tile (all mtiles of one ntile) get consecutive ids on one XCD
@@ -350,12 +376,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 
     const int mt = pid % mtiles, nt = pid / mtiles;
 
     const int64_t rb = (int64_t)nsb * 144;
-    const int64_t row0 = (int64_t)nt * kBN + 64 * w;
-    const int64_t nv64 = N - row0;
-    const int nvalid = nv64 <= 0 ? 0 : (nv64 >= 64 ? 64 : (int)nv64);
+    constexpr int kRows = 16 * kNS;   // weight rows per wave
+    const int64_t row0 = (int64_t)nt * kBN + kRows * wn;
+    const int64_t nvr = N - row0;
+    const int nvalid = nvr <= 0 ? 0 : (nvr >= kRows ? kRows : (int)nvr);
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W + (nvalid ? row0 * rb : 0), (uint32_t)(nvalid * rb));
-    uint8_t* const b0 = sB0 + w * kSliceB;
-    uint8_t* const b1 = sB1 + w * kSliceB;
+    uint8_t* const b0 = sB0 + wn * kSliceB;
+    uint8_t* const b1 = sB1 + wn * kSliceB;
 
     f4_t acc[kMS][kNS], D1[kMS][kNS];
 #pragma unroll
@@ -366,34 +393,38 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 
     const int64_t cbase = (int64_t)mt * nsb;
     dma_blocks(wr, (uint32_t)rb, 0, b0, lane);
     dma_chunk<kA0 / 1024 / kWaves>(ws, cbase, 0, sA0, w, lane);
-    // One super-block: [wait, h1 copy, next blocks] h0 MFMAs [wait, next h0 copy] h1 + epilogue.
+    // One super-block: [wait, barrier, copy h1, copy next blocks] h0 MFMAs [wait for h1,
+    // barrier, copy next h0] h1 MFMAs + epilogue.
 #define AIPU_SUPERBLOCK(BCUR, BNXT)                                                                         \
     {                                                                                                       \
         __builtin_amdgcn_s_waitcnt(kWaitAll);                                                               \
-        __syncthreads();                                                                                    \
+        lds_barrier();                                                                                      \
         dma_chunk<kA1 / 1024 / kWaves>(ws, cbase + b, kA0, sA1, w, lane);                                   \
-        const bool more = b + 1 < nsb;                                                                      \
-        if (more) dma_blocks(wr, (uint32_t)rb, b + 1, BNXT, lane);                                          \
-        half_block(sA0, BCUR, 0, n, g, lane, D1);                                                           \
-        if (more) __builtin_amdgcn_s_waitcnt(kWaitB); else __builtin_amdgcn_s_waitcnt(kWaitAll);            \
-        __syncthreads();                                                                                    \
-        if (more) dma_chunk<kA0 / 1024 / kWaves>(ws, cbase + b + 1, 0, sA0, w, lane);                       \
-        half_block(sA1, BCUR, 1, n, g, lane, D1);                                                           \
-        block_epilogue(sA1 + kChunkA / 2, BCUR, n, g, lane, D1, acc);                                       \
+        dma_blocks(wr, (uint32_t)rb, bn, BNXT, lane);                                                   \
+        half_block(sA0, BCUR, 0, i0, n, g, lane, D1);                                                       \
+        __builtin_amdgcn_s_waitcnt(kWaitAll | kBq);                                                         \
+        lds_barrier();                                                                                      \
+        dma_chunk<kA0 / 1024 / kWaves>(ws, cbase + bn, 0, sA0, w, lane);                                    \
+        half_block(sA1, BCUR, 1, i0, n, g, lane, D1);                                                       \
+        block_epilogue(sA1 + kChunkA / 2, BCUR, i0, n, g, lane, D1, acc);                                   \
     }
+    // The copies for super-block b + 1 are issued unconditionally (the last super-block
+    // re-copies itself into the idle stages), so every wave's copy count and wait is static.
     for (int b = 0; b < nsb; ++b) {
+        int bn = b + 1 < nsb ? b + 1 : b;
         AIPU_SUPERBLOCK(b0, b1)
         if (++b >= nsb) break;
+        bn = b + 1 < nsb ? b + 1 : b;
         AIPU_SUPERBLOCK(b1, b0)
     }
 #undef AIPU_SUPERBLOCK
 
-    // y = bf16(acc * 2^e_m); lane holds rows 16i + 4g + r, columns 16j + n
+    // y = bf16(acc * 2^e_m); lane holds rows 16(i0 + i) + 4g + r, columns 16j + n
 #pragma unroll
     for (int i = 0; i < kMS; ++i) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int64_t m = (int64_t)mt * kBM + 16 * i + 4 * g + r;
+            const int64_t m = (int64_t)mt * kBM + 16 * (i0 + i) + 4 * g + r;
             if (m >= M) continue;
             const int e = rexp[m];
 #pragma unroll
@@ -428,9 +459,9 @@ hipError_t launch_gemm_prefill(int type, const void* w, int64_t N, int64_t K, co
     if ((int64_t)mtiles * ntiles > 0x7FFFFFFF || (int64_t)64 * nsb * 144 >= (1LL << 32)) return hipErrorInvalidValue;
     uint8_t* chunks = (uint8_t*)ws;
     int32_t* rexp = (int32_t*)(chunks + (int64_t)mtiles * nsb * kChunk);
-    hipLaunchKernelGGL(k_prefill_rowexp, dim3((unsigned)(Mp / 4)), dim3(256), 0, st, x, K, (int)M, (int)Mp, rexp);
-    hipLaunchKernelGGL(k_prefill_pack, dim3((unsigned)nsb, (unsigned)mtiles), dim3(256), 0, st, x, K, (int)M, rexp,
-                       chunks, nsb);
+    hipLaunchKernelGGL(k_prefill_rowexp, dim3((unsigned)Mp), dim3(256), 0, st, x, K, (int)M, rexp);
+    hipLaunchKernelGGL(k_prefill_pack, dim3((unsigned)nsb, (unsigned)mtiles, kBM * 8 / 256), dim3(256), 0, st, x, K,
+                       (int)M, rexp, chunks, nsb);
     hipLaunchKernelGGL(k_prefill_gemm, dim3((unsigned)(mtiles * ntiles)), dim3(kWaves * 64), 0, st,
                        (const uint8_t*)w, N, nsb, chunks, rexp, (int)M, y, y_f32, mtiles, (int)ntiles);
     return hipGetLastError();

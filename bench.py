@@ -357,7 +357,7 @@ def summarize_traffic(fetch_dir, write_dir, out=TRAFFIC_JSON):
 
 def _short_kernel(name):
     """`void aipu::(anonymous namespace)::k_gemv1<3, ...>(...)` -> `k_gemv1<3, ...>`."""
-    n = name.split("(")[0] if not name.startswith("void ") else name[5:]
+    n = name[5:] if name.startswith("void ") else name
     n = n.replace("aipu::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
     depth, out = 0, ""
     for ch in n:
