@@ -483,6 +483,173 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     pb.finish(wg, red, KP, tid);
 }
 
+// ------------------------------------------------- small-batch kernel (M = 2 .. 8)
+// One 16-row weight tile per workgroup, its K split over KP waves of BPK blocks each.  A
+// wave loads its weight blocks straight into registers (all of them at once), and stages
+// only its own K-slice of the MR activation rows in its own LDS region, so no barrier
+// precedes the block loop.  Activation rows 4h .. 4h+3 form the block-diagonal operand of
+// MFMA set h (lane 16g + n reads row 4h + n - 4g of K-group g), so one set of codes serves
+// four rows and lane 16g + n ends with the sums of rows 4h + r in its D registers r.
+// LDS layout per wave: operand entries [b][g][m][t] (16 B each; a (b, g, m) group of 8 is
+// padded to 144 B so that the 16 diagonal lanes hit distinct banks), the sub-block sums
+// [b][g][lo/hi][m] (fp32), and one zero group that the off-diagonal lanes read (plain LDS
+// loads on every lane, so the compiler tracks every wait).
+
+template <int MR, int BPK>
+__global__ __launch_bounds__(kMaxW * 64) void k_gemvm(ProbPlain<MR> pb, const uint16_t* __restrict__ X, int K,
+                                                      int KP) {
+    constexpr int MRQ = MR < 4 ? MR : 4;   // rows per MFMA set
+    constexpr int NH = MR / MRQ;           // MFMA sets (1, or 2 for MR = 8)
+    constexpr int kGrp = 144;                       // bytes per (b, g, m) group of 8 entries
+    constexpr int kEnt = BPK * 4 * MR * kGrp;       // operand bytes per wave
+    constexpr int kSums = BPK * 8 * MR * 4;
+    constexpr int kZero = kGrp;                     // zeros read by off-diagonal lanes
+    constexpr int kWave = kEnt + kSums + kZero;
+    constexpr int kPieces = MR * BPK * 32;   // 16-B activation pieces per wave
+    constexpr int kXL = (kPieces + 63) / 64;
+    __shared__ __align__(16) uint8_t s_act[kMaxW * kWave];
+    __shared__ float red[kMaxW * kTR * MR];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nsb = K / QK_K;
+    const int wg = blockIdx.x;
+    uint8_t* wA = s_act + (uint32_t)w * kWave;
+    float* wS = (float*)(wA + kEnt);
+    const int kb0 = w * BPK;
+    const int64_t rb = (int64_t)nsb * 144;
+    const int n = lane & 15, g = lane >> 4;
+
+    // 1. activations of this wave's K-slice (rows >= M read as zero), 2. its weight blocks
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)((int64_t)pb.M * K * 2));
+    uint4 xv[kXL];
+#pragma unroll
+    for (int i = 0; i < kXL; ++i) {
+        const int q = lane + 64 * i;
+        const int m = q / (BPK * 32), p = q - m * (BPK * 32);
+        const uint32_t off = q < kPieces ? 2u * (uint32_t)((int64_t)m * K + (int64_t)kb0 * QK_K) + 16u * (uint32_t)p : kOOB;
+        xv[i] = buf_load16(xr, off);
+    }
+    const TileRef tr = pb.tile(wg, 0);
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
+    Raw R[BPK];
+#pragma unroll
+    for (int b = 0; b < BPK; ++b) R[b] = raw_load(wr, (uint32_t)(n * rb) + (uint32_t)(kb0 + b) * 144u, g);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. stage operand entries and sub-block sums, and clear the zero region
+    if (lane < kZero / 16) *(u32x4_t*)(wA + kEnt + kSums + 16u * (uint32_t)lane) = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < kXL; ++i) {
+        const int q = lane + 64 * i;
+        const int m = q / (BPK * 32), p = q - m * (BPK * 32);
+        const uint32_t ones = 0x3F803F80u;
+        float sm = 0.f;
+        sm = dot2(xv[i].x, ones, sm);
+        sm = dot2(xv[i].y, ones, sm);
+        sm = dot2(xv[i].z, ones, sm);
+        sm = dot2(xv[i].w, ones, sm);
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+        if (q < kPieces) {
+            const int bb = p >> 5, gg = (p >> 3) & 3, t = p & 7;
+            *(u32x4_t*)(wA + (uint32_t)(kGrp * ((bb * 4 + gg) * MR + m) + 16 * t)) = act_perm(xv[i]);
+            if ((p & 3) == 0) wS[((bb * 4 + gg) * 2 + ((p >> 2) & 1)) * MR + m] = sm;
+        }
+    }
+
+    // 4. block loop
+    const int mm = n - 4 * g;
+    const bool diag = mm >= 0 && mm < MRQ;
+    const HdrSel hs = hdr_sel(g);
+    const CodeK ck = code_k();
+    u32x4_t A[NH][8];
+    float acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+    f32x4_t dlo[NH], dhi[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) dlo[h] = dhi[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint32_t zero_off = (uint32_t)(kEnt + kSums);
+#pragma unroll
+    for (int b = 0; b < BPK; ++b) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const uint32_t base = diag ? (uint32_t)(kGrp * ((b * 4 + g) * MR + 4 * h + mm)) : zero_off;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) A[h][t] = lds128(wA, base + 16u * (uint32_t)t);
+        }
+        float alo[MR], ahi[MR];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            alo[r] = wS[((b * 4 + g) * 2 + 0) * MR + r];
+            ahi[r] = wS[((b * 4 + g) * 2 + 1) * MR + r];
+        }
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int r = 0; r < MRQ; ++r) {
+                dlo[h][r] = -kCodeBiasF * alo[4 * h + r];
+                dhi[h][r] = -kCodeBiasF * ahi[4 * h + r];
+            }
+        const uint32_t qd[8] = {R[b].q0.x, R[b].q0.y, R[b].q0.z, R[b].q0.w, R[b].q1.x, R[b].q1.y, R[b].q1.z, R[b].q1.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const u32x4_t cl = codes_lo(qd[2 * t], qd[2 * t + 1], ck);
+            const u32x4_t cu = codes_hi(qd[2 * t], qd[2 * t + 1], ck);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                dlo[h] = mfma(A[h][t], cl, dlo[h]);
+                dhi[h] = mfma(A[h][4 + t], cu, dhi[h]);
+            }
+        }
+        const Hdr H = hdr_decode(R[b].h, hs);
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int r = 0; r < MRQ; ++r) {
+                const int m = 4 * h + r;
+                const float t1 = __builtin_fmaf(H.sc1, dhi[h][r], H.sc0 * dlo[h][r]);
+                const float v = __builtin_fmaf(H.m1, ahi[m], H.m0 * alo[m]);
+                acc[m] = __builtin_fmaf(H.d, t1, acc[m]);
+                acc[m] = __builtin_fmaf(-H.dm, v, acc[m]);
+            }
+    }
+
+    // 5. reduce over the four K-groups, then across the K parts
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        acc[r] += __shfl_xor(acc[r], 16, 64);
+        acc[r] += __shfl_xor(acc[r], 32, 64);
+    }
+    if (lane < kTR) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r) red[(w * kTR + lane) * MR + r] = acc[r];
+    }
+    __syncthreads();
+    pb.finish(wg, red, KP, tid);
+}
+
+template <int MR>
+hipError_t run_gemvm(const ProbPlain<MR>& pb, int nsb, unsigned nwg, const uint16_t* x, int K, hipStream_t st) {
+    // KP waves of BPK blocks: the largest KP <= 8 that divides nsb with a supported BPK
+    for (int kp = kMaxW; kp >= 1; --kp) {
+        if (nsb % kp || 64 * kp < kTR * MR) continue;   // the final reduction uses kTR * MR threads
+        const int bpk = nsb / kp;
+        const dim3 grid(nwg), block(64 * kp);
+#define AIPU_LM(B)                                                                       \
+    case B: hipLaunchKernelGGL((k_gemvm<MR, B>), grid, block, 0, st, pb, x, K, kp); return hipGetLastError();
+        switch (bpk) {
+            AIPU_LM(1)
+            AIPU_LM(2)
+            AIPU_LM(3)
+            AIPU_LM(4)
+            default: break;
+        }
+#undef AIPU_LM
+    }
+    return hipErrorNotSupported;
+}
+
 // ------------------------------------------------------------------ planning
 int pick_pd(int bpk) {
     for (int pd = 4; pd >= 2; --pd)
@@ -581,6 +748,14 @@ hipError_t run1(const Prob& pb, const Plan1& pl, unsigned nwg, const uint16_t* X
     return hipGetLastError();
 }
 
+// Shapes the small-batch kernel covers: K / 256 split into at most 8 parts of 1 .. 4 blocks,
+// with enough waves for the reduction of mr rows.
+bool gemvm_supported(int nsb, int mr) {
+    for (int kp = kMaxW; kp >= 1; --kp)
+        if (nsb % kp == 0 && nsb / kp <= 4 && 64 * kp >= kTR * mr) return true;
+    return false;
+}
+
 template <int MR>
 hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int M, uint16_t* y, float* yf,
                       int64_t ystride, hipStream_t st) {
@@ -589,6 +764,7 @@ hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x,
     const unsigned nwg = (unsigned)((N + kTR - 1) / kTR);
     Plan1 p1;
     if (MR == 1 && make_plan1(nsb, 1, kMaxW, p1)) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
+    if (MR > 1 && gemvm_supported(nsb, MR)) return run_gemvm<MR>(pb, nsb, nwg, x, (int)K, st);
     Plan pl;
     if (!make_plan(nsb, 1, 1, MR, kMaxW, pl)) return hipErrorInvalidValue;
     return run_mfma<MR>(pb, pl, nwg, x, 0, (int64_t)M * K * 2, (int)K, M, st);
@@ -609,7 +785,16 @@ bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M) {
 hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
                             float* y_f32, int64_t ystride, hipStream_t st) {
     const uint8_t* W = (const uint8_t*)w;
-    for (int64_t m0 = 0; m0 < M; m0 += 4) {
+    const int nsb = (int)(K / QK_K);
+    for (int64_t m0 = 0; m0 < M;) {
+        if (M - m0 >= 8 && gemvm_supported(nsb, 8)) {   // eight rows in one pass
+            const ProbPlain<8> pb{W, N, row_bytes(T_Q4_K, K), y + m0 * ystride, y_f32 ? y_f32 + m0 * ystride : nullptr,
+                                  ystride, 8};
+            const hipError_t e = run_gemvm<8>(pb, nsb, (unsigned)((N + kTR - 1) / kTR), x + m0 * K, (int)K, st);
+            if (e != hipSuccess) return e;
+            m0 += 8;
+            continue;
+        }
         const int mr = (int)(M - m0 < 4 ? M - m0 : 4);
         const uint16_t* xm = x + m0 * K;
         uint16_t* ym = y + m0 * ystride;
@@ -619,6 +804,7 @@ hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t*
         else if (mr == 2) e = plain_pass<2>(W, N, K, xm, 2, ym, yfm, ystride, st);
         else e = plain_pass<4>(W, N, K, xm, mr, ym, yfm, ystride, st);
         if (e != hipSuccess) return e;
+        m0 += mr;
     }
     return hipSuccess;
 }

@@ -150,6 +150,9 @@ def test_gemv_f32_matmul_q4k_col():
 FAST_CASES = [
     (6144, 6144, 1), (4096, 4096, 1), (6144, 6144, 2), (6144, 6144, 4), (6144, 6144, 8),
     (1001, 2048, 1), (77, 256, 3), (300, 2304, 1), (64, 18432, 1), (2048, 6144, 5),
+    # small-batch kernel: K split 3 / 4 blocks per wave, passes of 8 + 4, 4 + 2, and a K
+    # too large for it (served by the staged kernel in passes of 4)
+    (300, 2304, 8), (129, 8192, 6), (16, 512, 12), (64, 18432, 8),
 ]
 
 
