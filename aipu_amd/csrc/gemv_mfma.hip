@@ -462,14 +462,13 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
             R[bb].q1 = *(const uint4*)(p + 32 + 32 * g);
         }
         if (gi + 1 < NG) {
-            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);   // the slice has been read: refill it
+            regs_consumed(R);   // the slice has been read: refill it
             dma_group<GS>(wr, wW, rb, kb0 + (gi + 1) * GS, lane);
         }
 #pragma unroll
         for (int bb = 0; bb < GS; ++bb) {
             const int b = gi * GS + bb;   // block index within this wave's part
             a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
-            a_wait(A);
             const float2 as = *(const float2*)(wS + (b * 4 + g) * 2);
             acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
         }

@@ -354,7 +354,7 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
                 R[bb].q1 = *(const uint4*)(p + 32 + 32 * g);
             }
             if (gi + 1 < NG) {
-                __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+                regs_consumed(R);   // the slice has been read: refill it
                 const int nxt = (gi + 1) * G::GS;
                 dma.issue(wr, wW, kb0 + nxt, bpk - nxt);
             }
@@ -362,7 +362,6 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
             for (int bb = 0; bb < G::GS; ++bb) {
                 const int b = gi * G::GS + bb;
                 a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
-                a_wait(A);
                 const float2 as = *(const float2*)(wS + (b * 4 + g) * 2);
                 acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
             }
@@ -379,7 +378,7 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
 #pragma unroll
                 for (int bb = 0; bb < G::GS; ++bb) R[bb] = q6_read(p + G::kPitch * bb, g);
                 if (gi + 1 < NG) {
-                    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+                    regs_consumed(R);   // the slice has been read: refill it
                     const int nxt = (gi + 1) * G::GS;
                     dma.issue(wr, wW, kb0 + nxt, bpk - nxt);
                 }
@@ -393,7 +392,7 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
 #pragma unroll
                 for (int bb = 0; bb < G::GS; ++bb) R[bb] = q8_read(p + G::kPitch * bb, g);
                 if (gi + 1 < NG) {
-                    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+                    regs_consumed(R);   // the slice has been read: refill it
                     const int nxt = (gi + 1) * G::GS;
                     dma.issue(wr, wW, kb0 + nxt, bpk - nxt);
                 }
@@ -409,7 +408,7 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
 #pragma unroll
                     for (int i = 0; i < 8; ++i) R[bb].v[i] = *(const uint4*)(p + G::kPitch * bb + 128 * g + 16 * i);
                 if (gi + 1 < NG) {
-                    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+                    regs_consumed(R);   // the slice has been read: refill it
                     const int nxt = (gi + 1) * G::GS;
                     dma.issue(wr, wW, kb0 + nxt, bpk - nxt);
                 }

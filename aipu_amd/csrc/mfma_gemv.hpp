@@ -176,6 +176,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // The 8 activation operands of a block, read on the lanes in `mask` only (the diagonal
 // lanes of the block-diagonal A); every other lane keeps its register contents, which stay
 // zero for the whole kernel.  This moves 64 B per read instead of a 1 KB broadcast of zeros.
+// The loads complete inside the asm (lgkmcnt(0) before it returns): the compiler treats the
+// outputs as written when the statement ends, so no load may still be in flight then.
+// s_and_b64 sets SCC, so SCC is declared clobbered (the compiler may keep a loop condition
+// there).
 __device__ __forceinline__ void a_reads(u32x4_t (&A)[8], uint32_t aa, uint64_t mask) {
     uint64_t saved;
     asm volatile(
@@ -189,16 +193,29 @@ __device__ __forceinline__ void a_reads(u32x4_t (&A)[8], uint32_t aa, uint64_t m
         "ds_read_b128 %5, %9 offset:320\n\t"
         "ds_read_b128 %6, %9 offset:384\n\t"
         "ds_read_b128 %7, %9 offset:448\n\t"
-        "s_mov_b64 exec, %8"
+        "s_mov_b64 exec, %8\n\t"
+        "s_waitcnt lgkmcnt(0)"
         : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]),
           "=&s"(saved)
-        : "v"(aa), "s"(mask));
+        : "v"(aa), "s"(mask)
+        : "memory", "scc");   // s_and_b64 writes SCC
 }
 
-// Wait for the reads above; the operands are tied so that no use moves above the wait.
-__device__ __forceinline__ void a_wait(u32x4_t (&A)[8]) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]));
+// A point after which the weight blocks in R are in registers: the asm consumes every
+// register of R (so the LDS loads that produce them have completed), and its memory clobber
+// keeps later memory operations -- the copy that refills the same LDS slice -- behind it.
+template <class T, int N>
+__device__ __forceinline__ void regs_consumed(const T (&R)[N]) {
+    static_assert(sizeof(T) % 4 == 0, "register blocks are whole dwords");
+    struct Dw {
+        uint32_t d[sizeof(T) / 4];
+    };
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const Dw w = __builtin_bit_cast(Dw, R[i]);
+#pragma unroll
+        for (int k = 0; k < (int)(sizeof(T) / 4); ++k) asm volatile("" ::"v"(w.d[k]) : "memory");
+    }
 }
 
 // Diagonal lanes of the block-diagonal activation operand: lane 16g + 4g + m for m < MR.

@@ -153,6 +153,9 @@ FAST_CASES = [
     # small-batch kernel: K split 3 / 4 blocks per wave, passes of 8 + 4, 4 + 2, and a K
     # too large for it (served by the staged kernel in passes of 4)
     (300, 2304, 8), (129, 8192, 6), (16, 512, 12), (64, 18432, 8),
+    # several weight-copy rounds per wave (3-block groups x 2, 2-block groups x 3): the
+    # round loop must run to the end
+    (64, 9216, 1), (40, 12288, 1),
 ]
 
 
