@@ -389,7 +389,8 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     const int BPK = GS * NG;
     const int XP = BPK * 32;
     const uint32_t kA = (uint32_t)BPK * 512;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: the copies take a scalar LDS base
     const int nsb = K / QK_K;
     const int wg = blockIdx.x;
     uint8_t* wA = s_act + (uint32_t)w * kActWave;
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
         for (int bb = 0; bb < GS; ++bb) {
             const int b = gi * GS + bb;   // block index within this wave's part
             a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
-            const float2 as = *(const float2*)(wS + (b * 4 + g) * 2);
+            const float2 as = sums_read(wS + (b * 4 + g) * 2);   // no wait on the refill in flight
             acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
         }
     }

@@ -218,6 +218,15 @@ __device__ __forceinline__ void regs_consumed(const T (&R)[N]) {
     }
 }
 
+// The sub-block activation sums (lo, hi) of one block for this lane, read inside an asm
+// statement that also waits for it: the compiler sees no LDS load there, so it does not
+// order the read behind direct-to-LDS copies still in flight into other LDS buffers.
+__device__ __forceinline__ float2 sums_read(const float* p) {
+    float2 v;
+    asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+    return v;
+}
+
 // Diagonal lanes of the block-diagonal activation operand: lane 16g + 4g + m for m < MR.
 __host__ __device__ constexpr uint64_t diag_mask(int mr) {
     uint64_t m = 0;
