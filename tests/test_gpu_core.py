@@ -156,6 +156,8 @@ FAST_CASES = [
     # several weight-copy rounds per wave (3-block groups x 2, 2-block groups x 3): the
     # round loop must run to the end
     (64, 9216, 1), (40, 12288, 1),
+    # N / #CUs rows per workgroup (two tiles, the second partly or barely filled)
+    (4100, 2048, 1), (7000, 6144, 1),
 ]
 
 
