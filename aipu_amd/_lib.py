@@ -82,6 +82,8 @@ SIGNATURES = {
                                     _P, _I, _P, _I64, _P]),
     "aipu_gemm_prefill_workspace_bytes": (_I64, [_I64, _I64]),
     "aipu_gemm_prefill": (_I, [_I, _P, _I64, _I64, _P, _I64, _P, _P, _I, _P, _I64, _P]),
+    "aipu_lm_head_workspace_bytes": (_I64, [_I64]),
+    "aipu_lm_head": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "aipu_stream_read": (_I, [_P, _I64, _P, _P]),
 }
 

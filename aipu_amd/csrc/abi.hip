@@ -299,6 +299,31 @@ int aipu_gemm_prefill(int ggml_type, const void* w, int64_t N, int64_t K, const 
                       "aipu_gemm_prefill");
 }
 
+int64_t aipu_lm_head_workspace_bytes(int64_t V) {
+    if (V < 1 || V > (1LL << 31)) return -1;
+    return aipu::lm_head_workspace_bytes(V);
+}
+
+int aipu_lm_head(const uint16_t* w, int64_t V, int64_t K, const uint16_t* x, uint16_t* logits, int32_t* argmax,
+                 void* workspace, int64_t ws_bytes, void* stream) {
+    if (!w || !x) return fail(AIPU_ERR_ARG, "null weight or activation pointer");
+    if (!logits && !argmax) return fail(AIPU_ERR_ARG, "neither logits nor argmax requested");
+    if (V < 1 || V > (1LL << 31)) return fail(AIPU_ERR_SHAPE, "V = %lld out of range", (long long)V);
+    if (K < 8 || K % 8 || K > (1LL << 24))
+        return fail(AIPU_ERR_SHAPE, "K = %lld must be a positive multiple of 8 (at most 2^24)", (long long)K);
+    if (!aligned(w, 16) || !aligned(x, 16)) return fail(AIPU_ERR_ALIGN, "w and x must be 16-byte aligned");
+    if (logits && !aligned(logits, 2)) return fail(AIPU_ERR_ALIGN, "logits must be 2-byte aligned");
+    if (argmax) {
+        const int64_t need = aipu::lm_head_workspace_bytes(V);
+        if (!workspace || ws_bytes < need)
+            return fail(AIPU_ERR_WORKSPACE, "lm_head workspace of %lld bytes needed, %lld given", (long long)need,
+                        (long long)ws_bytes);
+        if (!aligned(workspace, 256)) return fail(AIPU_ERR_ALIGN, "workspace must be 256-byte aligned");
+        if (!aligned(argmax, 4)) return fail(AIPU_ERR_ALIGN, "argmax must be 4-byte aligned");
+    }
+    return hip_status(aipu::launch_lm_head(w, V, K, x, logits, argmax, workspace, S(stream)), "aipu_lm_head");
+}
+
 int aipu_stream_read(const void* p, int64_t bytes, uint32_t* sink, void* stream) {
     if (!p || !sink) return fail(AIPU_ERR_ARG, "null pointer");
     if (bytes < 16 || bytes % 16) return fail(AIPU_ERR_SHAPE, "bytes must be a positive multiple of 16");

@@ -108,6 +108,12 @@ int64_t prefill_workspace_bytes(int64_t M, int64_t K);
 hipError_t launch_gemm_prefill(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
                                uint16_t* y, float* y_f32, int precision, void* ws, hipStream_t st);
 
+// lmhead.hip -- bf16 LM head in the reference's 7-way interleaved order, plus argmax;
+// ws holds lm_head_workspace_bytes(V) (used only when argmax is requested).
+int64_t lm_head_workspace_bytes(int64_t V);
+hipError_t launch_lm_head(const void* w, int64_t V, int64_t K, const uint16_t* x, uint16_t* logits, int32_t* argmax,
+                          void* ws, hipStream_t st);
+
 int device_cu_count();
 
 }  // namespace aipu

@@ -223,6 +223,35 @@ def gemm_prefill(ggml_type, w, N, K, x, precision=_lib.PREFILL_CODES, out=None, 
     return (y, yf) if out_f32 else y
 
 
+def lm_head_workspace(V, device):
+    """A workspace for lm_head over a V-row vocabulary (reusable for any V' <= V)."""
+    n = _lib.lib().aipu_lm_head_workspace_bytes(V)
+    if n < 0:
+        raise ValueError(f"no lm_head workspace for V={V}")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def lm_head(w, x, logits=True, argmax=True, workspace=None):
+    """bf16 LM head in the reference's 7-way interleaved order (bit-exact) and its argmax.
+
+    w: [V, K] bf16 rows; x: [K] bf16.  Returns (logits [V] bf16 or None, argmax [1] int32 or
+    None) as device tensors."""
+    _need_cuda(w, x)
+    w = _bf16(w)
+    x = _bf16(x).reshape(-1)
+    V, K = w.shape
+    if x.numel() != K:
+        raise ValueError(f"x has {x.numel()} values, W rows have {K}")
+    lg = torch.empty(V, dtype=torch.bfloat16, device=x.device) if logits else None
+    am = torch.empty(1, dtype=torch.int32, device=x.device) if argmax else None
+    ws = None
+    if argmax:
+        ws = workspace if workspace is not None else lm_head_workspace(V, x.device)
+    call("aipu_lm_head", _ptr(w), V, K, _ptr(x), _ptr(lg), _ptr(am), _ptr(ws), ws.numel() if ws is not None else 0,
+         _stream(x))
+    return lg, am
+
+
 def stream_read(buf, sink):
     """Read-bandwidth probe over a uint8 device buffer (bytes multiple of 16)."""
     _need_cuda(buf, sink)

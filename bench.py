@@ -253,6 +253,25 @@ def bench_prefill(dev, torch, M=512, K=6144, N=16384, reps=20):
                 timing=f"HIP graph of {reps} calls (row scaling + operand staging + GEMM), weights rotated over {nbuf} copies")
 
 
+def bench_lmhead(dev, torch, V=154880, K=6144, reps=20):
+    """Next-row F4: the bf16 LM head (vocabulary x MODEL_DIM, 1.9 GB of rows, far above the
+    256 MB MALL, so every call streams its weights from HBM) + argmax, bit-exact order."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(8)
+    w = (torch.randn((V, K), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    x = torch.randn(K, device="cuda", generator=gen).to(torch.bfloat16)
+    ws = dev.lm_head_workspace(V, "cuda")
+    fns = [(lambda: dev.lm_head(w, x, workspace=ws)) for _ in range(reps)]
+    ms, _ = time_graph(fns, reps=3)
+    t = min(ms) / reps
+    alg = 2 * V * K + 2 * K + 2 * V + 4
+    del w
+    torch.cuda.empty_cache()
+    return dict(V=V, K=K, us=t * 1e3, alg_bytes=alg, gbs=alg / (t * 1e-3) / 1e9,
+                pct_peak=100.0 * alg / (t * 1e-3) / 1e9 / PEAK_GBS,
+                timing=f"HIP graph of {reps} calls (logits kernel + argmax pass)")
+
+
 def cpu_baseline(budget_s=12.0):
     """Time the repo's CPU restatement of the reference's path on this host (1 core)."""
     import numpy as np
@@ -401,7 +420,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of one HIP graph")
-    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1"], default=None,
+    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1", "lmhead"], default=None,
                     help="run one measurement only (for kernel tracing / counter runs)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
                     help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into "
@@ -441,6 +460,9 @@ def main():
     if args.only == "prefill":
         print(json.dumps(bench_prefill(dev, torch)))
         return
+    if args.only == "lmhead":
+        print(json.dumps(bench_lmhead(dev, torch)))
+        return
     if args.only == "c1":
         print(json.dumps({f"m{M}": bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, label="C1") for M in (2, 4, 8)}))
         return
@@ -468,6 +490,8 @@ def main():
         log(f"mixed tiles: {extra['mixed_tiles_c3']['us']:.1f} us")
         extra["prefill_c4"] = bench_prefill(dev, torch)
         log(f"prefill: {extra['prefill_c4']['ms']:.2f} ms, {extra['prefill_c4']['tflops']:.1f} TFLOP/s")
+        extra["lm_head_f4"] = bench_lmhead(dev, torch)
+        log(f"lm head: {extra['lm_head_f4']['us']:.1f} us, {extra['lm_head_f4']['gbs']:.0f} GB/s")
     cpu = None if args.no_cpu else cpu_baseline()
 
     achieved = head["gbs"]

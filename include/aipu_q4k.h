@@ -168,6 +168,18 @@ int aipu_gemm_prefill(int ggml_type, const void* w, int64_t N, int64_t K, const 
                       int64_t M, uint16_t* y, float* y_f32, int precision, void* workspace,
                       int64_t ws_bytes, void* stream);
 
+/* bf16 LM head + greedy argmax, bit-exact in the reference's order.  Replaces the LM head
+ * of model_forward (tools/glm_model_q4k_ref.py:826-834): logits[v] = matmul_bf16_dot(x,
+ * W[v]) (:476-486; products into 7 round-robin fp32 partial sums in k order, added as
+ * ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+0)), bf16 out) and the strict-greater bf16_gt scan
+ * from -inf with lower-index ties (:138-148).  w: V rows of K bf16 (row-major, 16-B
+ * aligned; GGUF ne = [K, V]); x: K bf16 (16-B aligned); K a multiple of 8.  logits (V bf16)
+ * and argmax (one int32) may each be NULL, not both; the argmax needs a workspace of
+ * aipu_lm_head_workspace_bytes(V) bytes, 256-B aligned, any contents. */
+int64_t aipu_lm_head_workspace_bytes(int64_t V);
+int aipu_lm_head(const uint16_t* w, int64_t V, int64_t K, const uint16_t* x, uint16_t* logits,
+                 int32_t* argmax, void* workspace, int64_t ws_bytes, void* stream);
+
 /* Measurement utility with no counterpart in the reference: streams `bytes` (a multiple of
  * 16) from `p` with the same 16-B global loads the GEMV kernels use and folds them into
  * sink[0..255]; used to measure the achievable HBM read ceiling beside the 8 TB/s peak. */

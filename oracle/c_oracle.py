@@ -45,6 +45,12 @@ def lib():
         L.oq_glm_silu.restype = ctypes.c_uint16
         L.oq_glm_sigmoid.argtypes = [ctypes.c_uint16]
         L.oq_glm_sigmoid.restype = ctypes.c_uint16
+        L.oq_bf16_dot7.argtypes = [P, P, I64, P]
+        L.oq_bf16_dot7.restype = ctypes.c_uint16
+        L.oq_bf16_gt.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
+        L.oq_bf16_gt.restype = ctypes.c_int
+        L.oq_lm_head.argtypes = [P, I64, I64, P, I64, I64, P, P]
+        L.oq_lm_head.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -75,3 +81,29 @@ def gemv_ref(ggml_type, raw, N, K, x_bf16, n0=0, n1=None):
     if rc != 0:
         raise ValueError("oq_gemv_ref rejected its arguments")
     return acc, y
+
+
+def bf16_dot7(a_bits, w_bits):
+    """matmul_bf16_dot of one bf16 row pair: (bf16 bits, fp32 sum before rounding)."""
+    a = np.ascontiguousarray(a_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    s = np.zeros(1, np.float32)
+    b = lib().oq_bf16_dot7(_p(a), _p(w), int(a.size), _p(s))
+    return int(b), s[0]
+
+
+def lm_head(w_bits, x_bits, v0=0, v1=None):
+    """LM-head logits (bf16 bits, rows [v0, v1); other rows 0) and, for the full range, argmax."""
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16).reshape(-1)
+    V, K = w.shape
+    v1 = V if v1 is None else v1
+    logits = np.zeros(V, np.uint16)
+    am = np.zeros(1, np.int32)
+    if lib().oq_lm_head(_p(w), int(V), int(K), _p(x), int(v0), int(v1), _p(logits), _p(am)) != 0:
+        raise ValueError("oq_lm_head rejected its arguments")
+    return logits, int(am[0])
+
+
+def bf16_gt(a, b):
+    return bool(lib().oq_bf16_gt(int(a) & 0xFFFF, int(b) & 0xFFFF))

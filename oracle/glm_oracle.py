@@ -12,6 +12,9 @@ Imported only by ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 * ``swiglu_expert``        -- ``:702-708``
 * MoE combine              -- ``:797-809`` (slot-ordered fp32 ``facc += g*y``, shared expert
   last with weight 1, bf16 out)
+* LM head                  -- ``:476-486`` (``matmul_bf16_dot``: 7 round-robin fp32 partial
+  sums, fixed add tree) and the argmax scan of ``model_forward`` ``:826-834`` with
+  ``bf16_gt`` ``:138-148``
 
 All fp32 arithmetic is numpy float32 (one IEEE rounding per op, no fusion).  The
 scalar forms restate the reference op by op; the vectorised forms (``*_vec``) are checked
@@ -336,3 +339,49 @@ def moe_decode_ref(x_bits, router_type, router_w, experts, ggml_type, E, H, I, t
         ysh, _ = swiglu_expert(x_bits, shared[0], shared[1], shared[2], ggml_type, H, I)
     y, facc = moe_combine(sel_w, ys, ysh)
     return dict(y=y, sel_idx=sel, sel_w=sel_w, logits=logits, gates=gates, facc=facc, y_slots=ys)
+
+
+# ------------------------------------------------------------------ LM head
+LM_L = 7   # glm_matmul_pipe interleave (FP_MAC_LAT), tools/glm_model_q4k_ref.py:474
+
+
+def bf16_dot7_rows(w_bits, x_bits):
+    """``matmul_bf16_dot`` (:476-486) for every row of ``w`` at once: numpy float32 with the
+    K loop sequential, vectorised across rows.  Returns (bf16 bits [V], fp32 sums [V])."""
+    W = qo.bf16_bits_to_f32(np.asarray(w_bits, np.uint16))
+    W = np.atleast_2d(W)
+    x = qo.bf16_bits_to_f32(np.asarray(x_bits, np.uint16).reshape(-1))
+    V, K = W.shape
+    ps = np.zeros((LM_L, V), np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):      # inf - inf -> nan, as in fp32
+        for k in range(K):
+            ps[k % LM_L] = ps[k % LM_L] + W[:, k] * x[k]
+        a01 = ps[0] + ps[1]
+        a23 = ps[2] + ps[3]
+        a45 = ps[4] + ps[5]
+        a6 = ps[6] + F32(0.0)
+        s = (a01 + a23) + (a45 + a6)
+    return qo.bf16_round_bits(s), s
+
+
+def bf16_gt(a, b):
+    """``bf16_gt`` (:138-148): strict '>' on bf16 patterns."""
+    sa, sb = (a >> 15) & 1, (b >> 15) & 1
+    ma, mb = a & 0x7FFF, b & 0x7FFF
+    if sa != sb:
+        if ma == 0 and mb == 0:
+            return False
+        return sb == 1
+    if sa == 0:
+        return ma > mb
+    return ma < mb
+
+
+def lm_argmax(logit_bits):
+    """The argmax scan of ``model_forward`` (:826-834): start at -inf (0xFF80) and index 0,
+    replace on strict ``bf16_gt`` only (so ties keep the lower index)."""
+    best, arg = 0xFF80, 0
+    for v, lb in enumerate(np.asarray(logit_bits, np.uint16).tolist()):
+        if bf16_gt(lb, best):
+            best, arg = lb, v
+    return arg

@@ -12,6 +12,8 @@
  *   tools/q4k_ref.py:76-84    bf16_round                (RNE; inf/nan truncated)
  *   tools/q4k_ref.py:86-92    matmul_q4k_col            (sequential fp32 MAC in K order)
  *   tools/glm_model_q4k_ref.py:96-116,214-299  fp32_rsqrt, glm_sigmoid, glm_silu
+ *   tools/glm_model_q4k_ref.py:476-486        matmul_bf16_dot (7-way interleave + tree)
+ *   tools/glm_model_q4k_ref.py:138-148,826-834 bf16_gt argmax of the LM head
  *
  * Build: gcc -O2 -ffp-contract=off (every float op is one correctly rounded binary32
  * op on x86-64 SSE; contraction off keeps mul and add separate).  See oracle/Makefile.
@@ -235,3 +237,50 @@ uint16_t oq_glm_silu(uint16_t xb) {
 uint16_t oq_bf16_round_bits(uint32_t u) { return oq_bf16_round(u2f(u)); }
 uint32_t oq_rsqrt_bits(uint32_t u) { return f2u(oq_rsqrt(u2f(u))); }
 uint32_t oq_f16_to_f32_bits(uint16_t h) { return f2u(oq_f16_to_f32(h)); }
+
+/* ---- glm_model_q4k_ref.py:476-486 matmul_bf16_dot: product k goes into partial sum
+ * ps[k % 7] (ps starts at +0), then ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+0)), bf16 out. ---- */
+uint16_t oq_bf16_dot7(const uint16_t* a, const uint16_t* w, int64_t K, float* sum_out) {
+    float ps[7] = {0, 0, 0, 0, 0, 0, 0};
+    for (int64_t k = 0; k < K; k++) {
+        float prod = bf2f(a[k]) * bf2f(w[k]);
+        ps[k % 7] = ps[k % 7] + prod;
+    }
+    float a01 = ps[0] + ps[1], a23 = ps[2] + ps[3], a45 = ps[4] + ps[5], a6 = ps[6] + 0.0f;
+    float b0 = a01 + a23, b1 = a45 + a6;
+    float s = b0 + b1;
+    if (sum_out) *sum_out = s;
+    return oq_bf16_round(s);
+}
+
+/* ---- glm_model_q4k_ref.py:138-148 bf16_gt: strict '>' on bf16 patterns ---- */
+int oq_bf16_gt(uint16_t a, uint16_t b) {
+    int sa = (a >> 15) & 1, sb = (b >> 15) & 1;
+    int ma = a & 0x7FFF, mb = b & 0x7FFF;
+    if (sa != sb) {
+        if (ma == 0 && mb == 0) return 0;
+        return sb == 1;
+    }
+    if (sa == 0) return ma > mb;
+    return ma < mb;
+}
+
+/* ---- glm_model_q4k_ref.py:826-834: logits over rows [v0, v1) of the V x K bf16 head, and
+ * the argmax scan (start at -inf = 0xFF80, index 0; replace only on strict bf16_gt).
+ * argmax (nullable) is only meaningful for the full range v0 = 0, v1 = V. ---- */
+int oq_lm_head(const uint16_t* w, int64_t V, int64_t K, const uint16_t* x, int64_t v0, int64_t v1,
+               uint16_t* logits, int32_t* argmax) {
+    if (v0 < 0 || v1 > V || v0 > v1 || K < 1) return -1;
+    uint16_t best = 0xFF80;
+    int32_t arg = 0;
+    for (int64_t v = v0; v < v1; v++) {
+        uint16_t lb = oq_bf16_dot7(x, w + v * K, K, 0);
+        logits[v] = lb;
+        if (oq_bf16_gt(lb, best)) {
+            best = lb;
+            arg = (int32_t)v;
+        }
+    }
+    if (argmax) *argmax = arg;
+    return 0;
+}

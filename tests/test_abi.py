@@ -153,3 +153,19 @@ def test_error_raises_with_message():
     with pytest.raises(_lib.AipuError) as ei:
         _lib.call("aipu_gemv", 12, FAKE, 64, 100, FAKE, 1, FAKE, NULL, 0, S)
     assert ei.value.code == SHAPE and "multiple" in str(ei.value)
+
+
+def test_lm_head_validation():
+    f = L().aipu_lm_head
+    wsb = L().aipu_lm_head_workspace_bytes
+    assert wsb(154880) == 2420 * 8                  # one 8-byte (key, index) pair per 64-row wave
+    assert wsb(65) == 16 and wsb(0) < 0
+    need = wsb(1000)
+    assert f(NULL, 1000, 64, FAKE, FAKE, FAKE, FAKE, need, S) == ARG
+    assert f(FAKE, 1000, 64, FAKE, NULL, NULL, FAKE, need, S) == ARG
+    assert f(FAKE, 1000, 60, FAKE, FAKE, FAKE, FAKE, need, S) == SHAPE
+    assert f(FAKE, 0, 64, FAKE, FAKE, FAKE, FAKE, need, S) == SHAPE
+    assert f(FAKE, 1000, 64, ctypes.c_void_p(0x100008), FAKE, FAKE, FAKE, need, S) == ALIGN
+    assert f(FAKE, 1000, 64, FAKE, FAKE, FAKE, FAKE, need - 1, S) == WS
+    assert f(FAKE, 1000, 64, FAKE, FAKE, FAKE, NULL, need, S) == WS
+    assert f(FAKE, 1000, 64, FAKE, FAKE, FAKE, ctypes.c_void_p(0x100010), need, S) == ALIGN
