@@ -221,11 +221,13 @@ int aipu_swiglu_expert(int ggml_type, const void* wg, const void* wu, const void
                       "aipu_swiglu_expert");
 }
 
-int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type, const void* gate_exps,
-                           const void* up_exps, const void* down_exps, const void* shared_gate, const void* shared_up,
-                           const void* shared_down, int64_t E, int64_t H, int64_t I, int topk, uint32_t scale_bits,
-                           const uint16_t* x, uint16_t* y, int32_t* sel_idx, uint16_t* sel_w, int mode,
-                           void* workspace, int64_t ws_bytes, void* stream) {
+// Checks shared by the MoE decode step and the MoE layer step; fills `a` (need = workspace
+// bytes the caller's entry point requires).
+static int moe_args(int router_type, const void* router_w, int ggml_type, const void* gate_exps, const void* up_exps,
+                    const void* down_exps, const void* shared_gate, const void* shared_up, const void* shared_down,
+                    int64_t E, int64_t H, int64_t I, int topk, uint32_t scale_bits, const uint16_t* x, uint16_t* y,
+                    int32_t* sel_idx, uint16_t* sel_w, int mode, void* workspace, int64_t ws_bytes, int64_t need,
+                    aipu::MoeArgs& a) {
     if (!known_type(router_type)) return fail(AIPU_ERR_TYPE, "unsupported router type %d", router_type);
     if (!router_w || !gate_exps || !up_exps || !down_exps) return fail(AIPU_ERR_ARG, "null weight pointer");
     const bool sh_any = shared_gate || shared_up || shared_down;
@@ -245,12 +247,10 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
         return fail(AIPU_ERR_ALIGN, "misaligned expert weights");
     if ((sel_idx && !aligned(sel_idx, 4)) || (sel_w && !aligned(sel_w, 2)))
         return fail(AIPU_ERR_ALIGN, "misaligned routing outputs");
-    const int64_t need = aipu::moe_workspace_bytes(E, H, I, topk);
     if (!workspace || ws_bytes < need || !aligned(workspace, 256))
         return fail(AIPU_ERR_WORKSPACE, "workspace must be 256-byte aligned and >= %lld bytes", (long long)need);
     if (mode == AIPU_MODE_FAST && ggml_type == aipu::T_Q4_K && I / 256 > 8 * 8)
         return fail(AIPU_ERR_SHAPE, "fast mode supports I <= 16384");
-    aipu::MoeArgs a;
     a.router_type = router_type;
     a.router_w = router_w;
     a.type = ggml_type;
@@ -271,8 +271,50 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
     a.sel_w_out = sel_w;
     a.mode = mode;
     a.ws = workspace;
+    return AIPU_OK;
+}
+
+int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type, const void* gate_exps,
+                           const void* up_exps, const void* down_exps, const void* shared_gate, const void* shared_up,
+                           const void* shared_down, int64_t E, int64_t H, int64_t I, int topk, uint32_t scale_bits,
+                           const uint16_t* x, uint16_t* y, int32_t* sel_idx, uint16_t* sel_w, int mode,
+                           void* workspace, int64_t ws_bytes, void* stream) {
+    aipu::MoeArgs a;
+    const int rc = moe_args(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, shared_gate, shared_up,
+                            shared_down, E, H, I, topk, scale_bits, x, y, sel_idx, sel_w, mode, workspace, ws_bytes,
+                            E >= 1 && topk >= 1 ? aipu::moe_workspace_bytes(E, H, I, topk) : 0, a);
+    if (rc) return rc;
     return hip_status(aipu::launch_moe_decode(a, S(stream)), "aipu_moe_swiglu_decode");
 }
+
+int64_t aipu_moe_layer_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk) {
+    if (E < 1 || H < 1 || I < 1 || topk < 1) return -1;
+    return aipu::moe_layer_workspace_bytes(E, H, I, topk);
+}
+
+int aipu_moe_layer_decode(int router_type, const void* router_w, int ggml_type, const void* gate_exps,
+                          const void* up_exps, const void* down_exps, const void* shared_gate, const void* shared_up,
+                          const void* shared_down, int64_t E, int64_t H, int64_t I, int topk, uint32_t scale_bits,
+                          const uint16_t* h, const uint16_t* gamma, uint16_t* y, int32_t* sel_idx, uint16_t* sel_w,
+                          int mode, void* workspace, int64_t ws_bytes, void* stream) {
+    if (!gamma || !h || !y) return fail(AIPU_ERR_ARG, "null h, gamma or output pointer");
+    if (!aligned(gamma, 2)) return fail(AIPU_ERR_ALIGN, "gamma must be 2-byte aligned");
+    aipu::MoeArgs a;
+    const int rc = moe_args(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, shared_gate, shared_up,
+                            shared_down, E, H, I, topk, scale_bits, h, y, sel_idx, sel_w, mode, workspace, ws_bytes,
+                            E >= 1 && topk >= 1 ? aipu::moe_layer_workspace_bytes(E, H, I, topk) : 0, a);
+    if (rc) return rc;
+    return hip_status(aipu::launch_moe_layer_decode(a, gamma, S(stream)), "aipu_moe_layer_decode");
+}
+
+int aipu_rmsnorm(const uint16_t* x, const uint16_t* gamma, int64_t n, uint16_t* y, int mode, void* stream) {
+    if (!x || !gamma || !y) return fail(AIPU_ERR_ARG, "null pointer");
+    if (n < 1 || n > (1LL << 31)) return fail(AIPU_ERR_SHAPE, "n = %lld out of range", (long long)n);
+    if (mode != AIPU_MODE_REF && mode != AIPU_MODE_FAST) return fail(AIPU_ERR_ARG, "unknown mode %d", mode);
+    if (!aligned(x, 2) || !aligned(gamma, 2) || !aligned(y, 2)) return fail(AIPU_ERR_ALIGN, "misaligned pointer");
+    return hip_status(aipu::launch_rmsnorm(x, gamma, n, y, mode, S(stream)), "aipu_rmsnorm");
+}
+
 
 int64_t aipu_gemm_prefill_workspace_bytes(int64_t M, int64_t K) {
     if (M < 1 || K < aipu::QK_K || K % aipu::QK_K || M > (1LL << 31) || K > (1LL << 31)) return -1;

@@ -134,6 +134,12 @@ struct ProbDown {
     int topk, nslots, E, passthrough;
     int64_t H, rb, ebytes;
     uint16_t* Y;
+    // Split combine (more slots than one workgroup's waves): the first launch leaves the
+    // fp32 running sum in acc_out, the second starts from acc_in.  resid (nullable) is added
+    // after the bf16 rounding: Y = bf16(resid + bf16(facc)) (the decoder block's residual).
+    const float* acc_in = nullptr;
+    float* acc_out = nullptr;
+    const uint16_t* resid = nullptr;
     static constexpr bool kRoutes = false;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ TileRef tile(int wg, int t) const {
@@ -146,7 +152,7 @@ struct ProbDown {
         if (tid >= kTR) return;
         const int64_t d = (int64_t)wg * kTR + tid;
         if (d >= H) return;
-        float facc = 0.f;
+        float facc = acc_in ? acc_in[d] : 0.f;
         for (int s = 0; s < nslots; ++s) {
             float ys = 0.f;
             for (int k = 0; k < KP; ++k) ys += red[(s * KP + k) * kTR + tid];
@@ -158,7 +164,13 @@ struct ProbDown {
             const float p = s < topk ? bf16_to_f32(selw[s]) * yb : yb;
             facc = facc + p;
         }
-        Y[d] = (uint16_t)bf16_rne(facc);
+        if (acc_out) {
+            acc_out[d] = facc;
+            return;
+        }
+        uint32_t yb = bf16_rne(facc);
+        if (resid) yb = bf16_rne(bf16_to_f32(resid[d]) + bf16_to_f32(yb));
+        Y[d] = (uint16_t)yb;
     }
 };
 
@@ -830,26 +842,49 @@ hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint
     return run_mfma<1>(pb, pl, nwg, x, 0, H * 2, (int)H, 1, st);
 }
 
+// One down launch over `nslots` slots (at most one workgroup's waves).
+static hipError_t down_once(const ProbDown& pb, int64_t I, const uint16_t* h, hipStream_t st) {
+    const int nsb = (int)(I / QK_K);
+    const unsigned nwg = (unsigned)((pb.H + kTR - 1) / kTR);
+    const int kpmax = kMaxW / pb.nslots > 0 ? kMaxW / pb.nslots : 1;
+    Plan1 p1;
+    if (pb.nslots <= kMaxW && make_plan1(nsb, pb.nslots, kpmax, p1))
+        return run1(pb, p1, nwg, h, I, (int64_t)pb.nslots * I * 2, (int)I, st);
+    Plan pl;
+    if (!make_plan(nsb, pb.nslots, pb.nslots, 1, kpmax, pl)) return hipErrorInvalidValue;
+    return run_mfma<1>(pb, pl, nwg, h, I, (int64_t)pb.nslots * I * 2, (int)I, 1, st);
+}
+
 hipError_t launch_moe_down_mfma(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
                                 int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h, uint16_t* y,
-                                int passthrough, hipStream_t st) {
-    const int nsb = (int)(I / QK_K);
+                                int passthrough, hipStream_t st, float* acc_scratch, const uint16_t* resid) {
     const int64_t rb = row_bytes(T_Q4_K, I);
-    const ProbDown pb{D, shD, sel, selw, topk, nslots, (int)E, passthrough, H, rb, rb * H, y};
-    const unsigned nwg = (unsigned)((H + kTR - 1) / kTR);
-    const int kpmax = kMaxW / nslots > 0 ? kMaxW / nslots : 1;
-    Plan1 p1;
-    if (nslots <= kMaxW && make_plan1(nsb, nslots, kpmax, p1))
-        return run1(pb, p1, nwg, h, I, (int64_t)nslots * I * 2, (int)I, st);
-    Plan pl;
-    if (!make_plan(nsb, nslots, nslots, 1, kpmax, pl)) return hipErrorInvalidValue;
-    return run_mfma<1>(pb, pl, nwg, h, I, (int64_t)nslots * I * 2, (int)I, 1, st);
+    if (nslots <= kMaxW) {
+        ProbDown pb{D, shD, sel, selw, topk, nslots, (int)E, passthrough, H, rb, rb * H, y};
+        pb.resid = resid;
+        return down_once(pb, I, h, st);
+    }
+    // topk routed slots + the shared slot: routed slots first (fp32 running sum kept), then
+    // the shared slot continues the same sum and rounds.
+    if (nslots != topk + 1 || topk > kMaxW || !acc_scratch || passthrough) return hipErrorInvalidValue;
+    ProbDown routed{D, shD, sel, selw, topk, topk, (int)E, 0, H, rb, rb * H, y};
+    routed.acc_out = acc_scratch;
+    hipError_t e = down_once(routed, I, h, st);
+    if (e != hipSuccess) return e;
+    ProbDown shared{D, shD, sel, selw, 0, 1, (int)E, 0, H, rb, rb * H, y};
+    shared.acc_in = acc_scratch;
+    shared.resid = resid;
+    return down_once(shared, I, h + (int64_t)topk * I, st);
 }
 
 bool moe_mfma_supported(int nslots, int64_t H, int64_t I) {
     Plan p1, p2;
-    return I % kTR == 0 && make_plan((int)(H / QK_K), 2, 1, 1, 4, p1) &&
-           make_plan((int)(I / QK_K), nslots, nslots, 1, kMaxW / nslots > 0 ? kMaxW / nslots : 1, p2);
+    if (I % kTR != 0 || !make_plan((int)(H / QK_K), 2, 1, 1, 4, p1)) return false;
+    const auto down_ok = [&](int n) {
+        return make_plan((int)(I / QK_K), n, n, 1, kMaxW / n > 0 ? kMaxW / n : 1, p2);
+    };
+    if (nslots <= kMaxW) return down_ok(nslots);
+    return nslots == kMaxW + 1 && down_ok(kMaxW) && down_ok(1);
 }
 
 }  // namespace aipu

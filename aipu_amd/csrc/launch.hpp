@@ -72,9 +72,13 @@ bool moe_route_in_kernel(int64_t E, int topk);
 hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
                                   const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
                                   const uint16_t* x, uint16_t* h, hipStream_t st);
+// More slots than one workgroup holds (top-8 + shared) run as two launches that hand the
+// fp32 running sum over through acc_scratch (H floats); resid (nullable) is added to the
+// bf16 result (y = bf16(resid + bf16(facc))).
 hipError_t launch_moe_down_mfma(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
                                 int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h, uint16_t* y,
-                                int passthrough, hipStream_t st);
+                                int passthrough, hipStream_t st, float* acc_scratch = nullptr,
+                                const uint16_t* resid = nullptr);
 
 // moe.hip
 struct MoeArgs {
@@ -96,6 +100,7 @@ struct MoeArgs {
     uint16_t* sel_w_out;
     int mode;
     void* ws;
+    const uint16_t* resid = nullptr;   // when set, y = bf16(resid + bf16(combine)) (block residual)
 };
 int64_t moe_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
 hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st);
@@ -113,6 +118,17 @@ hipError_t launch_gemm_prefill(int type, const void* w, int64_t N, int64_t K, co
 int64_t lm_head_workspace_bytes(int64_t V);
 hipError_t launch_lm_head(const void* w, int64_t V, int64_t K, const uint16_t* x, uint16_t* logits, int32_t* argmax,
                           void* ws, hipStream_t st);
+
+// norm.hip -- pre-FFN RMSNorm (mode REF: element-order sum, bit-exact; FAST: tree) and
+// the residual add out = bf16(h + f)
+uint32_t recip_fp32_bits(int64_t n);
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* gamma, int64_t n, uint16_t* y, int mode,
+                          hipStream_t st);
+hipError_t launch_residual_add(const uint16_t* h, const uint16_t* f, int64_t n, uint16_t* out, hipStream_t st);
+
+// moe.hip -- FFN half of a decoder block: y = bf16(h + moe(rmsnorm(h, gamma)))
+int64_t moe_layer_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
+hipError_t launch_moe_layer_decode(const MoeArgs& a, const uint16_t* gamma, hipStream_t st);
 
 int device_cu_count();
 

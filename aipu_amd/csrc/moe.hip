@@ -28,7 +28,7 @@ constexpr int64_t kAlign = 256;
 inline int64_t up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    int64_t counter, logits, sel, selw, h, g, u, ys, total;
+    int64_t counter, logits, sel, selw, h, g, u, ys, facc, total;
 };
 
 WsLayout ws_layout(int64_t E, int64_t H, int64_t I, int topk) {
@@ -43,6 +43,7 @@ WsLayout ws_layout(int64_t E, int64_t H, int64_t I, int topk) {
     L.g = o;      o += up(nslots * I * 2);
     L.u = o;      o += up(nslots * I * 2);
     L.ys = o;     o += up(nslots * H * 2);
+    L.facc = o;   o += up(H * 4);
     L.total = o;
     return L;
 }
@@ -95,6 +96,7 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
     int32_t* sel = (int32_t*)(ws + L.sel);
     uint16_t* selw = (uint16_t*)(ws + L.selw);
     uint16_t* h = (uint16_t*)(ws + L.h);
+    float* facc = (float*)(ws + L.facc);
     const bool has_shared = a.sh_gate != nullptr;
     const int nslots = a.topk + (has_shared ? 1 : 0);
     const bool fast = a.mode == AIPU_MODE_FAST && a.type == T_Q4_K;
@@ -113,7 +115,8 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
         const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};
         AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
                                         a.I, a.x, h, st));
-        return launch_moe_down_mfma(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y, 0, st);
+        return launch_moe_down_mfma(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y, 0, st,
+                                    facc, a.resid);
     }
     // 2. router tail (one wave), then the experts
     AIPU_TRY(launch_router_tail(logits, (int)a.E, a.topk, a.scale_bits, sel, selw, nullptr, st, a.sel_idx_out,
@@ -122,14 +125,15 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
         const MoeRoute route{sel, nullptr, 0u, nullptr, nullptr, nullptr, nullptr};
         AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
                                         a.I, a.x, h, st));
-        return launch_moe_down_mfma(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y, 0, st);
+        return launch_moe_down_mfma(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y, 0, st,
+                                    facc, a.resid);
     }
     if (fast) {
         AIPU_TRY(launch_moe_gateup_fast(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, sel, a.topk, nslots, a.E, a.H,
                                         a.I, a.x, h, st));
         AIPU_TRY(launch_moe_down_fast(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y, 0,
                                       st));
-        return hipSuccess;
+        return a.resid ? launch_residual_add(a.resid, a.y, a.H, a.y, st) : hipSuccess;
     }
     uint16_t* g = (uint16_t*)(ws + L.g);
     uint16_t* u = (uint16_t*)(ws + L.u);
@@ -144,7 +148,8 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
     AIPU_TRY(launch_gemv_ref_gather(a.type, a.down_exps, a.H, a.I, h, 1, ys, nullptr, nslots, sel, a.topk, a.E,
                                     rbI * a.H, a.sh_down, a.I, a.H, st));
     hipLaunchKernelGGL(k_combine, dim3(blocks_for(a.H)), dim3(256), 0, st, ys, selw, a.topk, nslots, a.H, a.y);
-    return hipGetLastError();
+    AIPU_TRY(hipGetLastError());
+    return a.resid ? launch_residual_add(a.resid, a.y, a.H, a.y, st) : hipSuccess;
 }
 
 // A single SwiGLU expert: the expert is treated as the (only) shared slot, so no router
@@ -177,6 +182,24 @@ hipError_t launch_swiglu_expert(int type, const void* wg, const void* wu, const 
     hipLaunchKernelGGL(k_silu_mul, dim3(blocks_for(I)), dim3(256), 0, st, g, u, I, h);
     AIPU_TRY(hipGetLastError());
     return launch_gemv_ref(type, wd, H, I, h, 1, y, nullptr, st);
+}
+
+// The FFN half of decoder_block (tools/glm_model_q4k_ref.py:797-810) around the MoE step:
+// nrm = rmsnorm(h, gamma) (:451-465), then the MoE step on nrm with the residual
+// y = bf16(h + fbuf) applied to its output (fused into the last down launch on the
+// matrix-core path).  a.x is h and a.y the block output; the MoE workspace comes first in
+// `a.ws`, then nrm.
+int64_t moe_layer_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk) {
+    return moe_workspace_bytes(E, H, I, topk) + up(H * 2);
+}
+
+hipError_t launch_moe_layer_decode(const MoeArgs& a, const uint16_t* gamma, hipStream_t st) {
+    uint16_t* nrm = (uint16_t*)((uint8_t*)a.ws + moe_workspace_bytes(a.E, a.H, a.I, a.topk));
+    AIPU_TRY(launch_rmsnorm(a.x, gamma, a.H, nrm, a.mode, st));
+    MoeArgs m = a;
+    m.x = nrm;
+    m.resid = a.x;
+    return launch_moe_decode(m, st);
 }
 
 }  // namespace aipu

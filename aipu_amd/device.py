@@ -200,6 +200,47 @@ def moe_swiglu_decode(router_type, router_w, ggml_type, gate_exps, up_exps, down
     return y, sel, sw
 
 
+def rmsnorm(x, gamma, mode="fast", out=None):
+    """y = bf16((x * inv) * gamma), inv = fp32_rsqrt(mean(x^2) + 1e-5) (ref: element-order sum)."""
+    _need_cuda(x, gamma)
+    x = _bf16(x).reshape(-1)
+    gamma = _bf16(gamma).reshape(-1)
+    if gamma.numel() != x.numel():
+        raise ValueError("gamma and x differ in length")
+    y = out if out is not None else torch.empty(x.numel(), dtype=torch.bfloat16, device=x.device)
+    call("aipu_rmsnorm", _ptr(x), _ptr(gamma), x.numel(), _ptr(y), _mode(mode), _stream(x))
+    return y
+
+
+def moe_layer_workspace(E, H, I, topk, device):
+    """Zero-filled workspace for moe_layer_decode."""
+    n = _lib.lib().aipu_moe_layer_workspace_bytes(E, H, I, topk)
+    if n < 0:
+        raise ValueError("bad MoE layer shape")
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def moe_layer_decode(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, E, H, I, topk, h, gamma,
+                     mode="fast", shared=None, scale_bits=RSCALE_BITS, workspace=None, out=None, sel_out=None):
+    """FFN half of a MoE decoder block: y = bf16(h + moe(rmsnorm(h, gamma))).
+    Returns (y bf16[H], sel_idx int32[topk], sel_w bf16[topk])."""
+    _need_cuda(router_w, gate_exps, up_exps, down_exps, h, gamma)
+    h = _bf16(h).reshape(-1)
+    gamma = _bf16(gamma).reshape(-1)
+    ws = workspace if workspace is not None else moe_layer_workspace(E, H, I, topk, h.device)
+    y = out if out is not None else torch.empty(H, dtype=torch.bfloat16, device=h.device)
+    if sel_out is None:
+        sel = torch.empty(topk, dtype=torch.int32, device=h.device)
+        sw = torch.empty(topk, dtype=torch.bfloat16, device=h.device)
+    else:
+        sel, sw = sel_out
+    sg, su, sd = shared if shared is not None else (None, None, None)
+    call("aipu_moe_layer_decode", router_type, _ptr(router_w), ggml_type, _ptr(gate_exps), _ptr(up_exps),
+         _ptr(down_exps), _ptr(sg), _ptr(su), _ptr(sd), E, H, I, topk, scale_bits, _ptr(h), _ptr(gamma), _ptr(y),
+         _ptr(sel), _ptr(sw), _mode(mode), _ptr(ws), ws.numel(), _stream(h))
+    return y, sel, sw
+
+
 def prefill_workspace(M, K, device):
     """A workspace for gemm_prefill(M rows, K): reusable across calls of the same or smaller M."""
     n = _lib.lib().aipu_gemm_prefill_workspace_bytes(M, K)

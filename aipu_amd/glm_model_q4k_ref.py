@@ -15,6 +15,10 @@ QW :491-519                               QW (+ multi-super-block rows)    aipu_
 moe_router :663-681                       moe_router                      aipu_gemv + aipu_router_topk
 swiglu_expert :702-708                    swiglu_expert                   aipu_swiglu_expert
 decoder_block MoE half :797-809           moe_ffn                         aipu_moe_swiglu_decode
+rmsnorm :451-465                          rmsnorm                         aipu_rmsnorm
+decoder_block FFN half :797-810           ffn_block                       aipu_moe_layer_decode
+matmul_bf16_dot :476-486                  matmul_bf16_dot                 aipu_lm_head
+model_forward LM head :826-834            lm_head                         aipu_lm_head
 Config :559-611                           Config (hot-path fields)        --
 ========================================  ==============================  =====================
 
@@ -272,8 +276,62 @@ def moe_ffn(cfg, x_bf, Wg, Mg, Mu, Md, SHg=None, SHu=None, SHd=None):
             list(_vals_of(_host_u16(sw))))
 
 
+def rmsnorm(x_bf, gamma_bf):
+    """y[i] = bf16((x[i]*inv) * gamma[i]), inv = rsqrt(mean(x^2)+eps), on the GPU; reference
+    order in 'ref' mode (element-order sum of squares), tree sum in 'fast' mode."""
+    x = _dev_u16(_bits_of(x_bf))
+    g = _dev_u16(_bits_of(gamma_bf))
+    return list(_vals_of(_host_u16(dev.rmsnorm(x, g, mode=_MODE))))
+
+
+def ffn_block(cfg, h_bf, gamma_bf, Wg, Mg, Mu, Md, SHg=None, SHu=None, SHd=None):
+    """The FFN half of decoder_block (:797-810) for a MoE layer: y = bf16(h + MoE(rmsnorm(h))),
+    with the router, the routed experts in slot order and the optional shared expert.
+    Returns (y bf16 list, sel list, sel_w list)."""
+    E = len(Mg)
+    H = Wg.kpad
+    if len(h_bf) != H:
+        raise ValueError("ffn_block needs MODEL_DIM to be a whole number of 256-weight super-blocks")
+    I = (Mg[0].nout + 255) // 256 * 256
+    gate = torch.cat([_padded_rows(w, I) for w in Mg])
+    up = torch.cat([_padded_rows(w, I) for w in Mu])
+    down = torch.cat([_padded_rows(w, H) for w in Md])
+    shared = None
+    if SHg is not None:
+        shared = (_padded_rows(SHg, I), _padded_rows(SHu, I), _padded_rows(SHd, H))
+    y, sel, sw = dev.moe_layer_decode(TYPE_Q4_K, _padded_rows(Wg, Wg.nout), TYPE_Q4_K, gate, up, down, E, H, I,
+                                      cfg.TOPK, _dev_u16(_bits_of(h_bf)), _dev_u16(_bits_of(gamma_bf)), mode=_MODE,
+                                      shared=shared, scale_bits=cfg.RSCALE_BITS)
+    return (list(_vals_of(_host_u16(y))), [int(v) for v in sel.cpu().numpy()], list(_vals_of(_host_u16(sw))))
+
+
+def _pad8(bits):
+    out = np.zeros((bits.size + 7) // 8 * 8, np.uint16)
+    out[: bits.size] = bits
+    return out
+
+
+def matmul_bf16_dot(a_bf, w_bf):
+    """One LM-head output: 7 round-robin fp32 partial sums + the fixed add tree (GPU)."""
+    a = _pad8(_bits_of(a_bf))
+    w = _pad8(_bits_of(w_bf))
+    lg, _ = dev.lm_head(_dev_u16(w).view(1, -1), _dev_u16(a), argmax=False)
+    return F32(_vals_of(_host_u16(lg))[0])
+
+
+def lm_head(xn_bf, Wlm):
+    """The LM head of model_forward (:826-834): logits[v] = matmul_bf16_dot(xn, Wlm[v]) and the
+    strict-greater bf16 argmax with lower-index ties.  Returns (logits list, logits_bits list,
+    argmax int).  Rows are zero-padded to a multiple of 8 (zero products leave the sums)."""
+    x = _pad8(_bits_of(xn_bf))
+    W = np.stack([_pad8(_bits_of(r)) for r in Wlm])
+    lg, am = dev.lm_head(_dev_u16(W).view(W.shape[0], -1), _dev_u16(x))
+    bits = _host_u16(lg)
+    return list(_vals_of(bits)), [int(b) for b in bits], int(am.cpu().numpy()[0])
+
+
 __all__ = [
     "F32", "f32_bits", "bits_f32", "fp16_to_f32", "f32_to_f16bits", "bf16", "bf16_bits", "bf16_from_bits", "b2f",
     "fp32_rsqrt", "glm_sigmoid", "glm_silu", "f32_bits_key", "matmul_q4k", "QW", "Config", "moe_router",
-    "_sum_tree", "swiglu_expert", "moe_ffn", "set_mode",
+    "_sum_tree", "swiglu_expert", "moe_ffn", "set_mode", "rmsnorm", "ffn_block", "matmul_bf16_dot", "lm_head",
 ]

@@ -210,6 +210,47 @@ def bench_moe(dev, torch, steps, E=256, H=6144, I=2048, topk=8, mode="fast"):
     return res
 
 
+def bench_layer(dev, torch, steps=200, E=256, H=6144, I=2048, topk=8):
+    """Next-row F2: the FFN half of a MoE decoder block at the config-2 shape -- fast RMSNorm,
+    Q4_K router, 8 routed + 1 shared Q4_K SwiGLU experts, residual -- plus the RMSNorm alone
+    in both modes."""
+    device = "cuda"
+    gen = torch.Generator(device=device)
+    gen.manual_seed(98)
+    ge = gen_q4k(E * I, H, gen, device)
+    ue = gen_q4k(E * I, H, gen, device)
+    de = gen_q4k(E * H, I, gen, device)
+    rw = gen_q4k(E, H, gen, device)
+    sh = (gen_q4k(I, H, gen, device), gen_q4k(I, H, gen, device), gen_q4k(H, I, gen, device))
+    nx = 64
+    X = (torch.randn((nx, H), device=device, generator=gen) * 0.5).to(torch.bfloat16)
+    G = (1.0 + 0.1 * torch.randn(H, device=device, generator=gen)).to(torch.bfloat16)
+    Y = torch.empty((nx, H), dtype=torch.bfloat16, device=device)
+    ws = dev.moe_layer_workspace(E, H, I, topk, device)
+    sel = torch.empty(topk, dtype=torch.int32, device=device)
+    sw = torch.empty(topk, dtype=torch.bfloat16, device=device)
+
+    def step(i):
+        j = i % nx
+        return lambda: dev.moe_layer_decode(Q4K, rw, Q4K, ge, ue, de, E, H, I, topk, X[j], G, mode="fast",
+                                            shared=sh, workspace=ws, out=Y[j], sel_out=(sel, sw))
+
+    ms, _ = time_graph([step(i) for i in range(steps)], reps=3)
+    us = min(ms) * 1000.0 / steps
+    res = dict(E=E, H=H, I=I, topk=topk, shared=True, router="Q4_K", us_per_step=us,
+               alg_bytes=(topk + 1) * 3 * q4k_bytes(I, H) + q4k_bytes(E, H) + 4 * H * 2)
+    res["gbs"] = res["alg_bytes"] / (us * 1e-6) / 1e9
+    for mode in ("fast", "ref"):
+        out = torch.empty(H, dtype=torch.bfloat16, device=device)
+        ms, _ = time_graph([(lambda j=i: dev.rmsnorm(X[j % nx], G, mode=mode, out=out)) for i in range(200)], reps=3)
+        res[f"rmsnorm_{mode}_us"] = min(ms) * 1000.0 / 200
+    log(f"MoE layer (norm + 8+1 experts + residual): {us:.1f} us; rmsnorm fast {res['rmsnorm_fast_us']:.2f} us, "
+        f"ref {res['rmsnorm_ref_us']:.2f} us")
+    del ge, ue, de
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_tiles(dev, torch, steps=50):
     """24 column tiles of 256 rows cycling Q4_K, Q6_K, Q8_0, F16 at K=6144."""
     import numpy as np
@@ -420,7 +461,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of one HIP graph")
-    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1", "lmhead"], default=None,
+    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1", "lmhead", "layer"], default=None,
                     help="run one measurement only (for kernel tracing / counter runs)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
                     help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into "
@@ -460,6 +501,9 @@ def main():
     if args.only == "prefill":
         print(json.dumps(bench_prefill(dev, torch)))
         return
+    if args.only == "layer":
+        print(json.dumps(bench_layer(dev, torch)))
+        return
     if args.only == "lmhead":
         print(json.dumps(bench_lmhead(dev, torch)))
         return
@@ -491,6 +535,7 @@ def main():
         extra["prefill_c4"] = bench_prefill(dev, torch)
         log(f"prefill: {extra['prefill_c4']['ms']:.2f} ms, {extra['prefill_c4']['tflops']:.1f} TFLOP/s")
         extra["lm_head_f4"] = bench_lmhead(dev, torch)
+        extra["moe_layer_f2"] = bench_layer(dev, torch)
         log(f"lm head: {extra['lm_head_f4']['us']:.1f} us, {extra['lm_head_f4']['gbs']:.0f} GB/s")
     cpu = None if args.no_cpu else cpu_baseline()
 

@@ -151,6 +151,28 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
                            int32_t* sel_idx, uint16_t* sel_w, int mode, void* workspace,
                            int64_t ws_bytes, void* stream);
 
+/* RMSNorm of one bf16 vector: inv = fp32_rsqrt(f32(f32(sumsq * recip_fp32(n)) + 1e-5)),
+ * y[i] = bf16(f32(f32(x[i] * inv) * gamma[i])).  Replaces rmsnorm
+ * (tools/glm_model_q4k_ref.py:451-465, recip_fp32 :434-449; RTL src/rmsnorm_unit.v).
+ * AIPU_MODE_REF sums the squares in element order (bit-exact); AIPU_MODE_FAST sums them as a
+ * tree (tolerance mode). */
+int aipu_rmsnorm(const uint16_t* x, const uint16_t* gamma, int64_t n, uint16_t* y, int mode,
+                 void* stream);
+
+/* The FFN half of one MoE decoder block: y = bf16(f32(h) + f32(fbuf)), fbuf = the MoE decode
+ * step (as aipu_moe_swiglu_decode) on rmsnorm(h, gamma).  Replaces
+ * tools/glm_model_q4k_ref.py:797-810 (decoder_block after the attention residual).
+ * Arguments as aipu_moe_swiglu_decode with x -> h and gamma[H] added; the workspace is
+ * aipu_moe_layer_workspace_bytes(E, H, I, topk) bytes, zero-filled before first use. */
+int64_t aipu_moe_layer_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
+int aipu_moe_layer_decode(int router_type, const void* router_w, int ggml_type,
+                          const void* gate_exps, const void* up_exps, const void* down_exps,
+                          const void* shared_gate, const void* shared_up,
+                          const void* shared_down, int64_t E, int64_t H, int64_t I, int topk,
+                          uint32_t scale_bits, const uint16_t* h, const uint16_t* gamma,
+                          uint16_t* y, int32_t* sel_idx, uint16_t* sel_w, int mode,
+                          void* workspace, int64_t ws_bytes, void* stream);
+
 /* Prefill GEMM for large M on the matrix cores: y[M][N] = bf16(x[M][K] . dequant(w)^T),
  * tolerance mode (|acc - exact| <= 1e-5 * sum|a*w|; the summation order differs from the
  * reference, use aipu_gemv(..., AIPU_MODE_REF) for the bit-exact order).  Types: Q4_K.

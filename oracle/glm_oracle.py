@@ -12,6 +12,9 @@ Imported only by ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 * ``swiglu_expert``        -- ``:702-708``
 * MoE combine              -- ``:797-809`` (slot-ordered fp32 ``facc += g*y``, shared expert
   last with weight 1, bf16 out)
+* ``rmsnorm``              -- ``:451-465`` with ``_recip_fp32`` ``:434-449`` (element-order fp32
+  sum of squares, ``inv = rsqrt(sumsq*recip(n) + 1e-5)``, ``bf16((x*inv)*gamma)``)
+* MoE decoder FFN half     -- ``:797-810`` (rmsnorm -> MoE step -> residual ``bf16(h + fbuf)``)
 * LM head                  -- ``:476-486`` (``matmul_bf16_dot``: 7 round-robin fp32 partial
   sums, fixed add tree) and the argmax scan of ``model_forward`` ``:826-834`` with
   ``bf16_gt`` ``:138-148``
@@ -385,3 +388,52 @@ def lm_argmax(logit_bits):
         if bf16_gt(lb, best):
             best, arg = lb, v
     return arg
+
+
+# ------------------------------------------------------------------ RMSNorm + layer
+RMS_EPS_BITS = 0x3727C5AC   # 1e-5, :432
+
+
+def recip_fp32_bits(n):
+    """``_recip_fp32`` (:434-449): q = floor(2^60 / n) normalised to 64 bits, 23 mantissa
+    bits, guard bit, sticky from the rest of q, round half to even; a mantissa carry shifts
+    right and bumps the exponent."""
+    q = (1 << 60) // n
+    msb = q.bit_length() - 1
+    expo = msb - 60 + 127
+    qs = q << (63 - msb)
+    mant = (qs >> 40) & 0x7FFFFF
+    guard = (qs >> 39) & 1
+    sticky = 1 if qs & ((1 << 39) - 1) else 0
+    mant += guard & (sticky | (mant & 1))
+    if mant >> 23:
+        mant >>= 1
+        expo += 1
+    return ((expo & 0xFF) << 23) | (mant & 0x7FFFFF)
+
+
+def rmsnorm(x_bits, gamma_bits):
+    """``rmsnorm`` (:451-465) on bf16 patterns -> bf16 patterns.  The sum of squares is a
+    sequential float32 loop; the per-element tail is vectorised (elementwise float32 ops)."""
+    x = qo.bf16_bits_to_f32(np.asarray(x_bits, np.uint16).reshape(-1))
+    g = qo.bf16_bits_to_f32(np.asarray(gamma_bits, np.uint16).reshape(-1))
+    sq = x * x
+    s = F32(0.0)
+    for v in sq:
+        s = F32(s + v)
+    meps = fadd(fmul(s, _b(recip_fp32_bits(x.size))), _b(RMS_EPS_BITS))
+    inv = fp32_rsqrt(meps)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return qo.bf16_round_bits((x * inv) * g)
+
+
+def moe_layer_ref(h_bits, gamma_bits, router_type, router_w, experts, ggml_type, E, H, I, topk,
+                  scale_bits=0x40200000, shared=None):
+    """FFN half of ``decoder_block`` (:797-810): nrm = rmsnorm(h), fbuf = MoE step on nrm,
+    y = bf16(h + fbuf).  Returns dict(y, nrm, fbuf, sel_idx, sel_w)."""
+    nrm = rmsnorm(h_bits, gamma_bits)
+    r = moe_decode_ref(nrm, router_type, router_w, experts, ggml_type, E, H, I, topk, scale_bits, shared)
+    hf = qo.bf16_bits_to_f32(np.asarray(h_bits, np.uint16))
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = qo.bf16_round_bits(hf + qo.bf16_bits_to_f32(r["y"]))
+    return dict(y=y, nrm=nrm, fbuf=r["y"], sel_idx=r["sel_idx"], sel_w=r["sel_w"])

@@ -9,6 +9,10 @@ KAT or brute force pins are sampled here:
 * ``fp32_rsqrt`` over special values and a sweep of fp32 inputs  -> rsqrt_cases.npz
 * ``moe_router`` on Q4_K router weights (ties included)           -> router_cases.npz
 * ``swiglu_expert`` on one-super-block Q4_K experts               -> swiglu_cases.npz
+* ``rmsnorm`` (+ ``_recip_fp32``) on several lengths and ranges, and the FFN half of
+  ``decoder_block`` (rmsnorm -> moe_router -> swiglu_expert per slot -> shared expert ->
+  combine -> residual) on one-super-block experts               -> rmsnorm_cases.npz
+  (``--rmsnorm`` writes only this file)
 
 Inputs come from this script's own seeded generator; weights are passed to the reference
 through its ``QW`` container and stored here as raw ggml Q4_K blocks (144 B each), the
@@ -22,7 +26,8 @@ import sys
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-REF_TOOLS = sys.argv[1] if len(sys.argv) > 1 else "/root/reference/tools"
+_ARGS = [a for a in sys.argv[1:] if not a.startswith("--")]
+REF_TOOLS = _ARGS[0] if _ARGS else "/root/reference/tools"
 
 
 def codes_to_qs(codes):
@@ -121,5 +126,79 @@ def main():
     print("wrote act_tables.npz rsqrt_cases.npz router_cases.npz swiglu_cases.npz")
 
 
+def main_rmsnorm():
+    """rmsnorm_cases.npz: rmsnorm goldens and decoder-block FFN-half goldens."""
+    sys.path.insert(0, REF_TOOLS)
+    import glm_model_q4k_ref as ref  # noqa: E402  (reference golden, build container only)
+
+    F32 = np.float32
+    rng = np.random.default_rng(20261202)
+    out = {}
+    ns = [1, 7, 16, 100, 128, 256, 6144]
+    out["recip_n"] = np.array(ns + [3, 5, 1000, 4096, 12288, 65535], np.int64)
+    out["recip_bits"] = np.array([ref.f32_bits(ref._recip_fp32(int(n))) for n in out["recip_n"]], np.uint32)
+
+    def bits(vals):
+        return np.array([ref.bf16_bits(v) for v in vals], np.uint16)
+
+    ci = 0
+    for n in ns:
+        for scale in (1.0, 1e-3, 300.0):
+            xv = (rng.standard_normal(n) * scale).astype(np.float32)
+            gv = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+            if n >= 16 and scale == 1.0:
+                xv[0] = 4096.0                      # one large square first: later ones absorbed
+            x_bf = [ref.bf16(F32(v)) for v in xv]
+            g_bf = [ref.bf16(F32(v)) for v in gv]
+            y = ref.rmsnorm(x_bf, g_bf)
+            out[f"n{ci}_x"], out[f"n{ci}_g"], out[f"n{ci}_y"] = bits(x_bf), bits(g_bf), bits(y)
+            ci += 1
+    zero = [ref.bf16(F32(0.0))] * 64
+    out[f"n{ci}_x"], out[f"n{ci}_g"], out[f"n{ci}_y"] = bits(zero), bits(zero), bits(ref.rmsnorm(zero, zero))
+    out["n_cases"] = np.array([ci + 1], np.int32)
+
+    # FFN half of decoder_block (:797-810), HIDDEN = INTER = 256, E = 4, TOPK = 2, shared expert
+    E, TOPK, D = 4, 2, 256
+    cfg = ref.Config(MODEL_DIM=D, N_EXPERT=E, TOPK=TOPK, INTER_MOE=D)
+    for li in range(1):
+        wg_q, wg_img = random_qw(ref, rng, E)
+        mg = [random_qw(ref, rng, D) for _ in range(E)]
+        mu = [random_qw(ref, rng, D) for _ in range(E)]
+        md = [random_qw(ref, rng, D) for _ in range(E)]
+        sh = [random_qw(ref, rng, D) for _ in range(3)]
+        hv = (rng.standard_normal(D) * 0.5).astype(np.float32)
+        gv = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+        h = [ref.bf16(F32(v)) for v in hv]
+        gam = [ref.bf16(F32(v)) for v in gv]
+        nrm2 = ref.rmsnorm(h, gam)
+        sel, sel_w, _ = ref.moe_router(cfg, nrm2, wg_q)
+        facc = [F32(0.0)] * D
+        for slot in range(TOPK):
+            e = sel[slot]
+            y_e = ref.swiglu_expert(cfg, nrm2, mg[e][0], mu[e][0], md[e][0])
+            gw = ref.b2f(sel_w[slot])
+            for d in range(D):
+                facc[d] = ref.fadd(facc[d], ref.fmul(gw, ref.b2f(y_e[d])))
+        y_sh = ref.swiglu_expert(cfg, nrm2, sh[0][0], sh[1][0], sh[2][0])
+        for d in range(D):
+            facc[d] = ref.fadd(facc[d], ref.b2f(y_sh[d]))
+        fbuf = [ref.bf16(facc[d]) for d in range(D)]
+        y = [ref.bf16(ref.fadd(ref.b2f(h[i]), ref.b2f(fbuf[i]))) for i in range(D)]
+        k = f"l{li}_"
+        out[k + "h"], out[k + "gamma"], out[k + "router"] = bits(h), bits(gam), wg_img
+        out[k + "gate"] = np.concatenate([m[1] for m in mg])
+        out[k + "up"] = np.concatenate([m[1] for m in mu])
+        out[k + "down"] = np.concatenate([m[1] for m in md])
+        out[k + "sh"] = np.stack([m[1] for m in sh])
+        out[k + "nrm"], out[k + "fbuf"], out[k + "y"] = bits(nrm2), bits(fbuf), bits(y)
+        out[k + "sel"] = np.array(sel, np.int32)
+        out[k + "selw"] = bits(sel_w)
+    np.savez_compressed(os.path.join(HERE, "rmsnorm_cases.npz"), **out)
+    print("wrote rmsnorm_cases.npz")
+
+
 if __name__ == "__main__":
-    main()
+    if "--rmsnorm" in sys.argv:
+        main_rmsnorm()
+    else:
+        main()

@@ -111,11 +111,14 @@ def test_moe_ref_bitexact(router_type, shared, topk):
     assert_bits_equal(h_bits(y), r["y"], "y")
 
 
-@pytest.mark.parametrize("router_type,shared", [(BF16, False), (Q4K, True)])
-def test_moe_fast_small(router_type, shared):
-    E, H, I, topk = 16, 512, 256, 4
+@pytest.mark.parametrize("router_type,shared,topk", [(BF16, False, 4), (Q4K, True, 4), (Q4K, True, 8),
+                                                    (BF16, True, 7)])
+def test_moe_fast_small(router_type, shared, topk):
+    """topk = 8 with the shared expert is nine slots: the matrix-core down leg runs as two
+    launches handing the fp32 running sum over (routed slots, then the shared slot)."""
+    E, H, I = 16, 512, 256
     note(f"moe fast small router={router_type} shared={shared}")
-    rng = np.random.default_rng(77 + shared)
+    rng = np.random.default_rng(77 + shared + 100 * topk)
     rw, ex, sh, x = _moe_case(rng, E, H, I, router_type, shared)
     shd = tuple(d_u8(a) for a in sh) if sh else None
     y, sel, sw = dev.moe_swiglu_decode(router_type, d_u8(rw), Q4K, d_u8(ex[0]), d_u8(ex[1]), d_u8(ex[2]), E, H, I,
