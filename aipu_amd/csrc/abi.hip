@@ -287,6 +287,27 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
     return hip_status(aipu::launch_moe_decode(a, S(stream)), "aipu_moe_swiglu_decode");
 }
 
+int64_t aipu_moe_batched_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk) {
+    if (E < 1 || E > 4096 || H < 1 || I < 1 || topk < 1 || topk > 32) return -1;
+    return aipu::moe_batched_workspace_bytes(E, H, I, topk);
+}
+
+int aipu_moe_swiglu_decode_batched(int router_type, const void* router_w, int ggml_type, const void* gate_exps,
+                                   const void* up_exps, const void* down_exps, const void* shared_gate,
+                                   const void* shared_up, const void* shared_down, int64_t E, int64_t H, int64_t I,
+                                   int topk, uint32_t scale_bits, const uint16_t* x, int64_t M, uint16_t* y,
+                                   int32_t* sel_idx, uint16_t* sel_w, int mode, void* workspace, int64_t ws_bytes,
+                                   void* stream) {
+    if (M < 1 || M > (1LL << 20)) return fail(AIPU_ERR_SHAPE, "M = %lld out of range", (long long)M);
+    aipu::MoeArgs a;
+    const bool shape_ok = E >= 1 && E <= 4096 && topk >= 1 && topk <= 32;
+    const int rc = moe_args(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, shared_gate, shared_up,
+                            shared_down, E, H, I, topk, scale_bits, x, y, sel_idx, sel_w, mode, workspace, ws_bytes,
+                            shape_ok ? aipu::moe_batched_workspace_bytes(E, H, I, topk) : 0, a);
+    if (rc) return rc;
+    return hip_status(aipu::launch_moe_decode_batched(a, M, S(stream)), "aipu_moe_swiglu_decode_batched");
+}
+
 int64_t aipu_moe_layer_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk) {
     if (E < 1 || H < 1 || I < 1 || topk < 1) return -1;
     return aipu::moe_layer_workspace_bytes(E, H, I, topk);

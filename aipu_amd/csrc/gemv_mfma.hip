@@ -48,7 +48,10 @@ struct ProbPlain {
     int64_t ystride;   // N of the full output (tiles of a mixed call write a column slice)
     int M;
     static constexpr bool kRoutes = false;
+    static constexpr int kRows = MR;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
+    __device__ bool active(int) const { return true; }
+    __device__ const uint16_t* act(int, const uint16_t* X) const { return X; }
     __device__ TileRef tile(int wg, int) const {
         const int64_t r0 = (int64_t)wg * kTR;
         const int64_t nv = N - r0;
@@ -507,9 +510,8 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
 // [b][g][lo/hi][m] (fp32), and one zero group that the off-diagonal lanes read (plain LDS
 // loads on every lane, so the compiler tracks every wait).
 
-template <int MR, int BPK>
-__global__ __launch_bounds__(kMaxW * 64) void k_gemvm(ProbPlain<MR> pb, const uint16_t* __restrict__ X, int K,
-                                                      int KP) {
+template <int MR, int BPK, class Prob>
+__global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* __restrict__ X0, int K, int KP) {
     constexpr int MRQ = MR < 4 ? MR : 4;   // rows per MFMA set
     constexpr int NH = MR / MRQ;           // MFMA sets (1, or 2 for MR = 8)
     constexpr int kGrp = 144;                       // bytes per (b, g, m) group of 8 entries
@@ -525,6 +527,8 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(ProbPlain<MR> pb, const ui
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nsb = K / QK_K;
     const int wg = blockIdx.x;
+    if (!pb.active(wg)) return;            // workgroup-uniform: past a data-dependent grid end
+    const uint16_t* __restrict__ X = pb.act(wg, X0);
     uint8_t* wA = s_act + (uint32_t)w * kWave;
     float* wS = (float*)(wA + kEnt);
     const int kb0 = w * BPK;
@@ -641,15 +645,15 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(ProbPlain<MR> pb, const ui
     pb.finish(wg, red, KP, tid);
 }
 
-template <int MR>
-hipError_t run_gemvm(const ProbPlain<MR>& pb, int nsb, unsigned nwg, const uint16_t* x, int K, hipStream_t st) {
+template <int MR, class Prob>
+hipError_t run_gemvm(const Prob& pb, int nsb, unsigned nwg, const uint16_t* x, int K, hipStream_t st) {
     // KP waves of BPK blocks: the largest KP <= 8 that divides nsb with a supported BPK
     for (int kp = kMaxW; kp >= 1; --kp) {
         if (nsb % kp || 64 * kp < kTR * MR) continue;   // the final reduction uses kTR * MR threads
         const int bpk = nsb / kp;
         const dim3 grid(nwg), block(64 * kp);
 #define AIPU_LM(B)                                                                       \
-    case B: hipLaunchKernelGGL((k_gemvm<MR, B>), grid, block, 0, st, pb, x, K, kp); return hipGetLastError();
+    case B: hipLaunchKernelGGL((k_gemvm<MR, B, Prob>), grid, block, 0, st, pb, x, K, kp); return hipGetLastError();
         switch (bpk) {
             AIPU_LM(1)
             AIPU_LM(2)
@@ -875,6 +879,99 @@ hipError_t launch_moe_down_mfma(const uint8_t* D, const uint8_t* shD, const int3
     shared.acc_in = acc_scratch;
     shared.resid = resid;
     return down_once(shared, I, h + (int64_t)topk * I, st);
+}
+
+// ------------------------------------------- batched MoE over the expert union (M = 2..8)
+// Slot u of the union holds expert uidx[u] (-1 = the shared expert); *nslots of the grid's
+// slots are live, the rest of the workgroups return at once.  Gate/up: workgroup
+// ((u * 2 + part) * itiles + it) computes rows it*16.. of the gate (part 0) or up (part 1)
+// projection of slot u for all M rows -> gu[u][part][m][i].  Down: workgroup (u * htiles +
+// it) computes output rows it*16.. of slot u against h[u][m][:] -> y[u][m][d].
+template <int MR>
+struct ProbUGateUp {
+    const uint8_t *G, *U, *shG, *shU;
+    const int32_t* uidx;
+    const int32_t* nslots;
+    int itiles, M;
+    int64_t rb, ebytes, I;
+    uint16_t* gu;
+    static constexpr bool kRoutes = false;
+    __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
+    __device__ bool active(int wg) const { return wg / (2 * itiles) < *nslots; }
+    __device__ const uint16_t* act(int, const uint16_t* X) const { return X; }
+    __device__ TileRef tile(int wg, int) const {
+        const int u = wg / (2 * itiles), part = (wg / itiles) & 1, it = wg % itiles;
+        const int e = __builtin_amdgcn_readfirstlane(uidx[u]);
+        const uint8_t* base = e < 0 ? (part ? shU : shG) : (part ? U : G) + (int64_t)e * ebytes;
+        return TileRef{base + (int64_t)it * kTR * rb, kTR, 0};
+    }
+    __device__ void finish(int wg, const float* red, int KP, int tid) const {
+        if (tid >= kTR * MR) return;
+        const int n = tid / MR, r = tid % MR;
+        if (r >= M) return;
+        const int u = wg / (2 * itiles), part = (wg / itiles) & 1, it = wg % itiles;
+        float v = 0.f;
+        for (int k = 0; k < KP; ++k) v += red[(k * kTR + n) * MR + r];
+        gu[(((int64_t)u * 2 + part) * M + r) * I + (int64_t)it * kTR + n] = (uint16_t)bf16_rne(v);
+    }
+};
+
+template <int MR>
+struct ProbUDown {
+    const uint8_t *D, *shD;
+    const int32_t* uidx;
+    const int32_t* nslots;
+    int htiles, M;
+    int64_t rb, ebytes, I, H;
+    const uint16_t* h;
+    uint16_t* y;
+    static constexpr bool kRoutes = false;
+    __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
+    __device__ bool active(int wg) const { return wg / htiles < *nslots; }
+    __device__ const uint16_t* act(int wg, const uint16_t*) const { return h + (int64_t)(wg / htiles) * M * I; }
+    __device__ TileRef tile(int wg, int) const {
+        const int u = wg / htiles, it = wg % htiles;
+        const int e = __builtin_amdgcn_readfirstlane(uidx[u]);
+        const uint8_t* base = e < 0 ? shD : D + (int64_t)e * ebytes;
+        const int64_t nv = H - (int64_t)it * kTR;
+        return TileRef{base + (int64_t)it * kTR * rb, (int)(nv < kTR ? nv : kTR), 0};
+    }
+    __device__ void finish(int wg, const float* red, int KP, int tid) const {
+        if (tid >= kTR * MR) return;
+        const int n = tid / MR, r = tid % MR;
+        const int u = wg / htiles, it = wg % htiles;
+        const int64_t d = (int64_t)it * kTR + n;
+        if (r >= M || d >= H) return;
+        float v = 0.f;
+        for (int k = 0; k < KP; ++k) v += red[(k * kTR + n) * MR + r];
+        y[((int64_t)u * M + r) * H + d] = (uint16_t)bf16_rne(v);
+    }
+};
+
+bool moe_union_supported(int64_t H, int64_t I, int M) {
+    const int mr = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
+    return M >= 2 && M <= 8 && I % kTR == 0 && gemvm_supported((int)(H / QK_K), mr) &&
+           gemvm_supported((int)(I / QK_K), mr);
+}
+
+template <int MR>
+static hipError_t union_gemvs(const MoeUnionArgs& a, hipStream_t st) {
+    const int64_t rbH = row_bytes(T_Q4_K, a.H), rbI = row_bytes(T_Q4_K, a.I);
+    const int itiles = (int)(a.I / kTR), htiles = (int)((a.H + kTR - 1) / kTR);
+    const ProbUGateUp<MR> pg{a.G, a.U, a.shG, a.shU, a.uidx, a.nslots, itiles, a.M, rbH, rbH * a.I, a.I, a.gu};
+    hipError_t e = run_gemvm<MR>(pg, (int)(a.H / QK_K), (unsigned)(a.max_slots * 2 * itiles), a.x, (int)a.H, st);
+    if (e != hipSuccess) return e;
+    e = a.after_gateup(st);
+    if (e != hipSuccess) return e;
+    const ProbUDown<MR> pd{a.D, a.shD, a.uidx, a.nslots, htiles, a.M, rbI, rbI * a.H, a.I, a.H, a.h, a.y};
+    return run_gemvm<MR>(pd, (int)(a.I / QK_K), (unsigned)(a.max_slots * htiles), a.h, (int)a.I, st);
+}
+
+hipError_t launch_moe_union_mfma(const MoeUnionArgs& a, hipStream_t st) {
+    if (!moe_union_supported(a.H, a.I, a.M)) return hipErrorInvalidValue;
+    if (a.M <= 2) return union_gemvs<2>(a, st);
+    if (a.M <= 4) return union_gemvs<4>(a, st);
+    return union_gemvs<8>(a, st);
 }
 
 bool moe_mfma_supported(int nslots, int64_t H, int64_t I) {

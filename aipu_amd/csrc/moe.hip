@@ -74,6 +74,22 @@ __global__ void k_combine(const uint16_t* __restrict__ ys, const uint16_t* __res
     }
 }
 
+// Reorder the routing decision (sel, selw) by ascending expert index (one thread; topk <= 32).
+__global__ void k_sort_slots(int32_t* sel, uint16_t* selw, int topk) {
+    if (threadIdx.x != 0) return;
+    for (int i = 1; i < topk; ++i) {
+        const int32_t e = sel[i];
+        const uint16_t w = selw[i];
+        int j = i - 1;
+        for (; j >= 0 && sel[j] > e; --j) {
+            sel[j + 1] = sel[j];
+            selw[j + 1] = selw[j];
+        }
+        sel[j + 1] = e;
+        selw[j + 1] = w;
+    }
+}
+
 inline int blocks_for(int64_t n) {
     int64_t b = (n + 255) / 256;
     return (int)(b < 1 ? 1 : (b > 4096 ? 4096 : b));
@@ -111,7 +127,7 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
 
     // 2-3. fast path: the gate/up kernel routes from the logits in every workgroup and
     // publishes the decision for the down kernel (no separate router-tail launch)
-    if (fast && moe_mfma_supported(nslots, a.H, a.I) && moe_route_in_kernel(a.E, a.topk)) {
+    if (fast && !a.ascending && moe_mfma_supported(nslots, a.H, a.I) && moe_route_in_kernel(a.E, a.topk)) {
         const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};
         AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
                                         a.I, a.x, h, st));
@@ -121,6 +137,10 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
     // 2. router tail (one wave), then the experts
     AIPU_TRY(launch_router_tail(logits, (int)a.E, a.topk, a.scale_bits, sel, selw, nullptr, st, a.sel_idx_out,
                                 a.sel_w_out));
+    if (a.ascending) {   // batched-row semantics: experts combined in ascending index order
+        hipLaunchKernelGGL(k_sort_slots, dim3(1), dim3(64), 0, st, sel, selw, a.topk);
+        AIPU_TRY(hipGetLastError());
+    }
     if (fast && moe_mfma_supported(nslots, a.H, a.I)) {
         const MoeRoute route{sel, nullptr, 0u, nullptr, nullptr, nullptr, nullptr};
         AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,

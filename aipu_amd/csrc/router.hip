@@ -67,6 +67,17 @@ __global__ __launch_bounds__(64) void k_router_tail(const uint16_t* __restrict__
     router_tail_wave(logits, E, topk, scale_bits, sel, selw, sel2, selw2, gates, keys, win);
 }
 
+// One routing decision per activation row (row = workgroup).
+__global__ __launch_bounds__(64) void k_router_tail_rows(const uint16_t* __restrict__ logits, int E, int topk,
+                                                         uint32_t scale_bits, int32_t* sel, uint16_t* selw,
+                                                         int32_t* sel2, uint16_t* selw2) {
+    __shared__ uint32_t keys[kMaxE];
+    __shared__ uint32_t win[kMaxTopk];
+    const int r = blockIdx.x;
+    router_tail_wave(logits + (int64_t)r * E, E, topk, scale_bits, sel + r * topk, selw + r * topk,
+                     sel2 ? sel2 + r * topk : nullptr, selw2 ? selw2 + r * topk : nullptr, nullptr, keys, win);
+}
+
 // bf16 router GEMV: workgroup e computes logit e (256 threads split K; fixed-order
 // reduction) and writes it as bf16.
 constexpr int kRouterThreads = 256;
@@ -105,6 +116,13 @@ hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t 
                               uint16_t* sel_w, uint16_t* gates, hipStream_t st, int32_t* sel2, uint16_t* selw2) {
     hipLaunchKernelGGL(k_router_tail, dim3(1), dim3(64), 0, st, logits, E, topk, scale_bits, sel_idx, sel_w, gates,
                        sel2, selw2);
+    return hipGetLastError();
+}
+
+hipError_t launch_router_tail_rows(const uint16_t* logits, int M, int E, int topk, uint32_t scale_bits, int32_t* sel,
+                                   uint16_t* selw, int32_t* sel2, uint16_t* selw2, hipStream_t st) {
+    hipLaunchKernelGGL(k_router_tail_rows, dim3(M), dim3(64), 0, st, logits, E, topk, scale_bits, sel, selw, sel2,
+                       selw2);
     return hipGetLastError();
 }
 

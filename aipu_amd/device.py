@@ -200,6 +200,35 @@ def moe_swiglu_decode(router_type, router_w, ggml_type, gate_exps, up_exps, down
     return y, sel, sw
 
 
+def moe_batched_workspace(E, H, I, topk, device):
+    """Zero-filled workspace for moe_swiglu_decode_batched."""
+    n = _lib.lib().aipu_moe_batched_workspace_bytes(E, H, I, topk)
+    if n < 0:
+        raise ValueError("bad MoE shape")
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def moe_swiglu_decode_batched(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, E, H, I, topk, x,
+                              mode="fast", shared=None, scale_bits=RSCALE_BITS, workspace=None, out=None):
+    """MoE decode step for x[M, H]: per-row routing, union of experts evaluated once, each row
+    combining its experts in ascending index (M > 1).  Returns (y [M, H], sel [M, topk],
+    sel_w [M, topk])."""
+    _need_cuda(router_w, gate_exps, up_exps, down_exps, x)
+    x = _bf16(x)
+    if x.dim() == 1:
+        x = x[None]
+    M = x.shape[0]
+    ws = workspace if workspace is not None else moe_batched_workspace(E, H, I, topk, x.device)
+    y = out if out is not None else torch.empty((M, H), dtype=torch.bfloat16, device=x.device)
+    sel = torch.empty((M, topk), dtype=torch.int32, device=x.device)
+    sw = torch.empty((M, topk), dtype=torch.bfloat16, device=x.device)
+    sg, su, sd = shared if shared is not None else (None, None, None)
+    call("aipu_moe_swiglu_decode_batched", router_type, _ptr(router_w), ggml_type, _ptr(gate_exps), _ptr(up_exps),
+         _ptr(down_exps), _ptr(sg), _ptr(su), _ptr(sd), E, H, I, topk, scale_bits, _ptr(x), M, _ptr(y), _ptr(sel),
+         _ptr(sw), _mode(mode), _ptr(ws), ws.numel(), _stream(x))
+    return y, sel, sw
+
+
 def rmsnorm(x, gamma, mode="fast", out=None):
     """y = bf16((x * inv) * gamma), inv = fp32_rsqrt(mean(x^2) + 1e-5) (ref: element-order sum)."""
     _need_cuda(x, gamma)

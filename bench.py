@@ -251,6 +251,42 @@ def bench_layer(dev, torch, steps=200, E=256, H=6144, I=2048, topk=8):
     return res
 
 
+def bench_batched(dev, torch, steps=100, E=256, H=6144, I=2048, topk=8, Ms=(2, 4, 8)):
+    """Next-row F3: the batched MoE step at the config-2 shape for M rows -- the union of the
+    rows' experts evaluated once (its weights streamed once for all rows)."""
+    device = "cuda"
+    gen = torch.Generator(device=device)
+    gen.manual_seed(97)
+    ge = gen_q4k(E * I, H, gen, device)
+    ue = gen_q4k(E * I, H, gen, device)
+    de = gen_q4k(E * H, I, gen, device)
+    rw = (torch.randn((E, H), device=device, generator=gen) * 0.05).to(torch.bfloat16)
+    res = {}
+    for M in Ms:
+        nx = 16
+        X = (torch.randn((nx, M, H), device=device, generator=gen) * 0.05).to(torch.bfloat16)
+        Y = torch.empty((M, H), dtype=torch.bfloat16, device=device)
+        ws = dev.moe_batched_workspace(E, H, I, topk, device)
+        unions = []
+        for j in range(nx):
+            _, sel, _ = dev.moe_swiglu_decode_batched(BF16, rw, Q4K, ge, ue, de, E, H, I, topk, X[j], workspace=ws,
+                                                      out=Y)
+            unions.append(len(set(sel.cpu().numpy().reshape(-1).tolist())))
+        fns = [(lambda j=i % nx: dev.moe_swiglu_decode_batched(BF16, rw, Q4K, ge, ue, de, E, H, I, topk, X[j],
+                                                                 workspace=ws, out=Y)) for i in range(steps)]
+        ms, _ = time_graph(fns, reps=3)
+        us = min(ms) * 1000.0 / steps
+        u = float(sum(unions)) / len(unions)
+        alg = u * 3 * q4k_bytes(I, H) + E * H * 2 + 2 * M * H * 2
+        res[f"m{M}"] = dict(M=M, us_per_step=us, us_per_row=us / M, mean_union=u, alg_bytes=alg,
+                            gbs=alg / (us * 1e-6) / 1e9)
+        log(f"batched MoE M={M}: {us:.1f} us ({us / M:.1f} us/row), union {u:.1f} experts, "
+            f"{res[f'm{M}']['gbs']:.0f} GB/s")
+    del ge, ue, de
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_tiles(dev, torch, steps=50):
     """24 column tiles of 256 rows cycling Q4_K, Q6_K, Q8_0, F16 at K=6144."""
     import numpy as np
@@ -461,7 +497,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of one HIP graph")
-    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1", "lmhead", "layer"], default=None,
+    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1", "lmhead", "layer", "batched"], default=None,
                     help="run one measurement only (for kernel tracing / counter runs)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
                     help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into "
@@ -501,6 +537,9 @@ def main():
     if args.only == "prefill":
         print(json.dumps(bench_prefill(dev, torch)))
         return
+    if args.only == "batched":
+        print(json.dumps(bench_batched(dev, torch)))
+        return
     if args.only == "layer":
         print(json.dumps(bench_layer(dev, torch)))
         return
@@ -536,6 +575,7 @@ def main():
         log(f"prefill: {extra['prefill_c4']['ms']:.2f} ms, {extra['prefill_c4']['tflops']:.1f} TFLOP/s")
         extra["lm_head_f4"] = bench_lmhead(dev, torch)
         extra["moe_layer_f2"] = bench_layer(dev, torch)
+        extra["moe_batched_f3"] = bench_batched(dev, torch)
         log(f"lm head: {extra['lm_head_f4']['us']:.1f} us, {extra['lm_head_f4']['gbs']:.0f} GB/s")
     cpu = None if args.no_cpu else cpu_baseline()
 

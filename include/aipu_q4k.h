@@ -151,6 +151,23 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
                            int32_t* sel_idx, uint16_t* sel_w, int mode, void* workspace,
                            int64_t ws_bytes, void* stream);
 
+/* MoE decode step for M activation rows x[M][H] -> y[M][H], routing per row
+ * (sel_idx[M][topk], sel_w[M][topk], nullable, in each row's router order).  M = 1 is
+ * aipu_moe_swiglu_decode (routed experts combined in slot order).  M > 1 follows the
+ * union-skip batch of src/glm_decoder_block_q4k.v:530-560,836-906: the union of the rows'
+ * experts is evaluated once, in ascending expert index, and each row accumulates
+ * facc += f32(gate * bf16(y_e)) for its own experts in that order, then the shared expert
+ * with weight 1.  Workspace: aipu_moe_batched_workspace_bytes(E, H, I, topk), zero-filled
+ * before first use; other arguments as aipu_moe_swiglu_decode. */
+int64_t aipu_moe_batched_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
+int aipu_moe_swiglu_decode_batched(int router_type, const void* router_w, int ggml_type,
+                                   const void* gate_exps, const void* up_exps, const void* down_exps,
+                                   const void* shared_gate, const void* shared_up,
+                                   const void* shared_down, int64_t E, int64_t H, int64_t I,
+                                   int topk, uint32_t scale_bits, const uint16_t* x, int64_t M,
+                                   uint16_t* y, int32_t* sel_idx, uint16_t* sel_w, int mode,
+                                   void* workspace, int64_t ws_bytes, void* stream);
+
 /* RMSNorm of one bf16 vector: inv = fp32_rsqrt(f32(f32(sumsq * recip_fp32(n)) + 1e-5)),
  * y[i] = bf16(f32(f32(x[i] * inv) * gamma[i])).  Replaces rmsnorm
  * (tools/glm_model_q4k_ref.py:451-465, recip_fp32 :434-449; RTL src/rmsnorm_unit.v).

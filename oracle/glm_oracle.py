@@ -15,6 +15,9 @@ Imported only by ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 * ``rmsnorm``              -- ``:451-465`` with ``_recip_fp32`` ``:434-449`` (element-order fp32
   sum of squares, ``inv = rsqrt(sumsq*recip(n) + 1e-5)``, ``bf16((x*inv)*gamma)``)
 * MoE decoder FFN half     -- ``:797-810`` (rmsnorm -> MoE step -> residual ``bf16(h + fbuf)``)
+* batched MoE (M rows)     -- ``src/glm_decoder_block_q4k.v:530-560,836-906``: per-row routing;
+  for M > 1 each row combines its own experts in ascending expert index (union-skip scan),
+  shared expert last with weight 1; M = 1 keeps the slot order of ``:797-809``
 * LM head                  -- ``:476-486`` (``matmul_bf16_dot``: 7 round-robin fp32 partial
   sums, fixed add tree) and the argmax scan of ``model_forward`` ``:826-834`` with
   ``bf16_gt`` ``:138-148``
@@ -437,3 +440,28 @@ def moe_layer_ref(h_bits, gamma_bits, router_type, router_w, experts, ggml_type,
     with np.errstate(over="ignore", invalid="ignore"):
         y = qo.bf16_round_bits(hf + qo.bf16_bits_to_f32(r["y"]))
     return dict(y=y, nrm=nrm, fbuf=r["y"], sel_idx=r["sel_idx"], sel_w=r["sel_w"])
+
+
+def moe_decode_batched_ref(X_bits, router_type, router_w, experts, ggml_type, E, H, I, topk,
+                           scale_bits=0x40200000, shared=None):
+    """MoE step for M rows.  Returns dict(y [M][H], sel_idx [M][topk], sel_w [M][topk]) with
+    the routing in each row's router order."""
+    X = np.atleast_2d(np.asarray(X_bits, np.uint16))
+    M = X.shape[0]
+    ge, ue, de = (np.asarray(a, np.uint8).reshape(E, -1) for a in experts)
+    ysh_cache = {}
+    Y = np.zeros((M, H), np.uint16)
+    S = np.zeros((M, topk), np.int32)
+    W = np.zeros((M, topk), np.uint16)
+    for r in range(M):
+        x = X[r]
+        logits = router_logits(router_type, router_w, E, H, x)
+        sel, sel_w, _ = router_tail(logits, topk, scale_bits)
+        S[r], W[r] = sel, sel_w
+        order = list(range(topk)) if M == 1 else sorted(range(topk), key=lambda t: int(sel[t]))
+        ys = [swiglu_expert(x, ge[sel[t]], ue[sel[t]], de[sel[t]], ggml_type, H, I)[0] for t in order]
+        ysh = None
+        if shared is not None:
+            ysh, _ = swiglu_expert(x, shared[0], shared[1], shared[2], ggml_type, H, I)
+        Y[r], _ = moe_combine(np.asarray(sel_w)[order], ys, ysh)
+    return dict(y=Y, sel_idx=S, sel_w=W)
