@@ -26,6 +26,9 @@ hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t 
 // bf16 router GEMV: logits[e] = bf16(W[e] . x), one workgroup per expert.
 hipError_t launch_router_bf16_logits(const uint16_t* W, const uint16_t* x, int64_t K, int E, uint16_t* logits,
                                      hipStream_t st);
+// The same for M <= 8 rows x[M][K] -> logits[M][E] (router rows read once).
+hipError_t launch_router_bf16_logits_rows(const uint16_t* W, const uint16_t* x, int64_t K, int E, int M,
+                                          uint16_t* logits, hipStream_t st);
 
 // gemv_ref.hip -- bit-exact reference order
 hipError_t launch_gemv_ref(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,

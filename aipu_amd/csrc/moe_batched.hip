@@ -165,9 +165,7 @@ hipError_t fast_pass(const MoeArgs& a, int64_t r0, int M, const BLayout& L, hipS
 
     // router logits [M][E]
     if (a.router_type == T_BF16) {
-        for (int m = 0; m < M; ++m)
-            AIPU_TRY(launch_router_bf16_logits((const uint16_t*)a.router_w, x + (int64_t)m * a.H, a.H, (int)a.E,
-                                               logits + (int64_t)m * a.E, st));
+        AIPU_TRY(launch_router_bf16_logits_rows((const uint16_t*)a.router_w, x, a.H, (int)a.E, M, logits, st));
     } else if (a.router_type == T_Q4_K && gemv_mfma_supported(a.E, a.H, M)) {
         AIPU_TRY(launch_gemv_mfma(a.router_w, a.E, a.H, x, M, logits, nullptr, a.E, st));
     } else {

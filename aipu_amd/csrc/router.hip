@@ -110,7 +110,54 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_logits(const uint16_t
     }
 }
 
+// bf16 router GEMV for M <= 8 activation rows: workgroup e reads router row e once and forms
+// logit e of every row (same per-row arithmetic as k_router_logits).
+template <int MR>
+__global__ __launch_bounds__(kRouterThreads) void k_router_logits_rows(const uint16_t* __restrict__ W,
+                                                                       const uint16_t* __restrict__ x, int64_t K,
+                                                                       int M, int E, uint16_t* __restrict__ logits) {
+    __shared__ float wsum[MR][kRouterThreads / 64];
+    const int t = threadIdx.x, e = blockIdx.x;
+    const uint16_t* row = W + (int64_t)e * K;
+    float s0[MR], s1[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) s0[m] = s1[m] = 0.f;
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    for (int64_t c = (int64_t)t * 8; c < K; c += kRouterThreads * 8) {
+        const uint4 w = *(const uint4*)(row + c);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            if (m >= M) break;
+            const uint4 a = *(const uint4*)(x + (int64_t)m * K + c);
+            s0[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.x), __builtin_bit_cast(bf2, w.x), s0[m], false);
+            s1[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.y), __builtin_bit_cast(bf2, w.y), s1[m], false);
+            s0[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.z), __builtin_bit_cast(bf2, w.z), s0[m], false);
+            s1[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w), __builtin_bit_cast(bf2, w.w), s1[m], false);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        float v = s0[m] + s1[m];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if ((t & 63) == 0) wsum[m][t >> 6] = v;
+    }
+    __syncthreads();
+    if (t < M) {
+        float tot = 0.f;
+        for (int w = 0; w < kRouterThreads / 64; ++w) tot += wsum[t][w];
+        logits[(int64_t)t * E + e] = (uint16_t)bf16_rne(tot);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_router_bf16_logits_rows(const uint16_t* W, const uint16_t* x, int64_t K, int E, int M,
+                                          uint16_t* logits, hipStream_t st) {
+    if (M < 1 || M > 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_router_logits_rows<8>, dim3(E), dim3(kRouterThreads), 0, st, W, x, K, M, E, logits);
+    return hipGetLastError();
+}
 
 hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t scale_bits, int32_t* sel_idx,
                               uint16_t* sel_w, uint16_t* gates, hipStream_t st, int32_t* sel2, uint16_t* selw2) {

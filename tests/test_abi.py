@@ -158,7 +158,7 @@ def test_error_raises_with_message():
 def test_lm_head_validation():
     f = L().aipu_lm_head
     wsb = L().aipu_lm_head_workspace_bytes
-    assert wsb(154880) == 2420 * 8                  # one 8-byte (key, index) pair per 64-row wave
+    assert wsb(154880) == 4303 * 8                  # one 8-byte (key, index) pair per 36-row workgroup
     assert wsb(65) == 16 and wsb(0) < 0
     need = wsb(1000)
     assert f(NULL, 1000, 64, FAKE, FAKE, FAKE, FAKE, need, S) == ARG
