@@ -48,6 +48,7 @@ struct ProbPlain {
     int64_t ystride;   // N of the full output (tiles of a mixed call write a column slice)
     int M;
     static constexpr bool kRoutes = false;
+    static constexpr bool kShareAct = false;
     static constexpr int kRows = MR;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int) const { return true; }
@@ -88,6 +89,9 @@ struct ProbGateUp {
     int64_t I;
     int eid;   // expert of this workgroup's slot (setup)
     static constexpr bool kRoutes = true;
+    // the gate and up tiles of a workgroup read the same activations: the two waves of each
+    // K part share one staging slot (written by the gate wave)
+    static constexpr bool kShareAct = true;
     __device__ void setup(int wg, uint32_t* keys, uint32_t* win, int32_t* sel, uint16_t* selw) {
         const int s = wg / itiles;
         if (route.logits) {
@@ -144,6 +148,7 @@ struct ProbDown {
     float* acc_out = nullptr;
     const uint16_t* resid = nullptr;
     static constexpr bool kRoutes = false;
+    static constexpr bool kShareAct = false;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ TileRef tile(int wg, int t) const {
         const int64_t d0 = (int64_t)wg * kTR;
@@ -398,7 +403,8 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     // do not alias weight loads still in flight and does not make them wait for those.
     constexpr int kBpkMax = 2 * XI;             // activation pieces per wave <= 64 * XI
     constexpr uint32_t kActWave = kBpkMax * 544;
-    __shared__ __align__(16) uint8_t s_act[kMaxW * kActWave];
+    constexpr int kSlots = Prob::kShareAct ? kMaxW / 2 : kMaxW;   // activation staging slots
+    __shared__ __align__(16) uint8_t s_act[kSlots * kActWave];
     __shared__ float red[kMaxW * kTR];
     extern __shared__ __align__(16) uint8_t s_w[];
     const int BPK = GS * NG;
@@ -408,8 +414,6 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: the copies take a scalar LDS base
     const int nsb = K / QK_K;
     const int wg = blockIdx.x;
-    uint8_t* wA = s_act + (uint32_t)w * kActWave;
-    float* wS = (float*)(wA + kA);
     uint8_t* wW = s_w + (uint32_t)w * Dma<GS>::kBytes;
 
     Prob pb = pb0;
@@ -424,6 +428,9 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     const TileRef tr = pb.tile(wg, tt);
     const int kb0 = kp * BPK;
     const int64_t rb = (int64_t)nsb * 144;
+    uint8_t* wA = s_act + (uint32_t)(Prob::kShareAct ? kp : w) * kActWave;
+    float* wS = (float*)(wA + kA);
+    const bool stager = !Prob::kShareAct || tt == 0;
 
     // 1. this wave's activations, then 2. its first group of weights
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, xbytes);
@@ -432,13 +439,15 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
         const int q = lane + 64 * i;
-        xv[i] = buf_load16(xr, q < XP ? xbase + 16u * q : kOOB);
+        xv[i] = buf_load16(xr, q < XP && stager ? xbase + 16u * q : kOOB);
     }
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
     dma_group<GS>(wr, wW, rb, kb0, lane);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. stage: A entries, sums
+    // 3. stage: A entries, sums (with shared slots, the gate waves stage for both tiles and
+    // an LDS-only barrier -- the weight copies stay in flight -- publishes them)
+    if (stager) {
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
         const int q = lane + 64 * i;
@@ -456,6 +465,8 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
             if ((q & 3) == 0) wS[(bb * 4 + gg) * 2 + ((q >> 2) & 1)] = sm;
         }
     }
+    }
+    if constexpr (Prob::kShareAct) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // 4. block loop
     const int n = lane & 15, g = lane >> 4;
@@ -718,10 +729,13 @@ struct Plan1 {
 constexpr int64_t kMaxLds1 = 80 * 1024;   // two workgroups per CU
 
 int dma_bytes(int gs) { return ((16 * 9 * gs + 63) / 64) * 1024; }
-// static LDS of k_gemv1<GS, XI>: zero region, activation slices, reduction
-int64_t static_lds1(int xi) { return (int64_t)kMaxW * 2 * xi * 544 + kMaxW * kTR * 4; }
+// static LDS of k_gemv1<GS, XI>: activation slices (one per wave, or one per K part when the
+// tiles of a workgroup share them), reduction
+int64_t static_lds1(int xi, bool share) {
+    return (int64_t)(share ? kMaxW / 2 : kMaxW) * 2 * xi * 544 + kMaxW * kTR * 4;
+}
 
-bool make_plan1(int nsb, int T, int kp_max, Plan1& p) {
+bool make_plan1(int nsb, int T, int kp_max, Plan1& p, bool share = false) {
     for (int kp = (kp_max < kMaxW / T ? kp_max : kMaxW / T); kp >= 1; --kp) {
         if (nsb % kp) continue;
         const int bpk = nsb / kp;
@@ -732,7 +746,7 @@ bool make_plan1(int nsb, int T, int kp_max, Plan1& p) {
             if (bpk % gs) continue;
             const int W = T * kp;
             const int64_t lds = (int64_t)W * dma_bytes(gs);
-            if (lds + static_lds1(xi) > kMaxLds1) continue;
+            if (lds + static_lds1(xi, share) > kMaxLds1) continue;
             p = Plan1{kp, gs, bpk / gs, xi, W, lds};
             return true;
         }
@@ -839,7 +853,7 @@ hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint
     const ProbGateUp pb{G, U, shG, shU, route, topk, (int)E, (int)(I / kTR), rb, rb * I, h, I, 0};
     const unsigned nwg = (unsigned)(nslots * (I / kTR));
     Plan1 p1;
-    if (make_plan1(nsb, 2, 4, p1) && p1.W * 64 >= (route.logits ? (int)((E + 7) & ~7) : 0))
+    if (make_plan1(nsb, 2, 4, p1, true) && p1.W * 64 >= (route.logits ? (int)((E + 7) & ~7) : 0))
         return run1(pb, p1, nwg, x, 0, H * 2, (int)H, st);
     Plan pl;
     if (!make_plan(nsb, 2, 1, 1, 4, pl) || pl.W * 64 < (route.logits ? (int)((E + 7) & ~7) : 0)) return hipErrorInvalidValue;
@@ -896,6 +910,7 @@ struct ProbUGateUp {
     int64_t rb, ebytes, I;
     uint16_t* gu;
     static constexpr bool kRoutes = false;
+    static constexpr bool kShareAct = false;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int wg) const { return wg / (2 * itiles) < *nslots; }
     __device__ const uint16_t* act(int, const uint16_t* X) const { return X; }
@@ -926,6 +941,7 @@ struct ProbUDown {
     const uint16_t* h;
     uint16_t* y;
     static constexpr bool kRoutes = false;
+    static constexpr bool kShareAct = false;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int wg) const { return wg / htiles < *nslots; }
     __device__ const uint16_t* act(int wg, const uint16_t*) const { return h + (int64_t)(wg / htiles) * M * I; }

@@ -90,13 +90,29 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_logits(const uint16_t
     const uint16_t* row = W + (int64_t)e * K;
     float s0 = 0.f, s1 = 0.f;
     typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-    for (int64_t c = (int64_t)t * 8; c < K; c += kRouterThreads * 8) {
-        const uint4 w = *(const uint4*)(row + c);
-        const uint4 a = *(const uint4*)(x + c);
-        s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.x), __builtin_bit_cast(bf2, w.x), s0, false);
-        s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.y), __builtin_bit_cast(bf2, w.y), s1, false);
-        s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.z), __builtin_bit_cast(bf2, w.z), s0, false);
-        s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w), __builtin_bit_cast(bf2, w.w), s1, false);
+    // four chunks' loads are issued before any is used (K = 6144 is three chunks per thread);
+    // each thread still folds its chunks into s0 / s1 in increasing K
+    constexpr int kU = 4;
+    for (int64_t c0 = (int64_t)t * 8; c0 < K; c0 += kU * kRouterThreads * 8) {
+        uint4 wv[kU], av[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t c = c0 + (int64_t)u * kRouterThreads * 8;
+            if (c < K) {
+                wv[u] = *(const uint4*)(row + c);
+                av[u] = *(const uint4*)(x + c);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t c = c0 + (int64_t)u * kRouterThreads * 8;
+            if (c >= K) break;
+            const uint4 w = wv[u], a = av[u];
+            s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.x), __builtin_bit_cast(bf2, w.x), s0, false);
+            s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.y), __builtin_bit_cast(bf2, w.y), s1, false);
+            s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.z), __builtin_bit_cast(bf2, w.z), s0, false);
+            s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w), __builtin_bit_cast(bf2, w.w), s1, false);
+        }
     }
     float v = s0 + s1;
 #pragma unroll
