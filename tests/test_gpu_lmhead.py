@@ -3,8 +3,9 @@ against the C oracle (tools/glm_model_q4k_ref.py:476-486 summation order, :826-8
 with bf16_gt :138-148), including the full vocabulary x MODEL_DIM shape (154,880 x 6,144,
 1.9 GB of bf16 rows) checked on every row.
 
-Shapes cover K below, at and between chunk sizes of the kernel (56 bf16 per chunk; tails of
-8..48), vocabularies that end inside a 64-row wave, the order-sensitive cases the oracle is
+Shapes cover K below, at and between the chunk sizes of both kernels (448 bf16 per chunk for
+K <= 6720, 224 for the lane-per-row kernel used above that; ragged tails), vocabularies that end
+inside a wave or a workgroup, the order-sensitive cases the oracle is
 pinned with, and argmax edge cases (ties, +-0, infinities, NaNs, an all -inf vocabulary).
 """
 import numpy as np
@@ -36,7 +37,9 @@ def _check(w_bits, x_bits, what):
 
 
 @pytest.mark.parametrize("V,K", [(1, 8), (63, 56), (64, 64), (65, 112), (129, 152), (200, 104),
-                                 (1000, 6144), (777, 2048), (130, 4096 + 48)])
+                                 (1000, 6144), (777, 2048), (130, 4096 + 48), (37, 448), (36, 6720),
+                                 # K > 6720 runs the lane-per-row kernel
+                                 (300, 6728), (65, 8192), (130, 12288 + 40)])
 def test_lm_head_shapes(V, K):
     note(f"lm_head V={V} K={K}")
     rng = np.random.default_rng(V * 31 + K)
