@@ -512,8 +512,8 @@ def main():
         summarize_traffic(*args.traffic)
         return
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU sharding is a design "
-              f"note in DESIGN.md, not a measured configuration.", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); sharding across GPUs is "
+              f"designed (rows / experts / vocabulary per GPU) but not a measured configuration.", file=sys.stderr)
         sys.exit(2)
 
     import torch
