@@ -395,9 +395,9 @@ __device__ __forceinline__ void dma_group(__amdgpu_buffer_rsrc_t wr, uint8_t* sl
     }
 }
 
-template <int GS, int XI, class Prob>
+template <int GS, int XI, class Prob, bool kLoop = false>
 __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* __restrict__ X, int64_t xstride,
-                                                      uint32_t xbytes, int K, int KP, int NG) {
+                                                      uint32_t xbytes, int K, int KP, int NG, int tpw) {
     // Separate LDS objects for the direct-to-LDS weight slices (dynamic) and for everything
     // the waves write themselves (static), so the compiler can see that the staging writes
     // do not alias weight loads still in flight and does not make them wait for those.
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     constexpr uint32_t kActWave = kBpkMax * 544;
     constexpr int kSlots = Prob::kShareAct ? kMaxW / 2 : kMaxW;   // activation staging slots
     __shared__ __align__(16) uint8_t s_act[kSlots * kActWave];
-    __shared__ float red[kMaxW * kTR];
+    __shared__ float red[(kLoop ? 2 : 1) * kMaxW * kTR];   // double-buffered across a workgroup's tiles
     extern __shared__ __align__(16) uint8_t s_w[];
     const int BPK = GS * NG;
     const int XP = BPK * 32;
@@ -416,16 +416,20 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     const int wg = blockIdx.x;
     uint8_t* wW = s_w + (uint32_t)w * Dma<GS>::kBytes;
 
+    // A workgroup computes tiles t0 .. t0 + tpw - 1 (tiles that share the routing decision and
+    // the activations); the first weight group of tile t + 1 is copied while tile t finishes.
+    if constexpr (!kLoop) tpw = 1;   // one tile per workgroup: the loop folds away
+    const int t0 = wg * tpw;
     Prob pb = pb0;
     if constexpr (Prob::kRoutes) {   // routing decision (before any weight address is known)
         __shared__ uint32_t r_keys[kRouteMaxE];
         __shared__ uint32_t r_win[kRouteMaxTopk];
         __shared__ int32_t r_sel[kRouteMaxTopk];
         __shared__ uint16_t r_selw[kRouteMaxTopk];
-        pb.setup(wg, r_keys, r_win, r_sel, r_selw);
+        pb.setup(t0, r_keys, r_win, r_sel, r_selw);
     }
     const int tt = w / KP, kp = w - tt * KP;
-    const TileRef tr = pb.tile(wg, tt);
+    const TileRef tr = pb.tile(t0, tt);
     const int kb0 = kp * BPK;
     const int64_t rb = (int64_t)nsb * 144;
     uint8_t* wA = s_act + (uint32_t)(Prob::kShareAct ? kp : w) * kActWave;
@@ -441,7 +445,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
         const int q = lane + 64 * i;
         xv[i] = buf_load16(xr, q < XP && stager ? xbase + 16u * q : kOOB);
     }
-    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
+    __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
     dma_group<GS>(wr, wW, rb, kb0, lane);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -476,37 +480,48 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     const HdrSel hs = hdr_sel(g);
     const CodeK ck = code_k();
     const uint32_t rrow = (uint32_t)n * (144u * GS);
-    float acc = 0.f;
     f32x4_t dlo = {0.f, 0.f, 0.f, 0.f}, dhi = {0.f, 0.f, 0.f, 0.f};
-    for (int gi = 0; gi < NG; ++gi) {
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);    // this group's weights are in LDS
-        Raw R[GS];
+    for (int ti = 0; ti < tpw; ++ti) {
+        const int t = t0 + ti;
+        float acc = 0.f;
+        for (int gi = 0; gi < NG; ++gi) {
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);    // this group's weights are in LDS
+            Raw R[GS];
 #pragma unroll
-        for (int bb = 0; bb < GS; ++bb) {
-            const uint8_t* p = wW + rrow + 144u * bb;
-            R[bb].h = *(const uint4*)p;
-            R[bb].q0 = *(const uint4*)(p + 16 + 32 * g);
-            R[bb].q1 = *(const uint4*)(p + 32 + 32 * g);
-        }
-        if (gi + 1 < NG) {
-            regs_consumed(R);   // the slice has been read: refill it
-            dma_group<GS>(wr, wW, rb, kb0 + (gi + 1) * GS, lane);
-        }
+            for (int bb = 0; bb < GS; ++bb) {
+                const uint8_t* p = wW + rrow + 144u * bb;
+                R[bb].h = *(const uint4*)p;
+                R[bb].q0 = *(const uint4*)(p + 16 + 32 * g);
+                R[bb].q1 = *(const uint4*)(p + 32 + 32 * g);
+            }
+            if (gi + 1 < NG) {
+                regs_consumed(R);   // the slice has been read: refill it
+                dma_group<GS>(wr, wW, rb, kb0 + (gi + 1) * GS, lane);
+            } else if (ti + 1 < tpw) {
+                regs_consumed(R);   // the next tile's first group
+                const TileRef tn = pb.tile(t + 1, tt);
+                wr = buf_rsrc(tn.base, (uint32_t)(tn.nvalid * rb));
+                dma_group<GS>(wr, wW, rb, kb0, lane);
+            }
 #pragma unroll
-        for (int bb = 0; bb < GS; ++bb) {
-            const int b = gi * GS + bb;   // block index within this wave's part
-            a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
-            const float2 as = sums_read(wS + (b * 4 + g) * 2);   // no wait on the refill in flight
-            acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
+            for (int bb = 0; bb < GS; ++bb) {
+                const int b = gi * GS + bb;   // block index within this wave's part
+                a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
+                const float2 as = sums_read(wS + (b * 4 + g) * 2);   // no wait on the refill in flight
+                acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
+            }
         }
-    }
 
-    // 5. reduce over the four K-groups, then across the K parts
-    acc += __shfl_xor(acc, 16, 64);
-    acc += __shfl_xor(acc, 32, 64);
-    if (lane < kTR) red[w * kTR + lane] = acc;
-    __syncthreads();
-    pb.finish(wg, red, KP, tid);
+        // 5. reduce over the four K-groups, then across the K parts (an LDS-only barrier: the
+        // next tile's copies stay in flight)
+        acc += __shfl_xor(acc, 16, 64);
+        acc += __shfl_xor(acc, 32, 64);
+        float* rd = red + (ti & 1) * (kMaxW * kTR);
+        if (lane < kTR) rd[w * kTR + lane] = acc;
+        if constexpr (kLoop) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else __syncthreads();
+        pb.finish(t, rd, KP, tid);
+    }
 }
 
 // ------------------------------------------------- small-batch kernel (M = 2 .. 8)
@@ -756,12 +771,16 @@ bool make_plan1(int nsb, int T, int kp_max, Plan1& p, bool share = false) {
 
 template <class Prob>
 hipError_t run1(const Prob& pb, const Plan1& pl, unsigned nwg, const uint16_t* X, int64_t xstride, int64_t xbytes,
-                int K, hipStream_t st) {
+                int K, hipStream_t st, int tpw = 1) {
     const dim3 grid(nwg), block(64 * pl.W);
     const size_t lds = (size_t)pl.lds;
-#define AIPU_L1(GSV, XIV)                                                                                             \
-    hipLaunchKernelGGL((k_gemv1<GSV, XIV, Prob>), grid, block, lds, st, pb, X, xstride, (uint32_t)xbytes, K, pl.KP, \
-                       pl.NG)
+#define AIPU_L1(GSV, XIV)                                                                                      \
+    if (tpw > 1)                                                                                               \
+        hipLaunchKernelGGL((k_gemv1<GSV, XIV, Prob, true>), grid, block, lds, st, pb, X, xstride, (uint32_t)xbytes, \
+                           K, pl.KP, pl.NG, tpw);                                                              \
+    else                                                                                                       \
+        hipLaunchKernelGGL((k_gemv1<GSV, XIV, Prob, false>), grid, block, lds, st, pb, X, xstride,               \
+                           (uint32_t)xbytes, K, pl.KP, pl.NG, 1)
 #define AIPU_L1X(GSV)                        \
     switch (pl.XI) {                         \
         case 2: AIPU_L1(GSV, 2); break;      \
@@ -851,13 +870,28 @@ hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint
     if (route.logits && !moe_route_in_kernel(E, topk)) return hipErrorInvalidValue;
     const int64_t rb = row_bytes(T_Q4_K, H);
     const ProbGateUp pb{G, U, shG, shU, route, topk, (int)E, (int)(I / kTR), rb, rb * I, h, I, 0};
-    const unsigned nwg = (unsigned)(nslots * (I / kTR));
+    const int itiles = (int)(I / kTR);
+    const int64_t ntiles = (int64_t)nslots * itiles;
+    // tiles of one slot per workgroup: the count that takes the fewest tile-times at two
+    // workgroups per CU (ties to the larger count: fewer routing and staging passes)
+    const int64_t wave_slots = 2LL * device_cu_count();
+    int tpw = 1;
+    int64_t best = (ntiles + wave_slots - 1) / wave_slots;
+    for (int c = 2; c <= 4; c *= 2) {
+        if (itiles % c) continue;
+        const int64_t cost = (ntiles / c + wave_slots - 1) / wave_slots * c;
+        if (cost <= best) {
+            best = cost;
+            tpw = c;
+        }
+    }
+    const unsigned nwg = (unsigned)(ntiles / tpw);
     Plan1 p1;
     if (make_plan1(nsb, 2, 4, p1, true) && p1.W * 64 >= (route.logits ? (int)((E + 7) & ~7) : 0))
-        return run1(pb, p1, nwg, x, 0, H * 2, (int)H, st);
+        return run1(pb, p1, nwg, x, 0, H * 2, (int)H, st, tpw);
     Plan pl;
     if (!make_plan(nsb, 2, 1, 1, 4, pl) || pl.W * 64 < (route.logits ? (int)((E + 7) & ~7) : 0)) return hipErrorInvalidValue;
-    return run_mfma<1>(pb, pl, nwg, x, 0, H * 2, (int)H, 1, st);
+    return run_mfma<1>(pb, pl, (unsigned)ntiles, x, 0, H * 2, (int)H, 1, st);   // one tile per workgroup
 }
 
 // One down launch over `nslots` slots (at most one workgroup's waves).
