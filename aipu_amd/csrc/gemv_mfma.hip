@@ -671,6 +671,153 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* _
     pb.finish(wg, red, KP, tid);
 }
 
+// ------------------------------------------------- two-row kernel (M = 2)
+// The single-row kernel's memory plan for two activation rows.  A workgroup owns one 16-row
+// tile, its K split over KP <= NW waves of GS blocks; each wave copies all its weight blocks
+// straight into its LDS slice at once (1 KB of consecutive row bytes per instruction) and
+// stages its own K-slice of both activation rows.  Activation rows 0 and 1 are rows 4g and
+// 4g + 1 of the block-diagonal operand, so one set of codes serves both and lane 16g + n
+// ends with the row-n sums of both activation rows in its D registers 0 and 1.
+// LDS per wave: the weight slice and the operand entries [b][t][g][m] (16 B).  The sub-block
+// activation sums stay in registers (each lane fetches its own from the staging lanes), and
+// the cross-wave partial sums go through each wave's own weight slice, which is free once
+// the blocks are in registers: at K = 6144 eight waves of three blocks take 57,344 +
+// 24,576 B, exactly half the CU's LDS, so two workgroups share a CU as in the M = 1 kernel.
+template <int GS, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemv2(ProbPlain<2> pb, const uint16_t* __restrict__ X, int K, int KP) {
+    constexpr int MR = 2;
+    constexpr int BPK = GS;                  // blocks per wave
+    constexpr uint32_t kActWave = BPK * 512 * MR;
+    constexpr int XP = BPK * 32;             // 16-B pieces per activation row
+    constexpr int XI = (MR * XP + 63) / 64;  // pieces per lane
+    __shared__ __align__(16) uint8_t s_act[NW * kActWave];
+    extern __shared__ __align__(16) uint8_t s_w[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: the copies take a scalar LDS base
+    const int nsb = K / QK_K;
+    const int wg = blockIdx.x;
+    uint8_t* wW = s_w + (uint32_t)w * Dma<GS>::kBytes;
+    const TileRef tr = pb.tile(wg, 0);
+    const int kb0 = w * BPK;
+    const int64_t rb = (int64_t)nsb * 144;
+    uint8_t* wA = s_act + (uint32_t)w * kActWave;
+
+    // 1. this wave's activations (rows >= M read as zero), then 2. its weights
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)((int64_t)pb.M * K * 2));
+    uint4 xv[XI];
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const int q = lane + 64 * i;
+        const int m = q >= XP ? 1 : 0, p = q - m * XP;
+        const uint32_t off = q < MR * XP ? 2u * (uint32_t)(m * K + kb0 * QK_K) + 16u * (uint32_t)p : kOOB;
+        xv[i] = buf_load16(xr, off);
+    }
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
+    dma_group<GS>(wr, wW, rb, kb0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. stage operand entries; sub-block sums (the four pieces of a sub-block are the four
+    // lanes of a quad)
+    float sums[XI];
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const int q = lane + 64 * i;
+        const int m = q >= XP ? 1 : 0, p = q - m * XP;
+        const uint32_t ones = 0x3F803F80u;
+        float sm = 0.f;
+        sm = dot2(xv[i].x, ones, sm);
+        sm = dot2(xv[i].y, ones, sm);
+        sm = dot2(xv[i].z, ones, sm);
+        sm = dot2(xv[i].w, ones, sm);
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+        sums[i] = sm;
+        if (q < MR * XP) {
+            const int bb = p >> 5, gg = (p >> 3) & 3, t = p & 7;
+            *(u32x4_t*)(wA + 16u * (uint32_t)((((bb * 8 + t) * 4 + gg) * MR) + m)) = act_perm(xv[i]);
+        }
+    }
+    // lane 16g + n takes the sums of sub-blocks 2g (lo) and 2g + 1 (hi) of every block and
+    // row: piece m * XP + 32b + 8g + 4h, which lies in staging register (m * XP + 32b) / 64
+    // for all g (a 32-aligned run of 32 pieces never straddles 64)
+    float4 as_r[BPK];   // lo row 0, lo row 1, hi row 0, hi row 1
+#pragma unroll
+    for (int b = 0; b < BPK; ++b) {
+        float v[4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const int q0 = m * XP + 32 * b + 4 * h;
+                v[2 * h + m] = __shfl(sums[q0 / 64], (q0 & 63) + 8 * (lane >> 4), 64);
+            }
+        as_r[b] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+
+    // 4. block loop
+    const int n = lane & 15, g = lane >> 4;
+    u32x4_t A[8];   // block-diagonal activation operands: off-diagonal lanes stay zero
+#pragma unroll
+    for (int t = 0; t < 8; ++t) A[t] = u32x4_t{0u, 0u, 0u, 0u};
+    const HdrSel hs = hdr_sel(g);
+    const CodeK ck = code_k();
+    const uint32_t rrow = (uint32_t)n * (144u * GS);
+    const uint32_t abase = lds_addr(wA + 16u * (uint32_t)(g * MR + ((n - 4 * g) & 1)));   // diagonal lanes
+    f32x4_t dlo = {0.f, 0.f, 0.f, 0.f}, dhi = {0.f, 0.f, 0.f, 0.f};
+    float acc0 = 0.f, acc1 = 0.f;
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);   // the weights are in LDS
+    Raw R[GS];
+#pragma unroll
+    for (int b = 0; b < GS; ++b) {
+        const uint8_t* p = wW + rrow + 144u * b;
+        R[b].h = *(const uint4*)p;
+        R[b].q0 = *(const uint4*)(p + 16 + 32 * g);
+        R[b].q1 = *(const uint4*)(p + 32 + 32 * g);
+    }
+#pragma unroll
+    for (int b = 0; b < GS; ++b) {
+        a_reads2(A, abase + (uint32_t)b * (512u * MR), diag_mask(MR));
+        const float4 as = as_r[b];
+        dlo[0] = -kCodeBiasF * as.x;
+        dlo[1] = -kCodeBiasF * as.y;
+        dhi[0] = -kCodeBiasF * as.z;
+        dhi[1] = -kCodeBiasF * as.w;
+        const uint32_t qd[8] = {R[b].q0.x, R[b].q0.y, R[b].q0.z, R[b].q0.w, R[b].q1.x, R[b].q1.y, R[b].q1.z, R[b].q1.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            dlo = mfma(A[t], codes_lo(qd[2 * t], qd[2 * t + 1], ck), dlo);
+            dhi = mfma(A[4 + t], codes_hi(qd[2 * t], qd[2 * t + 1], ck), dhi);
+        }
+        const Hdr H = hdr_decode(R[b].h, hs);
+        const float t0 = __builtin_fmaf(H.sc1, dhi[0], H.sc0 * dlo[0]);
+        const float t1 = __builtin_fmaf(H.sc1, dhi[1], H.sc0 * dlo[1]);
+        const float v0 = __builtin_fmaf(H.m1, as.z, H.m0 * as.x);
+        const float v1 = __builtin_fmaf(H.m1, as.w, H.m0 * as.y);
+        acc0 = __builtin_fmaf(H.d, t0, acc0);
+        acc0 = __builtin_fmaf(-H.dm, v0, acc0);
+        acc1 = __builtin_fmaf(H.d, t1, acc1);
+        acc1 = __builtin_fmaf(-H.dm, v1, acc1);
+    }
+
+    // 5. reduce over the four K-groups, then across the K parts in wave order
+    acc0 += __shfl_xor(acc0, 16, 64);
+    acc0 += __shfl_xor(acc0, 32, 64);
+    acc1 += __shfl_xor(acc1, 16, 64);
+    acc1 += __shfl_xor(acc1, 32, 64);
+    if (lane < kTR) *(float2*)(wW + 8u * (uint32_t)lane) = make_float2(acc0, acc1);
+    __syncthreads();
+    if (tid < kTR * MR) {
+        const int rn = tid >> 1, r = tid & 1;
+        const int64_t row = (int64_t)wg * kTR + rn;
+        if (r < pb.M && row < pb.N) {
+            float v = 0.f;
+            for (int k = 0; k < KP; ++k) v += ((const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes))[rn * MR + r];
+            pb.Y[r * pb.ystride + row] = (uint16_t)bf16_rne(v);
+            if (pb.Yf) pb.Yf[r * pb.ystride + row] = v;
+        }
+    }
+}
+
 template <int MR, class Prob>
 hipError_t run_gemvm(const Prob& pb, int nsb, unsigned nwg, const uint16_t* x, int K, hipStream_t st) {
     // KP waves of BPK blocks: the largest KP <= 8 that divides nsb with a supported BPK
@@ -797,6 +944,41 @@ hipError_t run1(const Prob& pb, const Plan1& pl, unsigned nwg, const uint16_t* X
     return hipGetLastError();
 }
 
+// Two-row plan: KP <= kNW2 waves of GS <= 4 blocks, weight slices and staged activations
+// within half the CU's LDS (two workgroups per CU).
+constexpr int kNW2 = 8;
+struct Plan2 {
+    int KP, GS;
+    int64_t lds;   // dynamic LDS (the weight slices)
+};
+
+bool make_plan2(int nsb, Plan2& p) {
+    for (int kp = kNW2; kp >= 1; --kp) {
+        if (nsb % kp || nsb / kp > 4) continue;
+        const int gs = nsb / kp;
+        const int64_t lds = (int64_t)kp * dma_bytes(gs);
+        if (lds + (int64_t)kNW2 * gs * 1024 > kMaxLds1) continue;
+        p = Plan2{kp, gs, lds};
+        return true;
+    }
+    return false;
+}
+
+hipError_t run2(const ProbPlain<2>& pb, const Plan2& pl, unsigned nwg, const uint16_t* X, int K, hipStream_t st) {
+    const dim3 grid(nwg), block(64 * pl.KP);
+    const size_t lds = (size_t)pl.lds;
+#define AIPU_L2(GSV) \
+    hipLaunchKernelGGL((k_gemv2<GSV, kNW2>), grid, block, lds, st, pb, X, K, pl.KP)
+    switch (pl.GS) {
+        case 1: AIPU_L2(1); break;
+        case 2: AIPU_L2(2); break;
+        case 3: AIPU_L2(3); break;
+        default: AIPU_L2(4); break;
+    }
+#undef AIPU_L2
+    return hipGetLastError();
+}
+
 // Shapes the small-batch kernel covers: K / 256 split into at most 8 parts of 1 .. 4 blocks,
 // with enough waves for the reduction of mr rows.
 bool gemvm_supported(int nsb, int mr) {
@@ -813,6 +995,10 @@ hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x,
     const unsigned nwg = (unsigned)((N + kTR - 1) / kTR);
     Plan1 p1;
     if (MR == 1 && make_plan1(nsb, 1, kMaxW, p1)) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
+    if constexpr (MR == 2) {
+        Plan2 p2;
+        if (make_plan2(nsb, p2)) return run2(pb, p2, nwg, x, (int)K, st);
+    }
     if (MR > 1 && gemvm_supported(nsb, MR)) return run_gemvm<MR>(pb, nsb, nwg, x, (int)K, st);
     Plan pl;
     if (!make_plan(nsb, 1, 1, MR, kMaxW, pl)) return hipErrorInvalidValue;

@@ -201,6 +201,29 @@ __device__ __forceinline__ void a_reads(u32x4_t (&A)[8], uint32_t aa, uint64_t m
         : "memory", "scc");   // s_and_b64 writes SCC
 }
 
+// a_reads for two activation rows: the operands of MFMA t sit 128 B apart (entries
+// [t][g][m], m < 2).
+__device__ __forceinline__ void a_reads2(u32x4_t (&A)[8], uint32_t aa, uint64_t mask) {
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %8, exec\n\t"
+        "s_and_b64 exec, exec, %10\n\t"
+        "ds_read_b128 %0, %9\n\t"
+        "ds_read_b128 %1, %9 offset:128\n\t"
+        "ds_read_b128 %2, %9 offset:256\n\t"
+        "ds_read_b128 %3, %9 offset:384\n\t"
+        "ds_read_b128 %4, %9 offset:512\n\t"
+        "ds_read_b128 %5, %9 offset:640\n\t"
+        "ds_read_b128 %6, %9 offset:768\n\t"
+        "ds_read_b128 %7, %9 offset:896\n\t"
+        "s_mov_b64 exec, %8\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]),
+          "=&s"(saved)
+        : "v"(aa), "s"(mask)
+        : "memory", "scc");
+}
+
 // A point after which the weight blocks in R are in registers: the asm consumes every
 // register of R (so the LDS loads that produce them have completed), and its memory clobber
 // keeps later memory operations -- the copy that refills the same LDS slice -- behind it.
@@ -224,6 +247,13 @@ __device__ __forceinline__ void regs_consumed(const T (&R)[N]) {
 __device__ __forceinline__ float2 sums_read(const float* p) {
     float2 v;
     asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+    return v;
+}
+
+// The same for two activation rows: (lo row 0, lo row 1, hi row 0, hi row 1).
+__device__ __forceinline__ float4 sums_read2(const float* p) {
+    float4 v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
     return v;
 }
 
