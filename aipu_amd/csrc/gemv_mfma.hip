@@ -524,7 +524,9 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     }
 }
 
-// ------------------------------------------------- small-batch kernel (M = 2 .. 8)
+// ------------------------------------------------- register-weight kernel (M = 5 .. 8)
+// Five to eight activation rows (eight rows' staged activations leave no LDS for copying the
+// weights), the batched-MoE union legs, and shapes the small-batch plan does not cover.
 // One 16-row weight tile per workgroup, its K split over KP waves of BPK blocks each.  A
 // wave loads its weight blocks straight into registers (all of them at once), and stages
 // only its own K-slice of the MR activation rows in its own LDS region, so no barrier
@@ -671,102 +673,90 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* _
     pb.finish(wg, red, KP, tid);
 }
 
-// ------------------------------------------------- two-row kernel (M = 2)
-// The single-row kernel's memory plan for two activation rows.  A workgroup owns one 16-row
-// tile, its K split over KP <= NW waves of GS blocks; each wave copies all its weight blocks
-// straight into its LDS slice at once (1 KB of consecutive row bytes per instruction) and
-// stages its own K-slice of both activation rows.  Activation rows 0 and 1 are rows 4g and
-// 4g + 1 of the block-diagonal operand, so one set of codes serves both and lane 16g + n
-// ends with the row-n sums of both activation rows in its D registers 0 and 1.
-// LDS per wave: the weight slice and the operand entries [b][t][g][m] (16 B).  The sub-block
-// activation sums stay in registers (each lane fetches its own from the staging lanes), and
-// the cross-wave partial sums go through each wave's own weight slice, which is free once
-// the blocks are in registers: at K = 6144 eight waves of three blocks take 57,344 +
-// 24,576 B, exactly half the CU's LDS, so two workgroups share a CU as in the M = 1 kernel.
-template <int GS, int NW>
-__global__ __launch_bounds__(NW * 64) void k_gemv2(ProbPlain<2> pb, const uint16_t* __restrict__ X, int K, int KP) {
-    constexpr int MR = 2;
-    constexpr int BPK = GS;                  // blocks per wave
-    constexpr uint32_t kActWave = BPK * 512 * MR;
-    constexpr int XP = BPK * 32;             // 16-B pieces per activation row
-    constexpr int XI = (MR * XP + 63) / 64;  // pieces per lane
-    __shared__ __align__(16) uint8_t s_act[NW * kActWave];
+// ------------------------------------------------- small-batch kernel (M = 2 .. 4)
+// The single-row kernel's memory plan for up to four activation rows.  A workgroup owns one
+// 16-row tile, its K split over KP <= NW waves of GS blocks; each wave copies all its weight
+// blocks straight into its LDS slice at once (1 KB of consecutive row bytes per
+// instruction) and moves them into registers.  Row m is row 4g + m of the block-diagonal
+// operand, so one set of codes (the VALU work of a block) serves all rows and lane 16g + n
+// ends with the row-n sums of every row in its D registers.  The operand entries
+// ([b][t][g][m & 1], 16 B) sit in two places: rows 0, 1 in the wave's static region, staged
+// while the weights are in flight, and rows 2, 3 in the wave's own weight slice, free once
+// the blocks are in registers.  The sub-block activation sums stay in registers (each lane
+// fetches its own from the staging lanes) and the cross-wave partial sums go through the
+// slices.  At K = 6144 eight waves of three blocks take 57,344 + 24,576 B, exactly half the
+// CU's LDS, so two workgroups share a CU as in the M = 1 kernel.
+constexpr int kSmallMaxRows = 4;
+
+template <int GS, int NW, int MR>   // MR = 2: rows 0, 1 only; MR = 4: up to four rows
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemvs(
+    ProbPlain<4> pb, const uint16_t* __restrict__ X, int K, int KP) {
+    constexpr int XP = GS * 32;              // 16-B pieces per activation row and wave
+    constexpr int XI = (2 * XP + 63) / 64;   // pieces per lane for a pair of rows
+    constexpr uint32_t kPair = GS * 1024u;   // operand entries of a pair of rows
+    constexpr uint32_t kRed = kPair;         // partial sums [n][row], after the entries in the slice
+    static_assert(kRed + kTR * kSmallMaxRows * 4 <= (uint32_t)Dma<GS>::kBytes, "slice holds a pair and the sums");
+    __shared__ __align__(16) uint8_t s_act[NW * kPair];
     extern __shared__ __align__(16) uint8_t s_w[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: the copies take a scalar LDS base
     const int nsb = K / QK_K;
     const int wg = blockIdx.x;
+    const int rows = pb.M;   // 1 .. MR
+    uint8_t* wA = s_act + (uint32_t)w * kPair;
     uint8_t* wW = s_w + (uint32_t)w * Dma<GS>::kBytes;
     const TileRef tr = pb.tile(wg, 0);
-    const int kb0 = w * BPK;
+    const int kb0 = w * GS;
     const int64_t rb = (int64_t)nsb * 144;
-    uint8_t* wA = s_act + (uint32_t)w * kActWave;
 
-    // 1. this wave's activations (rows >= M read as zero), then 2. its weights
+    // Activation pieces of rows r0, r0 + 1 (rows >= M read as zero).
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)((int64_t)pb.M * K * 2));
-    uint4 xv[XI];
+    auto load_pair = [&](int r0, uint4(&xv)[XI]) {
 #pragma unroll
-    for (int i = 0; i < XI; ++i) {
-        const int q = lane + 64 * i;
-        const int m = q >= XP ? 1 : 0, p = q - m * XP;
-        const uint32_t off = q < MR * XP ? 2u * (uint32_t)(m * K + kb0 * QK_K) + 16u * (uint32_t)p : kOOB;
-        xv[i] = buf_load16(xr, off);
-    }
+        for (int i = 0; i < XI; ++i) {
+            const int q = lane + 64 * i;
+            const int m = q >= XP ? 1 : 0, p = q - m * XP;
+            const uint32_t off = q < 2 * XP ? 2u * (uint32_t)((r0 + m) * K + kb0 * QK_K) + 16u * (uint32_t)p : kOOB;
+            xv[i] = buf_load16(xr, off);
+        }
+    };
+    // Stage a pair as operand entries at dst and keep the sub-block sums (the four pieces of
+    // a sub-block are the four lanes of a quad, which all end with the sum).
+    auto stage_pair = [&](const uint4(&xv)[XI], uint8_t* dst, float(&sums)[XI]) {
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int q = lane + 64 * i;
+            const int m = q >= XP ? 1 : 0, p = q - m * XP;
+            const uint32_t ones = 0x3F803F80u;
+            float sm = 0.f;
+            sm = dot2(xv[i].x, ones, sm);
+            sm = dot2(xv[i].y, ones, sm);
+            sm = dot2(xv[i].z, ones, sm);
+            sm = dot2(xv[i].w, ones, sm);
+            sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+            sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+            sums[i] = sm;
+            if (q < 2 * XP) {
+                const int bb = p >> 5, gg = (p >> 3) & 3, t = p & 7;
+                *(u32x4_t*)(dst + 16u * (uint32_t)(((bb * 8 + t) * 4 + gg) * 2 + m)) = act_perm(xv[i]);
+            }
+        }
+    };
+
+    // 1. rows 0, 1, then the weights; the pair is staged while the weights are in flight
+    uint4 xa[XI], xb[XI];
+    float sa[XI], sb[XI];
+    load_pair(0, xa);
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
     dma_group<GS>(wr, wW, rb, kb0, lane);
     __builtin_amdgcn_sched_barrier(0);
+    stage_pair(xa, wA, sa);
 
-    // 3. stage operand entries; sub-block sums (the four pieces of a sub-block are the four
-    // lanes of a quad)
-    float sums[XI];
-#pragma unroll
-    for (int i = 0; i < XI; ++i) {
-        const int q = lane + 64 * i;
-        const int m = q >= XP ? 1 : 0, p = q - m * XP;
-        const uint32_t ones = 0x3F803F80u;
-        float sm = 0.f;
-        sm = dot2(xv[i].x, ones, sm);
-        sm = dot2(xv[i].y, ones, sm);
-        sm = dot2(xv[i].z, ones, sm);
-        sm = dot2(xv[i].w, ones, sm);
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
-        sums[i] = sm;
-        if (q < MR * XP) {
-            const int bb = p >> 5, gg = (p >> 3) & 3, t = p & 7;
-            *(u32x4_t*)(wA + 16u * (uint32_t)((((bb * 8 + t) * 4 + gg) * MR) + m)) = act_perm(xv[i]);
-        }
-    }
-    // lane 16g + n takes the sums of sub-blocks 2g (lo) and 2g + 1 (hi) of every block and
-    // row: piece m * XP + 32b + 8g + 4h, which lies in staging register (m * XP + 32b) / 64
-    // for all g (a 32-aligned run of 32 pieces never straddles 64)
-    float4 as_r[BPK];   // lo row 0, lo row 1, hi row 0, hi row 1
-#pragma unroll
-    for (int b = 0; b < BPK; ++b) {
-        float v[4];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const int q0 = m * XP + 32 * b + 4 * h;
-                v[2 * h + m] = __shfl(sums[q0 / 64], (q0 & 63) + 8 * (lane >> 4), 64);
-            }
-        as_r[b] = make_float4(v[0], v[1], v[2], v[3]);
-    }
-
-    // 4. block loop
+    // 2. the weights into registers (the compiler waits for the copies into s_w), then rows
+    // 2, 3 over the slice
     const int n = lane & 15, g = lane >> 4;
-    u32x4_t A[8];   // block-diagonal activation operands: off-diagonal lanes stay zero
-#pragma unroll
-    for (int t = 0; t < 8; ++t) A[t] = u32x4_t{0u, 0u, 0u, 0u};
-    const HdrSel hs = hdr_sel(g);
-    const CodeK ck = code_k();
-    const uint32_t rrow = (uint32_t)n * (144u * GS);
-    const uint32_t abase = lds_addr(wA + 16u * (uint32_t)(g * MR + ((n - 4 * g) & 1)));   // diagonal lanes
-    f32x4_t dlo = {0.f, 0.f, 0.f, 0.f}, dhi = {0.f, 0.f, 0.f, 0.f};
-    float acc0 = 0.f, acc1 = 0.f;
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);   // the weights are in LDS
     Raw R[GS];
+    const uint32_t rrow = (uint32_t)n * (144u * GS);
 #pragma unroll
     for (int b = 0; b < GS; ++b) {
         const uint8_t* p = wW + rrow + 144u * b;
@@ -774,44 +764,79 @@ __global__ __launch_bounds__(NW * 64) void k_gemv2(ProbPlain<2> pb, const uint16
         R[b].q0 = *(const uint4*)(p + 16 + 32 * g);
         R[b].q1 = *(const uint4*)(p + 32 + 32 * g);
     }
-#pragma unroll
-    for (int b = 0; b < GS; ++b) {
-        a_reads2(A, abase + (uint32_t)b * (512u * MR), diag_mask(MR));
-        const float4 as = as_r[b];
-        dlo[0] = -kCodeBiasF * as.x;
-        dlo[1] = -kCodeBiasF * as.y;
-        dhi[0] = -kCodeBiasF * as.z;
-        dhi[1] = -kCodeBiasF * as.w;
-        const uint32_t qd[8] = {R[b].q0.x, R[b].q0.y, R[b].q0.z, R[b].q0.w, R[b].q1.x, R[b].q1.y, R[b].q1.z, R[b].q1.w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            dlo = mfma(A[t], codes_lo(qd[2 * t], qd[2 * t + 1], ck), dlo);
-            dhi = mfma(A[4 + t], codes_hi(qd[2 * t], qd[2 * t + 1], ck), dhi);
-        }
-        const Hdr H = hdr_decode(R[b].h, hs);
-        const float t0 = __builtin_fmaf(H.sc1, dhi[0], H.sc0 * dlo[0]);
-        const float t1 = __builtin_fmaf(H.sc1, dhi[1], H.sc0 * dlo[1]);
-        const float v0 = __builtin_fmaf(H.m1, as.z, H.m0 * as.x);
-        const float v1 = __builtin_fmaf(H.m1, as.w, H.m0 * as.y);
-        acc0 = __builtin_fmaf(H.d, t0, acc0);
-        acc0 = __builtin_fmaf(-H.dm, v0, acc0);
-        acc1 = __builtin_fmaf(H.d, t1, acc1);
-        acc1 = __builtin_fmaf(-H.dm, v1, acc1);
+    if (MR > 2 && rows > 2) {
+        load_pair(2, xb);
+        stage_pair(xb, wW, sb);
     }
 
-    // 5. reduce over the four K-groups, then across the K parts in wave order
-    acc0 += __shfl_xor(acc0, 16, 64);
-    acc0 += __shfl_xor(acc0, 32, 64);
-    acc1 += __shfl_xor(acc1, 16, 64);
-    acc1 += __shfl_xor(acc1, 32, 64);
-    if (lane < kTR) *(float2*)(wW + 8u * (uint32_t)lane) = make_float2(acc0, acc1);
+    // 3. the blocks
+    u32x4_t A[4];   // block-diagonal operands of four MFMAs: off-diagonal lanes stay zero
+#pragma unroll
+    for (int t = 0; t < 4; ++t) A[t] = u32x4_t{0u, 0u, 0u, 0u};
+    const HdrSel hs = hdr_sel(g);
+    const CodeK ck = code_k();
+    const int md = (n - 4 * g) & 3;   // the diagonal lanes' activation row
+    const uint32_t abase = lds_addr((md < 2 ? wA : wW) + 16u * (uint32_t)(g * 2 + (md & 1)));
+    const uint64_t mask = ((1ull << rows) - 1) * 0x1000010000100001ull;   // diag_mask(rows)
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+#pragma unroll
+    for (int b = 0; b < GS; ++b) {
+        // lane 16g + n: sums of sub-blocks 2g (lo), 2g + 1 (hi) of block b, rows m: piece
+        // (m & 1) * XP + 32b + 8g + 4h of its pair, in staging register ((m & 1) * XP + 32b)
+        // / 64 for all g (a 32-aligned run of 32 pieces never straddles 64)
+        float lo[MR], hi[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const int q0 = (m & 1) * XP + 32 * b;
+            const float src = m < 2 ? sa[q0 / 64] : sb[q0 / 64];
+            lo[m] = __shfl(src, (q0 & 63) + 8 * g, 64);
+            hi[m] = __shfl(src, (q0 & 63) + 8 * g + 4, 64);
+        }
+        f32x4_t dlo = {0.f, 0.f, 0.f, 0.f}, dhi = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            dlo[m] = -kCodeBiasF * lo[m];
+            dhi[m] = -kCodeBiasF * hi[m];
+        }
+        const uint32_t qd[8] = {R[b].q0.x, R[b].q0.y, R[b].q0.z, R[b].q0.w, R[b].q1.x, R[b].q1.y, R[b].q1.z, R[b].q1.w};
+        // low nibbles against operands t = 0..3, then high nibbles against t = 4..7
+        a_reads2h(A, abase + (uint32_t)b * 1024u, mask);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dlo = mfma(A[t], codes_lo(qd[2 * t], qd[2 * t + 1], ck), dlo);
+        a_reads2h(A, abase + (uint32_t)b * 1024u + 512u, mask);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dhi = mfma(A[t], codes_hi(qd[2 * t], qd[2 * t + 1], ck), dhi);
+        const Hdr H = hdr_decode(R[b].h, hs);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float t1 = __builtin_fmaf(H.sc1, dhi[m], H.sc0 * dlo[m]);
+            const float v = __builtin_fmaf(H.m1, hi[m], H.m0 * lo[m]);
+            acc[m] = __builtin_fmaf(H.d, t1, acc[m]);
+            acc[m] = __builtin_fmaf(-H.dm, v, acc[m]);
+        }
+    }
+
+    // 4. reduce over the four K-groups, then across the K parts in wave order
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        acc[m] += __shfl_xor(acc[m], 16, 64);
+        acc[m] += __shfl_xor(acc[m], 32, 64);
+    }
+    if (lane < kTR) {
+        float* red = (float*)(wW + kRed) + kSmallMaxRows * lane;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) red[m] = acc[m];
+    }
     __syncthreads();
-    if (tid < kTR * MR) {
-        const int rn = tid >> 1, r = tid & 1;
+    for (int e = tid; e < kTR * kSmallMaxRows; e += (int)blockDim.x) {
+        const int rn = e >> 2, r = e & 3;
         const int64_t row = (int64_t)wg * kTR + rn;
-        if (r < pb.M && row < pb.N) {
+        if (r < rows && row < pb.N) {
             float v = 0.f;
-            for (int k = 0; k < KP; ++k) v += ((const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes))[rn * MR + r];
+            for (int k = 0; k < KP; ++k)
+                v += ((const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes + kRed))[rn * kSmallMaxRows + r];
             pb.Y[r * pb.ystride + row] = (uint16_t)bf16_rne(v);
             if (pb.Yf) pb.Yf[r * pb.ystride + row] = v;
         }
@@ -944,39 +969,40 @@ hipError_t run1(const Prob& pb, const Plan1& pl, unsigned nwg, const uint16_t* X
     return hipGetLastError();
 }
 
-// Two-row plan: KP <= kNW2 waves of GS <= 4 blocks, weight slices and staged activations
-// within half the CU's LDS (two workgroups per CU).
-constexpr int kNW2 = 8;
-struct Plan2 {
+// Small-batch plan: KP <= 8 waves of GS <= 3 blocks (three blocks' weights, one block's
+// operands and four rows' sums fill the 128 registers of four waves per SIMD), the weight
+// slices and staged pair within half the CU's LDS.
+struct PlanS {
     int KP, GS;
     int64_t lds;   // dynamic LDS (the weight slices)
 };
 
-bool make_plan2(int nsb, Plan2& p) {
-    for (int kp = kNW2; kp >= 1; --kp) {
-        if (nsb % kp || nsb / kp > 4) continue;
+bool make_plans(int nsb, PlanS& p) {
+    for (int kp = kMaxW; kp >= 1; --kp) {
+        if (nsb % kp || nsb / kp > 3) continue;
         const int gs = nsb / kp;
         const int64_t lds = (int64_t)kp * dma_bytes(gs);
-        if (lds + (int64_t)kNW2 * gs * 1024 > kMaxLds1) continue;
-        p = Plan2{kp, gs, lds};
+        if (lds + (int64_t)kMaxW * gs * 1024 > kMaxLds1) continue;
+        p = PlanS{kp, gs, lds};
         return true;
     }
     return false;
 }
 
-hipError_t run2(const ProbPlain<2>& pb, const Plan2& pl, unsigned nwg, const uint16_t* X, int K, hipStream_t st) {
+template <int MR>
+hipError_t runs_mr(const ProbPlain<4>& pb, const PlanS& pl, unsigned nwg, const uint16_t* X, int K, hipStream_t st) {
     const dim3 grid(nwg), block(64 * pl.KP);
     const size_t lds = (size_t)pl.lds;
-#define AIPU_L2(GSV) \
-    hipLaunchKernelGGL((k_gemv2<GSV, kNW2>), grid, block, lds, st, pb, X, K, pl.KP)
     switch (pl.GS) {
-        case 1: AIPU_L2(1); break;
-        case 2: AIPU_L2(2); break;
-        case 3: AIPU_L2(3); break;
-        default: AIPU_L2(4); break;
+        case 1: hipLaunchKernelGGL((k_gemvs<1, kMaxW, MR>), grid, block, lds, st, pb, X, K, pl.KP); break;
+        case 2: hipLaunchKernelGGL((k_gemvs<2, kMaxW, MR>), grid, block, lds, st, pb, X, K, pl.KP); break;
+        default: hipLaunchKernelGGL((k_gemvs<3, kMaxW, MR>), grid, block, lds, st, pb, X, K, pl.KP); break;
     }
-#undef AIPU_L2
     return hipGetLastError();
+}
+
+hipError_t runs(const ProbPlain<4>& pb, const PlanS& pl, unsigned nwg, const uint16_t* X, int K, hipStream_t st) {
+    return pb.M <= 2 ? runs_mr<2>(pb, pl, nwg, X, K, st) : runs_mr<4>(pb, pl, nwg, X, K, st);
 }
 
 // Shapes the small-batch kernel covers: K / 256 split into at most 8 parts of 1 .. 4 blocks,
@@ -995,10 +1021,6 @@ hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x,
     const unsigned nwg = (unsigned)((N + kTR - 1) / kTR);
     Plan1 p1;
     if (MR == 1 && make_plan1(nsb, 1, kMaxW, p1)) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
-    if constexpr (MR == 2) {
-        Plan2 p2;
-        if (make_plan2(nsb, p2)) return run2(pb, p2, nwg, x, (int)K, st);
-    }
     if (MR > 1 && gemvm_supported(nsb, MR)) return run_gemvm<MR>(pb, nsb, nwg, x, (int)K, st);
     Plan pl;
     if (!make_plan(nsb, 1, 1, MR, kMaxW, pl)) return hipErrorInvalidValue;
@@ -1016,18 +1038,30 @@ bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M) {
     return K <= (1 << 20) && make_plan((int)(K / QK_K), 1, 1, mr, kMaxW, pl);
 }
 
-// y[M][N] (row stride ystride) = x[M][K] . W^T, in passes of at most 4 activation rows.
+// y[M][N] (row stride ystride) = x[M][K] . W^T, in passes of at most 8 activation rows.
 hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
                             float* y_f32, int64_t ystride, hipStream_t st) {
     const uint8_t* W = (const uint8_t*)w;
     const int nsb = (int)(K / QK_K);
+    PlanS ps;
+    const bool small = make_plans(nsb, ps);
     for (int64_t m0 = 0; m0 < M;) {
-        if (M - m0 >= 8 && gemvm_supported(nsb, 8)) {   // eight rows in one pass
+        const int left = (int)(M - m0 < 8 ? M - m0 : 8);
+        if (left >= 5 && gemvm_supported(nsb, 8)) {   // five to eight rows in one pass
             const ProbPlain<8> pb{W, N, row_bytes(T_Q4_K, K), y + m0 * ystride, y_f32 ? y_f32 + m0 * ystride : nullptr,
-                                  ystride, 8};
+                                  ystride, left};
             const hipError_t e = run_gemvm<8>(pb, nsb, (unsigned)((N + kTR - 1) / kTR), x + m0 * K, (int)K, st);
             if (e != hipSuccess) return e;
-            m0 += 8;
+            m0 += left;
+            continue;
+        }
+        if (small && left >= 2) {   // two to four rows, the weights read once
+            const int mr = left < kSmallMaxRows ? left : kSmallMaxRows;
+            const ProbPlain<4> pb{W, N, row_bytes(T_Q4_K, K), y + m0 * ystride, y_f32 ? y_f32 + m0 * ystride : nullptr,
+                                  ystride, mr};
+            const hipError_t e = runs(pb, ps, (unsigned)((N + kTR - 1) / kTR), x + m0 * K, (int)K, st);
+            if (e != hipSuccess) return e;
+            m0 += mr;
             continue;
         }
         const int mr = (int)(M - m0 < 4 ? M - m0 : 4);

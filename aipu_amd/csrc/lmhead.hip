@@ -92,9 +92,6 @@ __device__ __forceinline__ void chunk_sum(const uint8_t* row, const uint32_t* __
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-// s_waitcnt immediate for vmcnt(n), n < 64 (gfx9: vmcnt bits 3:0 and 15:14).
-__host__ __device__ constexpr int wait_vm(int n) { return (mg::kWaitVm0 & ~0xC00F) | (n & 0x0F) | ((n >> 4) << 14); }
-
 // Issue the P copies of chunk `ch` into one stage (all lanes read zeros without a memory
 // access when ch is past the end: the offset lands outside the buffer).
 template <int P>
@@ -114,7 +111,7 @@ __device__ __forceinline__ void stage_step(__amdgpu_buffer_rsrc_t rs, lds_u8* ds
                                            const uint32_t* voff, const uint32_t* xw, int ch,
                                            int nch, float (&ps)[kL]) {
     constexpr int P = pitch_units(U);
-    __builtin_amdgcn_s_waitcnt(wait_vm((S - 1) * P));
+    __builtin_amdgcn_s_waitcnt(mg::wait_vm((S - 1) * P));
     chunk_sum<U>(row, xw + (int64_t)ch * (4 * U), U, ps);
     __builtin_amdgcn_s_waitcnt(mg::kWaitLgkm0);
     chunk_copy<P>(rs, dst, voff, ch + S, nch, 16u * U);
@@ -313,12 +310,12 @@ __global__ void __launch_bounds__(64 * kRcWaves) k_lmhead_rc(const uint8_t* __re
         const uint8_t* xj = xs + j * xpitch;
         int ch = 0;
         for (; ch + 1 < nch; ch += 2) {
-            __builtin_amdgcn_s_waitcnt(wait_vm(kRcCopies));
+            __builtin_amdgcn_s_waitcnt(mg::wait_vm(kRcCopies));
             ps = rc_chunk(w0, xj + ch * 128, ps);
             __builtin_amdgcn_s_waitcnt(mg::kWaitLgkm0);
             rc_copy(rs, d0, voff, unit, ch + 2, nch, ch + 2 < nfull ? kRcUnits : tail);
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(wait_vm(kRcCopies));
+            __builtin_amdgcn_s_waitcnt(mg::wait_vm(kRcCopies));
             ps = rc_chunk(w1, xj + (ch + 1) * 128, ps);
             __builtin_amdgcn_s_waitcnt(mg::kWaitLgkm0);
             rc_copy(rs, d1, voff, unit, ch + 3, nch, ch + 3 < nfull ? kRcUnits : tail);

@@ -53,8 +53,10 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 }
 
 // (v & mask) | bias in one v_and_or_b32: gfx9 VOP3 encodings take no literal and read at
-// most one scalar operand, so the mask comes from an SGPR and the bias from a VGPR that the
-// caller keeps live (CodeK).
+// most one scalar operand, so the mask sits in an SGPR and the bias in a VGPR that the caller
+// keeps live (CodeK), both hidden from constant folding (which would split the and-or into
+// two literal-operand instructions).  The and-or itself is ordinary code, so the compiler's
+// hazard checks see it next to the matrix instructions that read its result.
 struct CodeK {
     uint32_t mask;   // wave-uniform (SGPR)
     uint32_t bias;   // VGPR
@@ -62,16 +64,14 @@ struct CodeK {
 
 __device__ __forceinline__ CodeK code_k() {
     CodeK k;
-    k.mask = __builtin_amdgcn_readfirstlane(kCodeMask);
+    k.mask = kCodeMask;
     k.bias = kCodeBias;
+    asm volatile("" : "+s"(k.mask));
+    asm volatile("" : "+v"(k.bias));
     return k;
 }
 
-__device__ __forceinline__ uint32_t c16(uint32_t v, const CodeK& k) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(k.mask), "v"(k.bias));
-    return r;
-}
+__device__ __forceinline__ uint32_t c16(uint32_t v, const CodeK& k) { return (v & k.mask) | k.bias; }
 
 // B operands (128 + q codes) of the low-nibble and high-nibble MFMAs over qs dwords x0, x1:
 // element pairs (byte 0, byte 2), (1, 3), (4, 6), (5, 7) of the 8 bytes.
@@ -201,25 +201,20 @@ __device__ __forceinline__ void a_reads(u32x4_t (&A)[8], uint32_t aa, uint64_t m
         : "memory", "scc");   // s_and_b64 writes SCC
 }
 
-// a_reads for two activation rows: the operands of MFMA t sit 128 B apart (entries
-// [t][g][m], m < 2).
-__device__ __forceinline__ void a_reads2(u32x4_t (&A)[8], uint32_t aa, uint64_t mask) {
+// Half of a_reads for a pair-major layout: the operands of four MFMAs, 128 B apart (entries
+// [t][g][m], m < 2, per pair).
+__device__ __forceinline__ void a_reads2h(u32x4_t (&A)[4], uint32_t aa, uint64_t mask) {
     uint64_t saved;
     asm volatile(
-        "s_mov_b64 %8, exec\n\t"
-        "s_and_b64 exec, exec, %10\n\t"
-        "ds_read_b128 %0, %9\n\t"
-        "ds_read_b128 %1, %9 offset:128\n\t"
-        "ds_read_b128 %2, %9 offset:256\n\t"
-        "ds_read_b128 %3, %9 offset:384\n\t"
-        "ds_read_b128 %4, %9 offset:512\n\t"
-        "ds_read_b128 %5, %9 offset:640\n\t"
-        "ds_read_b128 %6, %9 offset:768\n\t"
-        "ds_read_b128 %7, %9 offset:896\n\t"
-        "s_mov_b64 exec, %8\n\t"
+        "s_mov_b64 %4, exec\n\t"
+        "s_and_b64 exec, exec, %6\n\t"
+        "ds_read_b128 %0, %5\n\t"
+        "ds_read_b128 %1, %5 offset:128\n\t"
+        "ds_read_b128 %2, %5 offset:256\n\t"
+        "ds_read_b128 %3, %5 offset:384\n\t"
+        "s_mov_b64 exec, %4\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), "+v"(A[6]), "+v"(A[7]),
-          "=&s"(saved)
+        : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "=&s"(saved)
         : "v"(aa), "s"(mask)
         : "memory", "scc");
 }
@@ -250,12 +245,6 @@ __device__ __forceinline__ float2 sums_read(const float* p) {
     return v;
 }
 
-// The same for two activation rows: (lo row 0, lo row 1, hi row 0, hi row 1).
-__device__ __forceinline__ float4 sums_read2(const float* p) {
-    float4 v;
-    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
-    return v;
-}
 
 // Diagonal lanes of the block-diagonal activation operand: lane 16g + 4g + m for m < MR.
 __host__ __device__ constexpr uint64_t diag_mask(int mr) {
@@ -272,6 +261,8 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds
 // s_waitcnt immediates (gfx9 layout: vmcnt[3:0] expcnt[6:4] lgkmcnt[11:8] vmcnt_hi[15:14])
 constexpr int kWaitVm0 = 0x0F70;    // vmcnt(0)
 constexpr int kWaitLgkm0 = 0xC07F;  // lgkmcnt(0)
+// s_waitcnt immediate for vmcnt(n), n < 64 (vmcnt bits 3:0 and 15:14)
+__host__ __device__ constexpr int wait_vm(int n) { return (kWaitVm0 & ~0xC00F) | (n & 0x0F) | ((n >> 4) << 14); }
 
 // LDS layout of one staged activation (M_pad = MR rows, nsb blocks):
 //   A entries (16 B): [b][t][g][m]  at index (b*8 + t)*4*MR + g*MR + m

@@ -257,7 +257,10 @@ __device__ __forceinline__ u32x4_t min_operand(const uint4& h, int g) {
 }
 
 // (v & mask) | bias in one v_and_or_b32: gfx9 VOP3 takes no literal and one scalar operand,
-// so the masks sit in SGPRs and the bias in a VGPR the caller keeps live.
+// so the masks sit in SGPRs and the bias in a VGPR the caller keeps live, all hidden from
+// constant folding (which would split the and-or into two literal-operand instructions).
+// The and-or itself is ordinary code, so the compiler's hazard checks around the matrix
+// instructions see it.
 struct CodeMask {
     uint32_t lo, hi;   // 0x000F000F, 0x00F000F0 (SGPR)
     uint32_t bias;     // 0x64006400 (VGPR): fp16 1024 in both halves
@@ -265,17 +268,16 @@ struct CodeMask {
 
 __device__ __forceinline__ CodeMask code_mask() {
     CodeMask c;
-    c.lo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
-    c.hi = __builtin_amdgcn_readfirstlane(0x00F000F0u);
+    c.lo = 0x000F000Fu;
+    c.hi = 0x00F000F0u;
     c.bias = 0x64006400u;
+    asm volatile("" : "+s"(c.lo));
+    asm volatile("" : "+s"(c.hi));
+    asm volatile("" : "+v"(c.bias));
     return c;
 }
 
-__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bias) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(bias));
-    return r;
-}
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bias) { return (v & mask) | bias; }
 
 // The 8 fp16 operands sc*q of one MFMA from qs dword x.
 __device__ __forceinline__ h8_t b_operand(uint32_t x, const ChunkK& k, const CodeMask& cm) {

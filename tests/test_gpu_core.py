@@ -153,10 +153,12 @@ FAST_CASES = [
     # small-batch kernel: K split 3 / 4 blocks per wave, passes of 8 + 4, 4 + 2, and a K
     # too large for it (served by the staged kernel in passes of 4)
     (300, 2304, 8), (129, 8192, 6), (16, 512, 12), (64, 18432, 8),
-    # two-row kernel: 6 waves x 4 blocks (two tiles' worth of ragged rows), 4 x 4, 4 x 2,
-    # 6 x 3, 5 x 1 and 3 x 1 blocks per wave; the 256-row router shape
+    # small-batch kernel (2..4 rows): 8 waves x 3 blocks (ragged last tile), 8 x 2, 4 x 2,
+    # 6 x 3, 5 x 1, 3 x 1 and 1 x 1 blocks per wave, 2, 3 and 4 rows; the 256-row router
+    # shape; passes of 8 + 3 + 1, 7, 6 and 8 + 8 rows
     (6144 + 24, 6144, 2), (4096, 4096, 2), (1001, 2048, 2), (300, 4608, 2), (40, 1280, 2), (77, 768, 2),
-    (256, 6144, 2),
+    (256, 6144, 2), (6144, 6144, 3), (64, 256, 2), (64, 256, 4), (64, 512, 3), (48, 768, 4),
+    (100, 4608, 12), (1000, 6144, 7), (100, 4608, 6), (512, 4096, 16),
     # several weight-copy rounds per wave (3-block groups x 2, 2-block groups x 3): the
     # round loop must run to the end
     (64, 9216, 1), (40, 12288, 1),
