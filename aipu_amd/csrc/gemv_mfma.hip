@@ -743,10 +743,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         }
     };
 
-    // 1. rows 0, 1, then the weights; the pair is staged while the weights are in flight
+    // 1. the activations, then the weights; rows 0, 1 are staged while the weights are in
+    // flight
     uint4 xa[XI], xb[XI];
     float sa[XI], sb[XI];
     load_pair(0, xa);
+    if (MR > 2) load_pair(2, xb);   // rows >= M read as zero
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
     dma_group<GS>(wr, wW, rb, kb0, lane);
     __builtin_amdgcn_sched_barrier(0);
@@ -764,10 +766,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         R[b].q0 = *(const uint4*)(p + 16 + 32 * g);
         R[b].q1 = *(const uint4*)(p + 32 + 32 * g);
     }
-    if (MR > 2 && rows > 2) {
-        load_pair(2, xb);
-        stage_pair(xb, wW, sb);
-    }
+    if (MR > 2 && rows > 2) stage_pair(xb, wW, sb);
 
     // 3. the blocks
     u32x4_t A[4];   // block-diagonal operands of four MFMAs: off-diagonal lanes stay zero
