@@ -68,6 +68,13 @@ struct ProbPlain {
         Y[r * ystride + row] = (uint16_t)bf16_rne(v);
         if (Yf) Yf[r * ystride + row] = v;
     }
+    // one output (row n of the tile, activation row r) of the small-batch kernel
+    __device__ void store(int wg, int n, int r, float v) const {
+        const int64_t row = (int64_t)wg * kTR + n;
+        if (r >= M || row >= N) return;
+        Y[r * ystride + row] = (uint16_t)bf16_rne(v);
+        if (Yf) Yf[r * ystride + row] = v;
+    }
 };
 
 __device__ __forceinline__ int routed_expert(const int32_t* sel, int s, int E) {
@@ -688,9 +695,9 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* _
 // CU's LDS, so two workgroups share a CU as in the M = 1 kernel.
 constexpr int kSmallMaxRows = 4;
 
-template <int GS, int NW, int MR>   // MR = 2: rows 0, 1 only; MR = 4: up to four rows
+template <int GS, int NW, int MR, class Prob>   // MR = 2: rows 0, 1 only; MR = 4: up to four rows
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemvs(
-    ProbPlain<4> pb, const uint16_t* __restrict__ X, int K, int KP) {
+    Prob pb, const uint16_t* __restrict__ X0, int K, int KP) {
     constexpr int XP = GS * 32;              // 16-B pieces per activation row and wave
     constexpr int XI = (2 * XP + 63) / 64;   // pieces per lane for a pair of rows
     constexpr uint32_t kPair = GS * 1024u;   // operand entries of a pair of rows
@@ -702,6 +709,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: the copies take a scalar LDS base
     const int nsb = K / QK_K;
     const int wg = blockIdx.x;
+    if (!pb.active(wg)) return;   // workgroup-uniform: past a data-dependent grid end
+    const uint16_t* __restrict__ X = pb.act(wg, X0);
     const int rows = pb.M;   // 1 .. MR
     uint8_t* wA = s_act + (uint32_t)w * kPair;
     uint8_t* wW = s_w + (uint32_t)w * Dma<GS>::kBytes;
@@ -831,13 +840,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     __syncthreads();
     for (int e = tid; e < kTR * kSmallMaxRows; e += (int)blockDim.x) {
         const int rn = e >> 2, r = e & 3;
-        const int64_t row = (int64_t)wg * kTR + rn;
-        if (r < rows && row < pb.N) {
+        if (r < rows) {
             float v = 0.f;
             for (int k = 0; k < KP; ++k)
                 v += ((const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes + kRed))[rn * kSmallMaxRows + r];
-            pb.Y[r * pb.ystride + row] = (uint16_t)bf16_rne(v);
-            if (pb.Yf) pb.Yf[r * pb.ystride + row] = v;
+            pb.store(wg, rn, r, v);
         }
     }
 }
@@ -988,14 +995,14 @@ bool make_plans(int nsb, PlanS& p) {
     return false;
 }
 
-template <int MR>
-hipError_t runs_mr(const ProbPlain<4>& pb, const PlanS& pl, unsigned nwg, const uint16_t* X, int K, hipStream_t st) {
+template <int MR, class Prob>
+hipError_t runs_mr(const Prob& pb, const PlanS& pl, unsigned nwg, const uint16_t* X, int K, hipStream_t st) {
     const dim3 grid(nwg), block(64 * pl.KP);
     const size_t lds = (size_t)pl.lds;
     switch (pl.GS) {
-        case 1: hipLaunchKernelGGL((k_gemvs<1, kMaxW, MR>), grid, block, lds, st, pb, X, K, pl.KP); break;
-        case 2: hipLaunchKernelGGL((k_gemvs<2, kMaxW, MR>), grid, block, lds, st, pb, X, K, pl.KP); break;
-        default: hipLaunchKernelGGL((k_gemvs<3, kMaxW, MR>), grid, block, lds, st, pb, X, K, pl.KP); break;
+        case 1: hipLaunchKernelGGL((k_gemvs<1, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K, pl.KP); break;
+        case 2: hipLaunchKernelGGL((k_gemvs<2, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K, pl.KP); break;
+        default: hipLaunchKernelGGL((k_gemvs<3, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K, pl.KP); break;
     }
     return hipGetLastError();
 }
@@ -1182,6 +1189,11 @@ struct ProbUGateUp {
         for (int k = 0; k < KP; ++k) v += red[(k * kTR + n) * MR + r];
         gu[(((int64_t)u * 2 + part) * M + r) * I + (int64_t)it * kTR + n] = (uint16_t)bf16_rne(v);
     }
+    __device__ void store(int wg, int n, int r, float v) const {
+        if (r >= M) return;
+        const int u = wg / (2 * itiles), part = (wg / itiles) & 1, it = wg % itiles;
+        gu[(((int64_t)u * 2 + part) * M + r) * I + (int64_t)it * kTR + n] = (uint16_t)bf16_rne(v);
+    }
 };
 
 template <int MR>
@@ -1215,6 +1227,12 @@ struct ProbUDown {
         for (int k = 0; k < KP; ++k) v += red[(k * kTR + n) * MR + r];
         y[((int64_t)u * M + r) * H + d] = (uint16_t)bf16_rne(v);
     }
+    __device__ void store(int wg, int n, int r, float v) const {
+        const int u = wg / htiles, it = wg % htiles;
+        const int64_t d = (int64_t)it * kTR + n;
+        if (r >= M || d >= H) return;
+        y[((int64_t)u * M + r) * H + d] = (uint16_t)bf16_rne(v);
+    }
 };
 
 bool moe_union_supported(int64_t H, int64_t I, int M) {
@@ -1223,17 +1241,33 @@ bool moe_union_supported(int64_t H, int64_t I, int M) {
            gemvm_supported((int)(I / QK_K), mr);
 }
 
+// The union legs: up to four rows on the small-batch kernel (weights copied to LDS) when
+// both K's fit its plan, otherwise the register-weight kernel.
+template <int MR, class Prob>
+static hipError_t union_leg(const Prob& pb, int nsb, unsigned nwg, const uint16_t* x, int K, hipStream_t st) {
+    if constexpr (MR <= 4) {
+        PlanS ps;
+        if (make_plans(nsb, ps)) return pb.M <= 2 ? runs_mr<2>(pb, ps, nwg, x, K, st) : runs_mr<4>(pb, ps, nwg, x, K, st);
+    }
+    return run_gemvm<MR>(pb, nsb, nwg, x, K, st);
+}
+
 template <int MR>
 static hipError_t union_gemvs(const MoeUnionArgs& a, hipStream_t st) {
     const int64_t rbH = row_bytes(T_Q4_K, a.H), rbI = row_bytes(T_Q4_K, a.I);
     const int itiles = (int)(a.I / kTR), htiles = (int)((a.H + kTR - 1) / kTR);
     const ProbUGateUp<MR> pg{a.G, a.U, a.shG, a.shU, a.uidx, a.nslots, itiles, a.M, rbH, rbH * a.I, a.I, a.gu};
-    hipError_t e = run_gemvm<MR>(pg, (int)(a.H / QK_K), (unsigned)(a.max_slots * 2 * itiles), a.x, (int)a.H, st);
+    hipError_t e = union_leg<MR>(pg, (int)(a.H / QK_K), (unsigned)(a.max_slots * 2 * itiles), a.x, (int)a.H, st);
     if (e != hipSuccess) return e;
     e = a.after_gateup(st);
     if (e != hipSuccess) return e;
     const ProbUDown<MR> pd{a.D, a.shD, a.uidx, a.nslots, htiles, a.M, rbI, rbI * a.H, a.I, a.H, a.h, a.y};
-    return run_gemvm<MR>(pd, (int)(a.I / QK_K), (unsigned)(a.max_slots * htiles), a.h, (int)a.I, st);
+    return union_leg<MR>(pd, (int)(a.I / QK_K), (unsigned)(a.max_slots * htiles), a.h, (int)a.I, st);
+}
+
+int moe_union_pass_rows(int64_t H, int64_t I) {
+    PlanS p;
+    return make_plans((int)(H / QK_K), p) && make_plans((int)(I / QK_K), p) ? kSmallMaxRows : 8;
 }
 
 hipError_t launch_moe_union_mfma(const MoeUnionArgs& a, hipStream_t st) {
