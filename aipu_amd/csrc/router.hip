@@ -67,7 +67,28 @@ __global__ __launch_bounds__(64) void k_router_tail(const uint16_t* __restrict__
     router_tail_wave(logits, E, topk, scale_bits, sel, selw, sel2, selw2, gates, keys, win);
 }
 
-// One routing decision per activation row (row = workgroup).
+// One routing decision per activation row (row = workgroup), E <= kRouteMaxE: every key's
+// rank counted in parallel (route.hpp), the same decision as the one-wave tail.
+constexpr int kRankThreads = 2 * kRouteMaxE;
+
+__global__ __launch_bounds__(kRankThreads) void k_router_rank_rows(const uint16_t* __restrict__ logits, int E,
+                                                                   int topk, uint32_t scale_bits, int32_t* sel,
+                                                                   uint16_t* selw, int32_t* sel2, uint16_t* selw2) {
+    __shared__ __align__(16) uint32_t keys[kRouteMaxE];
+    __shared__ uint32_t win[kRouteMaxTopk];
+    __shared__ int32_t s_sel[kRouteMaxTopk];
+    __shared__ uint16_t s_selw[kRouteMaxTopk];
+    const int r = blockIdx.x, t = threadIdx.x;
+    route_workgroup(logits + (int64_t)r * E, E, topk, scale_bits, keys, win, s_sel, s_selw, true);
+    if (t < topk) {
+        sel[r * topk + t] = s_sel[t];
+        selw[r * topk + t] = s_selw[t];
+        if (sel2) sel2[r * topk + t] = s_sel[t];
+        if (selw2) selw2[r * topk + t] = s_selw[t];
+    }
+}
+
+// One routing decision per activation row (row = workgroup), any E <= kMaxE.
 __global__ __launch_bounds__(64) void k_router_tail_rows(const uint16_t* __restrict__ logits, int E, int topk,
                                                          uint32_t scale_bits, int32_t* sel, uint16_t* selw,
                                                          int32_t* sel2, uint16_t* selw2) {
@@ -184,6 +205,11 @@ hipError_t launch_router_tail(const uint16_t* logits, int E, int topk, uint32_t 
 
 hipError_t launch_router_tail_rows(const uint16_t* logits, int M, int E, int topk, uint32_t scale_bits, int32_t* sel,
                                    uint16_t* selw, int32_t* sel2, uint16_t* selw2, hipStream_t st) {
+    if (E <= kRouteMaxE && topk <= kRouteMaxTopk) {
+        hipLaunchKernelGGL(k_router_rank_rows, dim3(M), dim3(kRankThreads), 0, st, logits, E, topk, scale_bits, sel, selw,
+                           sel2, selw2);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_router_tail_rows, dim3(M), dim3(64), 0, st, logits, E, topk, scale_bits, sel, selw, sel2,
                        selw2);
     return hipGetLastError();
