@@ -49,6 +49,7 @@ struct ProbPlain {
     int M;
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
+    static constexpr bool kTwoTiles = false;
     static constexpr int kRows = MR;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int) const { return true; }
@@ -703,6 +704,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     constexpr uint32_t kPair = GS * 1024u;   // operand entries of a pair of rows
     constexpr uint32_t kRed = kPair;         // partial sums [n][row], after the entries in the slice
     static_assert(kRed + kTR * kSmallMaxRows * 4 <= (uint32_t)Dma<GS>::kBytes, "slice holds a pair and the sums");
+    static_assert(!Prob::kTwoTiles || MR == 2, "the second tile's copy reuses the slice rows 2, 3 would use");
     __shared__ __align__(16) uint8_t s_act[NW * kPair];
     extern __shared__ __align__(16) uint8_t s_w[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -764,16 +766,24 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     stage_pair(xa, wA, sa);
 
     // 2. the weights into registers (the compiler waits for the copies into s_w), then rows
-    // 2, 3 over the slice
+    // 2, 3 over the slice -- or, for a two-tile problem, the second tile's weights
     const int n = lane & 15, g = lane >> 4;
     Raw R[GS];
     const uint32_t rrow = (uint32_t)n * (144u * GS);
+    auto read_slice = [&]() {
 #pragma unroll
-    for (int b = 0; b < GS; ++b) {
-        const uint8_t* p = wW + rrow + 144u * b;
-        R[b].h = *(const uint4*)p;
-        R[b].q0 = *(const uint4*)(p + 16 + 32 * g);
-        R[b].q1 = *(const uint4*)(p + 32 + 32 * g);
+        for (int b = 0; b < GS; ++b) {
+            const uint8_t* p = wW + rrow + 144u * b;
+            R[b].h = *(const uint4*)p;
+            R[b].q0 = *(const uint4*)(p + 16 + 32 * g);
+            R[b].q1 = *(const uint4*)(p + 32 + 32 * g);
+        }
+    };
+    read_slice();
+    if constexpr (Prob::kTwoTiles) {
+        regs_consumed(R);   // the slice has been read: copy the second tile into it
+        const TileRef t1 = pb.tile(wg, 1);
+        dma_group<GS>(buf_rsrc(t1.base, (uint32_t)(t1.nvalid * rb)), wW, rb, kb0, lane);
     }
     if (MR > 2 && rows > 2) stage_pair(xb, wW, sb);
 
@@ -786,9 +796,18 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     const int md = (n - 4 * g) & 3;   // the diagonal lanes' activation row
     const uint32_t abase = lds_addr((md < 2 ? wA : wW) + 16u * (uint32_t)(g * 2 + (md & 1)));
     const uint64_t mask = ((1ull << rows) - 1) * 0x1000010000100001ull;   // diag_mask(rows)
-    float acc[MR];
+    constexpr int NT = Prob::kTwoTiles ? 2 : 1;
+    float acc[NT][MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    for (int k = 0; k < NT; ++k)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[k][m] = 0.f;
+#pragma unroll
+    for (int tile = 0; tile < NT; ++tile) {
+    if (tile > 0) {   // the second tile's weights (the compiler waits for the copies)
+        __builtin_amdgcn_sched_barrier(0);
+        read_slice();
+    }
 #pragma unroll
     for (int b = 0; b < GS; ++b) {
         // lane 16g + n: sums of sub-blocks 2g (lo), 2g + 1 (hi) of block b, rows m: piece
@@ -821,30 +840,40 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         for (int m = 0; m < MR; ++m) {
             const float t1 = __builtin_fmaf(H.sc1, dhi[m], H.sc0 * dlo[m]);
             const float v = __builtin_fmaf(H.m1, hi[m], H.m0 * lo[m]);
-            acc[m] = __builtin_fmaf(H.d, t1, acc[m]);
-            acc[m] = __builtin_fmaf(-H.dm, v, acc[m]);
+            acc[tile][m] = __builtin_fmaf(H.d, t1, acc[tile][m]);
+            acc[tile][m] = __builtin_fmaf(-H.dm, v, acc[tile][m]);
         }
     }
-
-    // 4. reduce over the four K-groups, then across the K parts in wave order
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        acc[m] += __shfl_xor(acc[m], 16, 64);
-        acc[m] += __shfl_xor(acc[m], 32, 64);
     }
+
+    // 4. reduce over the four K-groups, then across the K parts in wave order; a two-tile
+    // problem keeps its tiles' sums in columns 0..1 and 2..3 of the four per row
+#pragma unroll
+    for (int k = 0; k < NT; ++k)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            acc[k][m] += __shfl_xor(acc[k][m], 16, 64);
+            acc[k][m] += __shfl_xor(acc[k][m], 32, 64);
+        }
     if (lane < kTR) {
         float* red = (float*)(wW + kRed) + kSmallMaxRows * lane;
 #pragma unroll
-        for (int m = 0; m < MR; ++m) red[m] = acc[m];
+        for (int k = 0; k < NT; ++k)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) red[2 * k + m] = acc[k][m];
     }
     __syncthreads();
     for (int e = tid; e < kTR * kSmallMaxRows; e += (int)blockDim.x) {
         const int rn = e >> 2, r = e & 3;
         if (r < rows) {
-            float v = 0.f;
-            for (int k = 0; k < KP; ++k)
-                v += ((const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes + kRed))[rn * kSmallMaxRows + r];
-            pb.store(wg, rn, r, v);
+            float v = 0.f, v2 = 0.f;
+            for (int k = 0; k < KP; ++k) {
+                const float* red = (const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes + kRed) + rn * kSmallMaxRows;
+                v += red[r];
+                if constexpr (Prob::kTwoTiles) v2 += red[2 + r];
+            }
+            if constexpr (Prob::kTwoTiles) pb.store2(wg, rn, r, v, v2);
+            else pb.store(wg, rn, r, v);
         }
     }
 }
@@ -1171,6 +1200,7 @@ struct ProbUGateUp {
     uint16_t* gu;
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
+    static constexpr bool kTwoTiles = false;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int wg) const { return wg / (2 * itiles) < *nslots; }
     __device__ const uint16_t* act(int, const uint16_t* X) const { return X; }
@@ -1207,6 +1237,7 @@ struct ProbUDown {
     uint16_t* y;
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
+    static constexpr bool kTwoTiles = false;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int wg) const { return wg / htiles < *nslots; }
     __device__ const uint16_t* act(int wg, const uint16_t*) const { return h + (int64_t)(wg / htiles) * M * I; }
@@ -1235,6 +1266,35 @@ struct ProbUDown {
     }
 };
 
+// Gate/up with the SwiGLU fused, for the small-batch kernel: workgroup (u * itiles + it)
+// computes rows it*16.. of both the gate and the up projection of slot u (two tiles, the
+// second copied while the first computes) and writes h[u][m][i] = bf16(silu(g) * u) -- the
+// same rounding steps as the separate pass.
+struct ProbUGateUpH {
+    const uint8_t *G, *U, *shG, *shU;
+    const int32_t* uidx;
+    const int32_t* nslots;
+    int itiles, M;
+    int64_t rb, ebytes, I;
+    uint16_t* h;
+    static constexpr bool kTwoTiles = true;
+    __device__ bool active(int wg) const { return wg / itiles < *nslots; }
+    __device__ const uint16_t* act(int, const uint16_t* X) const { return X; }
+    __device__ TileRef tile(int wg, int part) const {
+        const int u = wg / itiles, it = wg % itiles;
+        const int e = __builtin_amdgcn_readfirstlane(uidx[u]);
+        const uint8_t* base = e < 0 ? (part ? shU : shG) : (part ? U : G) + (int64_t)e * ebytes;
+        return TileRef{base + (int64_t)it * kTR * rb, kTR, 0};
+    }
+    __device__ void store2(int wg, int n, int r, float g, float v) const {
+        if (r >= M) return;
+        const int u = wg / itiles, it = wg % itiles;
+        const uint32_t gb = bf16_rne(g), ub = bf16_rne(v);
+        h[((int64_t)u * M + r) * I + (int64_t)it * kTR + n] =
+            (uint16_t)bf16_rne(bf16_to_f32(glm_silu_bf16(gb)) * bf16_to_f32(ub));
+    }
+};
+
 bool moe_union_supported(int64_t H, int64_t I, int M) {
     const int mr = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
     return M >= 2 && M <= 8 && I % kTR == 0 && gemvm_supported((int)(H / QK_K), mr) &&
@@ -1256,10 +1316,17 @@ template <int MR>
 static hipError_t union_gemvs(const MoeUnionArgs& a, hipStream_t st) {
     const int64_t rbH = row_bytes(T_Q4_K, a.H), rbI = row_bytes(T_Q4_K, a.I);
     const int itiles = (int)(a.I / kTR), htiles = (int)((a.H + kTR - 1) / kTR);
-    const ProbUGateUp<MR> pg{a.G, a.U, a.shG, a.shU, a.uidx, a.nslots, itiles, a.M, rbH, rbH * a.I, a.I, a.gu};
-    hipError_t e = union_leg<MR>(pg, (int)(a.H / QK_K), (unsigned)(a.max_slots * 2 * itiles), a.x, (int)a.H, st);
-    if (e != hipSuccess) return e;
-    e = a.after_gateup(st);
+    hipError_t e;
+    PlanS ps, psI;
+    if (MR == 2 && make_plans((int)(a.H / QK_K), ps) && make_plans((int)(a.I / QK_K), psI)) {
+        // two rows: gate and up of a tile in one workgroup, h written directly
+        const ProbUGateUpH ph{a.G, a.U, a.shG, a.shU, a.uidx, a.nslots, itiles, a.M, rbH, rbH * a.I, a.I, a.h};
+        e = runs_mr<2>(ph, ps, (unsigned)(a.max_slots * itiles), a.x, (int)a.H, st);
+    } else {
+        const ProbUGateUp<MR> pg{a.G, a.U, a.shG, a.shU, a.uidx, a.nslots, itiles, a.M, rbH, rbH * a.I, a.I, a.gu};
+        e = union_leg<MR>(pg, (int)(a.H / QK_K), (unsigned)(a.max_slots * 2 * itiles), a.x, (int)a.H, st);
+        if (e == hipSuccess) e = a.after_gateup(st);
+    }
     if (e != hipSuccess) return e;
     const ProbUDown<MR> pd{a.D, a.shD, a.uidx, a.nslots, htiles, a.M, rbI, rbI * a.H, a.I, a.H, a.h, a.y};
     return union_leg<MR>(pd, (int)(a.I / QK_K), (unsigned)(a.max_slots * htiles), a.h, (int)a.I, st);
@@ -1267,7 +1334,7 @@ static hipError_t union_gemvs(const MoeUnionArgs& a, hipStream_t st) {
 
 int moe_union_pass_rows(int64_t H, int64_t I) {
     PlanS p;
-    return make_plans((int)(H / QK_K), p) && make_plans((int)(I / QK_K), p) ? kSmallMaxRows : 8;
+    return make_plans((int)(H / QK_K), p) && make_plans((int)(I / QK_K), p) ? 2 : 8;
 }
 
 hipError_t launch_moe_union_mfma(const MoeUnionArgs& a, hipStream_t st) {

@@ -99,8 +99,8 @@ struct MoeUnionArgs {
     hipError_t after_gateup(hipStream_t st) const { return after_gateup_fn(*this, st); }
 };
 bool moe_union_supported(int64_t H, int64_t I, int M);
-// Rows per union pass: four when both legs fit the small-batch kernel (weights copied to
-// LDS), else eight.
+// Rows per union pass: two when both legs fit the small-batch kernel (weights copied to LDS,
+// gate and up of a tile in one workgroup with the SwiGLU fused), else eight.
 int moe_union_pass_rows(int64_t H, int64_t I);
 hipError_t launch_moe_union_mfma(const MoeUnionArgs& a, hipStream_t st);
 hipError_t launch_router_tail_rows(const uint16_t* logits, int M, int E, int topk, uint32_t scale_bits, int32_t* sel,

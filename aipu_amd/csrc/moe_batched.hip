@@ -7,11 +7,11 @@
 // facc += f32(gate * bf16(y_e)) only for the experts it selected, in ascending expert index,
 // then adds the shared expert with weight 1; fbuf = bf16(facc).
 //
-// Fast mode (Q4_K, up to 8 rows per pass, 4 where the union legs fit the small-batch
+// Fast mode (Q4_K, up to 8 rows per pass, 2 where the union legs fit the small-batch
 // kernel): router logits for all rows, one routing decision per row, a one-wave union pass,
 // gate/up and down matrix-core GEMVs over the union slots (the grid is sized for the largest
-// possible union; workgroups past the live slot count return at once), h = bf16(silu(g) * u),
-// and a per-row combine.  Reference mode runs each row
+// possible union; workgroups past the live slot count return at once), h = bf16(silu(g) * u)
+// (fused into gate/up for two-row passes), and a per-row combine.  Reference mode runs each row
 // through the single-row reference path with its routing reordered by expert index.
 #include "common.hpp"
 #include "glm_act.hpp"
@@ -219,8 +219,8 @@ hipError_t launch_moe_decode_batched(const MoeArgs& a, int64_t M, hipStream_t st
         m.ws = ws + L.single;
         return launch_moe_decode(m, st);
     }
-    // passes of four rows where the union legs run on the small-batch kernel: two unions of
-    // four rows stream fewer bytes per row than one of eight on the register-weight kernel
+    // passes of two rows where the union legs run on the small-batch kernel (fused SwiGLU):
+    // per row, two-row unions cost less than wider ones on the slower kernels
     const int per = moe_union_pass_rows(a.H, a.I);
     int64_t r0 = 0;
     while (r0 < M) {

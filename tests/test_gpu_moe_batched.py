@@ -93,7 +93,8 @@ def _check_fast(y, sel, sw, X, router_type, rw, ex, sh, E, H, I, topk):
 
 
 @pytest.mark.parametrize("M,router_type,shared,topk", [(2, Q4K, True, 4), (4, BF16, False, 4), (8, Q4K, True, 8),
-                                                       (11, BF16, True, 3), (3, Q4K, False, 8)])
+                                                       (11, BF16, True, 3), (3, Q4K, False, 8), (6, BF16, True, 4),
+                                                       (2, BF16, False, 8)])
 def test_batched_fast_small(M, router_type, shared, topk):
     E, H, I = 16, 512, 256
     note(f"moe batched fast M={M} router={router_type} shared={shared} topk={topk}")
@@ -105,10 +106,12 @@ def test_batched_fast_small(M, router_type, shared, topk):
     _check_fast(y, sel, sw, X, router_type, rw, ex, sh, E, H, I, topk)
 
 
-def test_batched_fast_c2_shape():
-    """Config-2 expert shape (6144 <-> 2048, top-8) over 32 experts, 4 rows, shared expert."""
-    E, H, I, topk, M = 32, 6144, 2048, 8, 4
-    note("moe batched fast C2 shape")
+@pytest.mark.parametrize("M", [2, 4])
+def test_batched_fast_c2_shape(M):
+    """Config-2 expert shape (6144 <-> 2048, top-8) over 32 experts, shared expert; two rows
+    (gate and up of a tile in one workgroup, SwiGLU fused) and four."""
+    E, H, I, topk = 32, 6144, 2048, 8
+    note(f"moe batched fast C2 shape M={M}")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(8)
     exd = tuple(random_weights_gpu(Q4K, E * I, H, gen) if k < 2 else random_weights_gpu(Q4K, E * H, I, gen)
