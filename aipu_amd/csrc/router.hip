@@ -160,16 +160,30 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_logits_rows(const uin
 #pragma unroll
     for (int m = 0; m < MR; ++m) s0[m] = s1[m] = 0.f;
     typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-    for (int64_t c = (int64_t)t * 8; c < K; c += kRouterThreads * 8) {
-        const uint4 w = *(const uint4*)(row + c);
+    // four chunks' router loads are issued before any is used (K = 6144 is three chunks per
+    // thread); each row still folds its chunks into s0 / s1 in increasing K
+    constexpr int kU = 4;
+    for (int64_t c0 = (int64_t)t * 8; c0 < K; c0 += kU * kRouterThreads * 8) {
+        uint4 wv[kU];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            if (m >= M) break;
-            const uint4 a = *(const uint4*)(x + (int64_t)m * K + c);
-            s0[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.x), __builtin_bit_cast(bf2, w.x), s0[m], false);
-            s1[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.y), __builtin_bit_cast(bf2, w.y), s1[m], false);
-            s0[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.z), __builtin_bit_cast(bf2, w.z), s0[m], false);
-            s1[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w), __builtin_bit_cast(bf2, w.w), s1[m], false);
+        for (int u = 0; u < kU; ++u) {
+            const int64_t c = c0 + (int64_t)u * kRouterThreads * 8;
+            if (c < K) wv[u] = *(const uint4*)(row + c);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t c = c0 + (int64_t)u * kRouterThreads * 8;
+            if (c >= K) break;
+            const uint4 w = wv[u];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                if (m >= M) break;
+                const uint4 a = *(const uint4*)(x + (int64_t)m * K + c);
+                s0[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.x), __builtin_bit_cast(bf2, w.x), s0[m], false);
+                s1[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.y), __builtin_bit_cast(bf2, w.y), s1[m], false);
+                s0[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.z), __builtin_bit_cast(bf2, w.z), s0[m], false);
+                s1[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w), __builtin_bit_cast(bf2, w.w), s1[m], false);
+            }
         }
     }
 #pragma unroll
@@ -192,7 +206,10 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_logits_rows(const uin
 hipError_t launch_router_bf16_logits_rows(const uint16_t* W, const uint16_t* x, int64_t K, int E, int M,
                                           uint16_t* logits, hipStream_t st) {
     if (M < 1 || M > 8) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_router_logits_rows<8>, dim3(E), dim3(kRouterThreads), 0, st, W, x, K, M, E, logits);
+    if (M <= 2)
+        hipLaunchKernelGGL(k_router_logits_rows<2>, dim3(E), dim3(kRouterThreads), 0, st, W, x, K, M, E, logits);
+    else
+        hipLaunchKernelGGL(k_router_logits_rows<8>, dim3(E), dim3(kRouterThreads), 0, st, W, x, K, M, E, logits);
     return hipGetLastError();
 }
 
