@@ -1054,9 +1054,12 @@ hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x,
     const int nsb = (int)(K / QK_K);
     const ProbPlain<MR> pb{W, N, row_bytes(T_Q4_K, K), y, yf, ystride, M};
     const unsigned nwg = (unsigned)((N + kTR - 1) / kTR);
-    Plan1 p1;
-    if (MR == 1 && make_plan1(nsb, 1, kMaxW, p1)) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
-    if (MR > 1 && gemvm_supported(nsb, MR)) return run_gemvm<MR>(pb, nsb, nwg, x, (int)K, st);
+    if constexpr (MR == 1) {
+        Plan1 p1;
+        if (make_plan1(nsb, 1, kMaxW, p1)) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
+    } else {
+        if (gemvm_supported(nsb, MR)) return run_gemvm<MR>(pb, nsb, nwg, x, (int)K, st);
+    }
     Plan pl;
     if (!make_plan(nsb, 1, 1, MR, kMaxW, pl)) return hipErrorInvalidValue;
     return run_mfma<MR>(pb, pl, nwg, x, 0, (int64_t)M * K * 2, (int)K, M, st);
