@@ -50,6 +50,7 @@ struct ProbPlain {
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
     static constexpr bool kTwoTiles = false;
+    static constexpr uint32_t kPolicy = kNT;   // weights stream past the caches
     static constexpr int kRows = MR;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int) const { return true; }
@@ -100,6 +101,7 @@ struct ProbGateUp {
     // the gate and up tiles of a workgroup read the same activations: the two waves of each
     // K part share one staging slot (written by the gate wave)
     static constexpr bool kShareAct = true;
+    static constexpr uint32_t kPolicy = 0;   // default caching: measured faster for the MoE legs
     __device__ void setup(int wg, uint32_t* keys, uint32_t* win, int32_t* sel, uint16_t* selw) {
         const int s = wg / itiles;
         if (route.logits) {
@@ -157,6 +159,7 @@ struct ProbDown {
     const uint16_t* resid = nullptr;
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
+    static constexpr uint32_t kPolicy = 0;   // default caching: measured faster for the MoE legs
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ TileRef tile(int wg, int t) const {
         const int64_t d0 = (int64_t)wg * kTR;
@@ -392,14 +395,14 @@ struct Dma {
     static constexpr int kBytes = kInsts * 1024;           // LDS slice (the tail lanes write zeros)
 };
 
-template <int GS>
+template <int GS, uint32_t POL = kNT>
 __device__ __forceinline__ void dma_group(__amdgpu_buffer_rsrc_t wr, uint8_t* slice, int64_t rb, int blk0, int lane) {
 #pragma unroll
     for (int i = 0; i < Dma<GS>::kInsts; ++i) {
         const int j = 64 * i + lane;
         const int row = j / (9 * GS), within = j - row * (9 * GS);
         const uint32_t off = j < Dma<GS>::kPieces ? (uint32_t)(row * rb + (int64_t)blk0 * 144 + 16 * within) : kOOB;
-        lds_dma16(wr, slice + 1024 * i, off);
+        lds_dma16<POL>(wr, slice + 1024 * i, off);
     }
 }
 
@@ -454,7 +457,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
         xv[i] = buf_load16(xr, q < XP && stager ? xbase + 16u * q : kOOB);
     }
     __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
-    dma_group<GS>(wr, wW, rb, kb0, lane);
+    dma_group<GS, Prob::kPolicy>(wr, wW, rb, kb0, lane);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. stage: A entries, sums (with shared slots, the gate waves stage for both tiles and
@@ -504,12 +507,12 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
             }
             if (gi + 1 < NG) {
                 regs_consumed(R);   // the slice has been read: refill it
-                dma_group<GS>(wr, wW, rb, kb0 + (gi + 1) * GS, lane);
+                dma_group<GS, Prob::kPolicy>(wr, wW, rb, kb0 + (gi + 1) * GS, lane);
             } else if (ti + 1 < tpw) {
                 regs_consumed(R);   // the next tile's first group
                 const TileRef tn = pb.tile(t + 1, tt);
                 wr = buf_rsrc(tn.base, (uint32_t)(tn.nvalid * rb));
-                dma_group<GS>(wr, wW, rb, kb0, lane);
+                dma_group<GS, Prob::kPolicy>(wr, wW, rb, kb0, lane);
             }
 #pragma unroll
             for (int bb = 0; bb < GS; ++bb) {
@@ -761,7 +764,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     load_pair(0, xa);
     if (MR > 2) load_pair(2, xb);   // rows >= M read as zero
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(tr.base, (uint32_t)(tr.nvalid * rb));
-    dma_group<GS>(wr, wW, rb, kb0, lane);
+    dma_group<GS, Prob::kPolicy>(wr, wW, rb, kb0, lane);
     __builtin_amdgcn_sched_barrier(0);
     stage_pair(xa, wA, sa);
 
@@ -783,7 +786,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     if constexpr (Prob::kTwoTiles) {
         regs_consumed(R);   // the slice has been read: copy the second tile into it
         const TileRef t1 = pb.tile(wg, 1);
-        dma_group<GS>(buf_rsrc(t1.base, (uint32_t)(t1.nvalid * rb)), wW, rb, kb0, lane);
+        dma_group<GS, Prob::kPolicy>(buf_rsrc(t1.base, (uint32_t)(t1.nvalid * rb)), wW, rb, kb0, lane);
     }
     if (MR > 2 && rows > 2) stage_pair(xb, wW, sb);
 
@@ -1203,6 +1206,7 @@ struct ProbUGateUp {
     uint16_t* gu;
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
+    static constexpr uint32_t kPolicy = kNT;   // streaming (default caching measured slower here)
     static constexpr bool kTwoTiles = false;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int wg) const { return wg / (2 * itiles) < *nslots; }
@@ -1240,6 +1244,7 @@ struct ProbUDown {
     uint16_t* y;
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
+    static constexpr uint32_t kPolicy = kNT;   // streaming (default caching measured slower here)
     static constexpr bool kTwoTiles = false;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int wg) const { return wg / htiles < *nslots; }
@@ -1280,6 +1285,7 @@ struct ProbUGateUpH {
     int itiles, M;
     int64_t rb, ebytes, I;
     uint16_t* h;
+    static constexpr uint32_t kPolicy = kNT;   // streaming (default caching measured slower here)
     static constexpr bool kTwoTiles = true;
     __device__ bool active(int wg) const { return wg / itiles < *nslots; }
     __device__ const uint16_t* act(int, const uint16_t* X) const { return X; }

@@ -254,8 +254,9 @@ __host__ __device__ constexpr uint64_t diag_mask(int mr) {
     return m;
 }
 
+template <uint32_t POL = kNT>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t off) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, kNT);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, POL);
 }
 
 // s_waitcnt immediates (gfx9 layout: vmcnt[3:0] expcnt[6:4] lgkmcnt[11:8] vmcnt_hi[15:14])
