@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_mfma_gemv(Prob pb0, const uint16
     // ---- 2. the wave's tile and its first PD blocks of weights
     Prob pb = pb0;
     if constexpr (Prob::kRoutes) {
-        __shared__ uint32_t r_keys[kRouteMaxE];
+        __shared__ __align__(16) uint32_t r_keys[kRouteMaxE];
         __shared__ uint32_t r_win[kRouteMaxTopk];
         __shared__ int32_t r_sel[kRouteMaxTopk];
         __shared__ uint16_t r_selw[kRouteMaxTopk];
@@ -433,7 +433,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     const int t0 = wg * tpw;
     Prob pb = pb0;
     if constexpr (Prob::kRoutes) {   // routing decision (before any weight address is known)
-        __shared__ uint32_t r_keys[kRouteMaxE];
+        __shared__ __align__(16) uint32_t r_keys[kRouteMaxE];
         __shared__ uint32_t r_win[kRouteMaxTopk];
         __shared__ int32_t r_sel[kRouteMaxTopk];
         __shared__ uint16_t r_selw[kRouteMaxTopk];
@@ -1119,8 +1119,22 @@ hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t*
     return hipSuccess;
 }
 
-bool moe_route_in_kernel(int64_t E, int topk) {
-    return E >= 1 && E <= kRouteMaxE && topk >= 1 && topk <= kRouteMaxTopk && topk <= E;
+// Threads per gate/up workgroup of the plan launch_moe_gateup_mfma picks for an
+// H / 256 = nsb block row when it routes in the kernel (0: no plan); in-kernel routing ranks
+// one key per thread, so this bounds E.
+static int gateup_route_threads(int nsb, int64_t E) {
+    const int need = (int)((E + 7) & ~7);
+    Plan1 p1;
+    if (make_plan1(nsb, 2, 4, p1, true) && p1.W * 64 >= need) return p1.W * 64;
+    Plan pl;
+    if (make_plan(nsb, 2, 1, 1, 4, pl)) return pl.W * 64;
+    return 0;
+}
+
+bool moe_route_in_kernel(int64_t E, int topk, int64_t H) {
+    if (!(E >= 1 && E <= kRouteMaxE && topk >= 1 && topk <= kRouteMaxTopk && topk <= E)) return false;
+    if (H < QK_K || H % QK_K) return false;
+    return gateup_route_threads((int)(H / QK_K), E) >= (int)((E + 7) & ~7);
 }
 
 hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
@@ -1128,7 +1142,7 @@ hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint
                                   const uint16_t* x, uint16_t* h, hipStream_t st) {
     const int nsb = (int)(H / QK_K);
     if (I % kTR != 0) return hipErrorInvalidValue;
-    if (route.logits && !moe_route_in_kernel(E, topk)) return hipErrorInvalidValue;
+    if (route.logits && !moe_route_in_kernel(E, topk, H)) return hipErrorInvalidValue;
     const int64_t rb = row_bytes(T_Q4_K, H);
     const ProbGateUp pb{G, U, shG, shU, route, topk, (int)E, (int)(I / kTR), rb, rb * I, h, I, 0};
     const int itiles = (int)(I / kTR);

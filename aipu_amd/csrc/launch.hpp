@@ -71,7 +71,7 @@ struct MoeRoute {
     int32_t* sel_api;
     uint16_t* selw_api;
 };
-bool moe_route_in_kernel(int64_t E, int topk);
+bool moe_route_in_kernel(int64_t E, int topk, int64_t H);
 hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
                                   const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
                                   const uint16_t* x, uint16_t* h, hipStream_t st);

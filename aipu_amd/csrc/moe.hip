@@ -28,14 +28,13 @@ constexpr int64_t kAlign = 256;
 inline int64_t up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    int64_t counter, logits, sel, selw, h, g, u, ys, facc, total;
+    int64_t logits, sel, selw, h, g, u, ys, facc, total;
 };
 
 WsLayout ws_layout(int64_t E, int64_t H, int64_t I, int topk) {
     const int64_t nslots = topk + 1;
     WsLayout L;
     int64_t o = 0;
-    L.counter = o; o += up(4);
     L.logits = o; o += up(E * 2);
     L.sel = o;    o += up(64 * 4);
     L.selw = o;   o += up(64 * 2);
@@ -127,7 +126,7 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
 
     // 2-3. fast path: the gate/up kernel routes from the logits in every workgroup and
     // publishes the decision for the down kernel (no separate router-tail launch)
-    if (fast && !a.ascending && moe_mfma_supported(nslots, a.H, a.I) && moe_route_in_kernel(a.E, a.topk)) {
+    if (fast && !a.ascending && moe_mfma_supported(nslots, a.H, a.I) && moe_route_in_kernel(a.E, a.topk, a.H)) {
         const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};
         AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
                                         a.I, a.x, h, st));

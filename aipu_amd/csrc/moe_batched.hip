@@ -169,8 +169,10 @@ hipError_t fast_pass(const MoeArgs& a, int64_t r0, int M, const BLayout& L, hipS
         AIPU_TRY(launch_router_bf16_logits_rows((const uint16_t*)a.router_w, x, a.H, (int)a.E, M, logits, st));
     } else if (a.router_type == T_Q4_K && gemv_mfma_supported(a.E, a.H, M)) {
         AIPU_TRY(launch_gemv_mfma(a.router_w, a.E, a.H, x, M, logits, nullptr, a.E, st));
-    } else {
+    } else if (a.router_type == T_Q4_K || gemv_mixed_supported(a.router_type, a.H)) {
         AIPU_TRY(launch_gemv_fast(a.router_type, a.router_w, a.E, a.H, x, M, logits, nullptr, st));
+    } else {   // past the mixed-type kernel's staging limit: the exact kernel (within any tolerance)
+        AIPU_TRY(launch_gemv_ref(a.router_type, a.router_w, a.E, a.H, x, M, logits, nullptr, st));
     }
     AIPU_TRY(launch_router_tail_rows(logits, M, (int)a.E, a.topk, a.scale_bits, sel, selw,
                                      a.sel_idx_out ? a.sel_idx_out + r0 * a.topk : nullptr,

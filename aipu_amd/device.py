@@ -161,8 +161,8 @@ def router_topk(logits, topk, scale_bits=RSCALE_BITS, return_gates=False):
 
 
 def moe_workspace(E, H, I, topk, device):
-    """Zero-filled workspace (the fused router keeps a ticket word in it that must start at 0;
-    every call leaves it at 0 again)."""
+    """Workspace of aipu_moe_workspace_bytes() (logits, routing, h, per-slot scratch; every
+    call writes what it reads, so the initial contents do not matter)."""
     n = _lib.lib().aipu_moe_workspace_bytes(E, H, I, topk)
     if n < 0:
         raise ValueError("bad MoE shape")

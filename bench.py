@@ -28,6 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "Q4_K GEMV achieved HBM GB/s (% of peak) at M=1; MoE decode-step µs"
+REPS = 7          # timed graph replays per measurement (the median is reported)
 PEAK_GBS = 8000.0
 Q4K = 12
 BF16 = 30
@@ -51,8 +52,9 @@ def gen_q4k(n_rows, K, gen, device):
     return raw.view(-1)
 
 
-def time_graph(fn_list, reps=1):
-    """Capture fn_list into one graph, replay `reps` times; return ms per replay (list)."""
+def time_graph(fn_list, reps=1, discard=1):
+    """Capture fn_list into one graph, replay it `discard` times untimed and then `reps` times
+    bracketed by HIP events on the replay stream; return ms per timed replay (list)."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -65,6 +67,9 @@ def time_graph(fn_list, reps=1):
     with torch.cuda.graph(g):
         for f in fn_list:
             f()
+    torch.cuda.synchronize()
+    for _ in range(discard):
+        g.replay()
     torch.cuda.synchronize()
     out = []
     for _ in range(reps):
@@ -115,8 +120,8 @@ def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label
     for i in range(warmup):
         launcher(i)()
     torch.cuda.synchronize()
-    fns = [launcher(i) for i in range(steps)]
     if eager:
+        fns = [launcher(i) for i in range(steps)]
         total_ms = time_eager(fns)
         alg = wb + 2 * K * M + 2 * N * M
         us = 1000.0 * total_ms / steps
@@ -124,19 +129,20 @@ def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label
         return dict(N=N, K=K, M=M, mode=mode, us_per_launch=us, gbs=alg / (us * 1e-6) / 1e9, alg_bytes=alg,
                     weight_rotation_bytes=nbuf * wb, rotation_buffers=nbuf, pct_peak=100.0 * alg / (us * 1e-6) / 1e9 / PEAK_GBS,
                     timing="eager launches")
-    ms, _ = time_graph(fns, reps=1)
-    total_ms = ms[0]
-    # launch-group distribution: graphs of nbuf launches, replayed
-    grp, _ = time_graph([launcher(i) for i in range(nbuf)], reps=15)
-    per_launch_us = [1000.0 * t / nbuf for t in grp]
+    # One graph of max(steps, nbuf) launches, so every rotation buffer is read once per replay
+    # and the per-launch figure does not depend on --steps; one untimed replay, then the median
+    # of REPS timed replays.
+    nlaunch = max(steps, nbuf)
+    ms, _ = time_graph([launcher(i) for i in range(nlaunch)], reps=REPS)
+    per_launch_us = [1000.0 * t / nlaunch for t in ms]
     # cache-hot (labelled): the same buffer every launch
-    hot_ms, _ = time_graph([(lambda: dev.gemv(Q4K, W[0], N, K, X[0], mode=mode, out=Y[0])) for _ in range(200)])
+    hot_ms, _ = time_graph([(lambda: dev.gemv(Q4K, W[0], N, K, X[0], mode=mode, out=Y[0])) for _ in range(200)], reps=3)
     alg = wb + 2 * K * M + 2 * N * M
-    us = 1000.0 * total_ms / steps
+    us = pct(per_launch_us, 50)
     res = dict(N=N, K=K, M=M, mode=mode, us_per_launch=us, gbs=alg / (us * 1e-6) / 1e9,
-               alg_bytes=alg, weight_rotation_bytes=nbuf * wb, rotation_buffers=nbuf,
-               p10_us=pct(per_launch_us, 10), p50_us=pct(per_launch_us, 50), p90_us=pct(per_launch_us, 90),
-               hot_us=1000.0 * hot_ms[0] / 200, total_ms=total_ms)
+               alg_bytes=alg, weight_rotation_bytes=nbuf * wb, rotation_buffers=nbuf, launches_per_replay=nlaunch,
+               timed_replays=REPS, p10_us=pct(per_launch_us, 10), p50_us=us, p90_us=pct(per_launch_us, 90),
+               min_us=min(per_launch_us), hot_us=1000.0 * pct(hot_ms, 50) / 200)
     res["pct_peak"] = 100.0 * res["gbs"] / PEAK_GBS
     res["gemv_per_s"] = 1e6 / us
     res["tflops"] = 2.0 * M * N * K / (us * 1e-6) / 1e12
@@ -196,15 +202,17 @@ def bench_moe(dev, torch, steps, E=256, H=6144, I=2048, topk=8, mode="fast"):
     for i in range(3):
         step(i)()
     torch.cuda.synchronize()
-    ms, _ = time_graph([step(i) for i in range(steps)], reps=3)
+    ms, _ = time_graph([step(i) for i in range(steps)], reps=REPS)
     us = [1000.0 * t / steps for t in ms]
     per_expert = 3 * q4k_bytes(I, H)
     alg = E * H * 2 + topk * per_expert + 2 * H * 2
-    best = min(us)
-    res = dict(E=E, H=H, I=I, topk=topk, mode=mode, us_per_step=best, us_median=pct(us, 50), alg_bytes=alg,
-               gbs=alg / (best * 1e-6) / 1e9, expert_bytes_stored=3 * E * q4k_bytes(I, H))
+    med = pct(us, 50)
+    res = dict(E=E, H=H, I=I, topk=topk, mode=mode, us_per_step=med, us_min=min(us), us_p90=pct(us, 90),
+               alg_bytes=alg, gbs=alg / (med * 1e-6) / 1e9, expert_bytes_stored=3 * E * q4k_bytes(I, H),
+               timing=f"median of {REPS} replays of one HIP graph of {steps} steps (router -> top-8 -> "
+                      f"gate/up/silu -> down/combine), inputs rotated over 64 activation vectors")
     res["pct_peak"] = 100.0 * res["gbs"] / PEAK_GBS
-    log(f"MoE decode step ({mode}): {best:.1f} us, {res['gbs']:.0f} GB/s ({res['pct_peak']:.1f}% of 8 TB/s)")
+    log(f"MoE decode step ({mode}): {med:.1f} us, {res['gbs']:.0f} GB/s ({res['pct_peak']:.1f}% of 8 TB/s)")
     del ge, ue, de
     torch.cuda.empty_cache()
     return res
@@ -235,15 +243,15 @@ def bench_layer(dev, torch, steps=200, E=256, H=6144, I=2048, topk=8):
         return lambda: dev.moe_layer_decode(Q4K, rw, Q4K, ge, ue, de, E, H, I, topk, X[j], G, mode="fast",
                                             shared=sh, workspace=ws, out=Y[j], sel_out=(sel, sw))
 
-    ms, _ = time_graph([step(i) for i in range(steps)], reps=3)
-    us = min(ms) * 1000.0 / steps
+    ms, _ = time_graph([step(i) for i in range(steps)], reps=REPS)
+    us = pct(ms, 50) * 1000.0 / steps
     res = dict(E=E, H=H, I=I, topk=topk, shared=True, router="Q4_K", us_per_step=us,
                alg_bytes=(topk + 1) * 3 * q4k_bytes(I, H) + q4k_bytes(E, H) + 4 * H * 2)
     res["gbs"] = res["alg_bytes"] / (us * 1e-6) / 1e9
     for mode in ("fast", "ref"):
         out = torch.empty(H, dtype=torch.bfloat16, device=device)
-        ms, _ = time_graph([(lambda j=i: dev.rmsnorm(X[j % nx], G, mode=mode, out=out)) for i in range(200)], reps=3)
-        res[f"rmsnorm_{mode}_us"] = min(ms) * 1000.0 / 200
+        ms, _ = time_graph([(lambda j=i: dev.rmsnorm(X[j % nx], G, mode=mode, out=out)) for i in range(200)], reps=REPS)
+        res[f"rmsnorm_{mode}_us"] = pct(ms, 50) * 1000.0 / 200
     log(f"MoE layer (norm + 8+1 experts + residual): {us:.1f} us; rmsnorm fast {res['rmsnorm_fast_us']:.2f} us, "
         f"ref {res['rmsnorm_ref_us']:.2f} us")
     del ge, ue, de
@@ -274,8 +282,8 @@ def bench_batched(dev, torch, steps=100, E=256, H=6144, I=2048, topk=8, Ms=(2, 4
             unions.append(len(set(sel.cpu().numpy().reshape(-1).tolist())))
         fns = [(lambda j=i % nx: dev.moe_swiglu_decode_batched(BF16, rw, Q4K, ge, ue, de, E, H, I, topk, X[j],
                                                                  workspace=ws, out=Y)) for i in range(steps)]
-        ms, _ = time_graph(fns, reps=3)
-        us = min(ms) * 1000.0 / steps
+        ms, _ = time_graph(fns, reps=REPS)
+        us = pct(ms, 50) * 1000.0 / steps
         u = float(sum(unions)) / len(unions)
         alg = u * 3 * q4k_bytes(I, H) + E * H * 2 + 2 * M * H * 2
         res[f"m{M}"] = dict(M=M, us_per_step=us, us_per_row=us / M, mean_union=u, alg_bytes=alg,
@@ -287,25 +295,64 @@ def bench_batched(dev, torch, steps=100, E=256, H=6144, I=2048, topk=8, Ms=(2, 4
     return res
 
 
-def bench_tiles(dev, torch, steps=50):
-    """24 column tiles of 256 rows cycling Q4_K, Q6_K, Q8_0, F16 at K=6144."""
-    import numpy as np
-    from oracle import q4k_oracle as qo
+def gen_blocks(ggml_type, n_rows, K, gen, device):
+    """BASELINE config-3 distributions on the device, as a flat uint8 tensor:
+    Q4_K as gen_q4k; Q6_K ql/qh uniform bytes, int8 scales uniform -32..31, fp16 d = |N| 2^-8;
+    Q8_0 fp16 d = |N| 2^-8 then int8 uniform -127..127; F16 N(0, 0.02)."""
+    import torch
+    if ggml_type == Q4K:
+        return gen_q4k(n_rows, K, gen, device)
+    if ggml_type == 1:
+        return (torch.randn(n_rows * K, device=device, generator=gen) * 0.02).to(torch.float16).view(torch.uint8)
+    if ggml_type == 14:
+        nb = n_rows * K // 256
+        raw = torch.randint(0, 256, (nb, 210), dtype=torch.uint8, device=device, generator=gen)
+        raw[:, 192:208] = torch.randint(-32, 32, (nb, 16), dtype=torch.int8, device=device, generator=gen).view(torch.uint8)
+        raw[:, 208:210] = (torch.randn(nb, device=device, generator=gen).abs() * 2.0 ** -8).to(torch.float16) \
+            .view(torch.uint8).view(nb, 2)
+        return raw.view(-1)
+    if ggml_type == 8:
+        nb = n_rows * K // 32
+        raw = torch.empty((nb, 34), dtype=torch.uint8, device=device)
+        raw[:, 2:34] = torch.randint(-127, 128, (nb, 32), dtype=torch.int8, device=device, generator=gen).view(torch.uint8)
+        raw[:, 0:2] = (torch.randn(nb, device=device, generator=gen).abs() * 2.0 ** -8).to(torch.float16) \
+            .view(torch.uint8).view(nb, 2)
+        return raw.view(-1)
+    raise ValueError(ggml_type)
+
+
+def bench_tiles(dev, torch, steps=200, rot_bytes=1.05e9):
+    """24 column tiles of 256 rows cycling Q4_K, Q6_K, Q8_0, F16 at K=6144,
+    generated on the device.  Cold: the launches rotate over enough distinct tile sets (>= 1 GB)
+    that every launch streams its 42 MB from HBM; hot (labelled): one set, cache-resident."""
     K, rows = 6144, 256
     types = [Q4K, 14, 8, 1] * 6
-    rng = np.random.default_rng(3)
-    tiles, wbytes = [], 0
-    for i, t in enumerate(types):
-        raw = qo.random_weights(rng, t, rows, K)
-        wbytes += raw.size
-        tiles.append((t, torch.from_numpy(raw).cuda(), i * rows, rows))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
     N = rows * len(types)
-    x = torch.randn((1, K), device="cuda").to(torch.bfloat16)
+    one = [gen_blocks(t, rows, K, gen, "cuda") for t in types]
+    wbytes = sum(int(t.numel()) for t in one)
+    nset = max(2, math.ceil(rot_bytes / wbytes))
+    sets = [one] + [[gen_blocks(t, rows, K, gen, "cuda") for t in types] for _ in range(nset - 1)]
+    tsets = [[(t, w, i * rows, rows) for i, (t, w) in enumerate(zip(types, ws))] for ws in sets]
+    nx = 16
+    xs = torch.randn((nx, 1, K), device="cuda", generator=gen).to(torch.bfloat16)
     y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
-    ms, _ = time_graph([lambda: dev.gemv_tiles(tiles, N, K, x, mode="fast", out=y) for _ in range(steps)])
-    us = 1000.0 * ms[0] / steps
+    nl = max(steps, nset)
+    ms, _ = time_graph([(lambda j=i: dev.gemv_tiles(tsets[j % nset], N, K, xs[j % nx], mode="fast", out=y))
+                        for i in range(nl)], reps=REPS)
+    us = 1000.0 * pct(ms, 50) / nl
+    hot_ms, _ = time_graph([(lambda j=i: dev.gemv_tiles(tsets[0], N, K, xs[j % nx], mode="fast", out=y))
+                            for i in range(steps)], reps=REPS)
+    hot = 1000.0 * pct(hot_ms, 50) / steps
     alg = wbytes + 2 * K + 2 * N
-    return dict(N=N, K=K, us=us, alg_bytes=alg, gbs=alg / (us * 1e-6) / 1e9, cache="resident (42 MB < 256 MB MALL)")
+    del sets, tsets
+    torch.cuda.empty_cache()
+    log(f"mixed tiles: cold {us:.1f} us ({alg / (us * 1e-6) / 1e9:.0f} GB/s), hot {hot:.1f} us")
+    return dict(N=N, K=K, us=us, alg_bytes=alg, gbs=alg / (us * 1e-6) / 1e9,
+                pct_peak=100.0 * alg / (us * 1e-6) / 1e9 / PEAK_GBS, rotation_sets=nset,
+                rotation_bytes=nset * wbytes, timing=f"median of {REPS} replays of one HIP graph of {nl} launches",
+                hot_us_cache_resident=hot, hot_gbs_cache_resident=alg / (hot * 1e-6) / 1e9)
 
 
 def bench_prefill(dev, torch, M=512, K=6144, N=16384, reps=20):
@@ -320,8 +367,8 @@ def bench_prefill(dev, torch, M=512, K=6144, N=16384, reps=20):
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     ws = dev.prefill_workspace(M, K, "cuda")
     fns = [(lambda j=i % nbuf: dev.gemm_prefill(Q4K, W[j], N, K, x, out=y, workspace=ws)) for i in range(reps)]
-    ms, _ = time_graph(fns, reps=3)
-    t = min(ms) / reps
+    ms, _ = time_graph(fns, reps=REPS)
+    t = pct(ms, 50) / reps
     fl = 2.0 * M * N * K
     del W
     torch.cuda.empty_cache()
@@ -339,8 +386,8 @@ def bench_lmhead(dev, torch, V=154880, K=6144, reps=20):
     x = torch.randn(K, device="cuda", generator=gen).to(torch.bfloat16)
     ws = dev.lm_head_workspace(V, "cuda")
     fns = [(lambda: dev.lm_head(w, x, workspace=ws)) for _ in range(reps)]
-    ms, _ = time_graph(fns, reps=3)
-    t = min(ms) / reps
+    ms, _ = time_graph(fns, reps=REPS)
+    t = pct(ms, 50) / reps
     alg = 2 * V * K + 2 * K + 2 * V + 4
     del w
     torch.cuda.empty_cache()
@@ -570,7 +617,6 @@ def main():
         for M in (2, 4, 8):
             extra[f"gemv_c1_m{M}"] = bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, label="C1")
         extra["mixed_tiles_c3"] = bench_tiles(dev, torch)
-        log(f"mixed tiles: {extra['mixed_tiles_c3']['us']:.1f} us")
         extra["prefill_c4"] = bench_prefill(dev, torch)
         log(f"prefill: {extra['prefill_c4']['ms']:.2f} ms, {extra['prefill_c4']['tflops']:.1f} TFLOP/s")
         extra["lm_head_f4"] = bench_lmhead(dev, torch)
@@ -596,7 +642,8 @@ def main():
         "config": {"workload": "Q4_K GEMV M=1 K=N=6144 (north-star shape; BASELINE configs[1] at M=1)",
                    "M": 1, "K": 6144, "N": 6144, "mode": "fast", "weights": "Q4_K (ggml 144 B / 256 w)",
                    "activations": "bf16", "weight_rotation_bytes": head["weight_rotation_bytes"],
-                   "timed_region": "one HIP graph of `steps` launches, HIP events on the launch stream"},
+                   "timed_region": "median over 7 replays of one HIP graph of max(steps, rotation buffers) "
+                                   "launches, HIP events on the replay stream around each replay"},
         "pct_of_peak": round(head["pct_peak"], 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": None},

@@ -6,8 +6,8 @@
  *   - takes plain device pointers and int64 sizes (no framework types);
  *   - is stream-ordered on the hipStream_t passed as `stream` (NULL = default stream)
  *     and never synchronises the host;
- *   - never allocates device memory; entry points that need scratch take a caller-owned,
- *     zero-initialised `workspace` of at least the size *_workspace_bytes() returns;
+ *   - never allocates device memory; entry points that need scratch take a caller-owned
+ *     `workspace` (any contents) of at least the size *_workspace_bytes() returns;
  *   - validates its arguments before touching the GPU and returns AIPU_OK (0) or a negative
  *     status; aipu_last_error() then returns a thread-local message.
  *
@@ -79,7 +79,9 @@ int aipu_gemv_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t 
 /* The GEMM core: y[M][N] = bf16(x[M][K] . dequant(w)^T) straight from ggml blocks.
  * Replaces matmul_q4k(x, QW.dequant()) (tools/glm_model_q4k_ref.py:470-472 with
  * tools/q4k_matmul_gen.py:28-40) and the glm_matmul_q4k datapath (src/glm_matmul_q4k.v:50-288).
- * Types: Q4_K, Q6_K, Q8_0, F16, BF16.  K must be a multiple of the type's block size.
+ * Types: Q4_K, Q6_K, Q8_0, F16, BF16.  K must be a multiple of 256 for every type: the
+ * reference's datapath works in 256-weight super-blocks along K for all types (a Q8_0
+ * super-block is 8 blocks of 32; src/glm_matmul_q4k.v:90-91, tools/q4k_mixed_gen.py:131,143,296).
  * y_f32 (nullable) receives the fp32 accumulators.  M >= 1 (M = K+1 <= 8 for speculative
  * verification batches; large M is served too, see aipu_gemm_prefill). */
 int aipu_gemv(int ggml_type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
@@ -121,10 +123,10 @@ int aipu_fp32_rsqrt(const float* x, int64_t n, float* y, void* stream);
 int aipu_router_topk(const uint16_t* logits, int64_t E, int topk, uint32_t scale_bits,
                      int32_t* sel_idx, uint16_t* sel_w, uint16_t* gates, void* stream);
 
-/* Workspace bytes for aipu_swiglu_expert / aipu_moe_swiglu_decode.  The workspace must be
- * zero-filled before its first use (it holds a ticket counter the decode step's router
- * uses for its last-workgroup hand-off; every call leaves it at zero again) and must not be
- * shared by calls that can run concurrently. */
+/* Workspace bytes for aipu_swiglu_expert / aipu_moe_swiglu_decode.  The workspace holds the
+ * router logits, the routing decision, h and per-slot scratch; every call writes what it
+ * reads, so its contents on entry do not matter.  It must not be shared by calls that can
+ * run concurrently. */
 int64_t aipu_moe_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
 
 /* One SwiGLU expert: gate/up GEMVs (bf16), h = bf16(f32(silu(gate)) * f32(up)),
@@ -157,8 +159,8 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
  * union-skip batch of src/glm_decoder_block_q4k.v:530-560,836-906: the union of the rows'
  * experts is evaluated once, in ascending expert index, and each row accumulates
  * facc += f32(gate * bf16(y_e)) for its own experts in that order, then the shared expert
- * with weight 1.  Workspace: aipu_moe_batched_workspace_bytes(E, H, I, topk), zero-filled
- * before first use; other arguments as aipu_moe_swiglu_decode. */
+ * with weight 1.  Workspace: aipu_moe_batched_workspace_bytes(E, H, I, topk) bytes, any
+ * contents; other arguments as aipu_moe_swiglu_decode. */
 int64_t aipu_moe_batched_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
 int aipu_moe_swiglu_decode_batched(int router_type, const void* router_w, int ggml_type,
                                    const void* gate_exps, const void* up_exps, const void* down_exps,
@@ -180,7 +182,7 @@ int aipu_rmsnorm(const uint16_t* x, const uint16_t* gamma, int64_t n, uint16_t* 
  * step (as aipu_moe_swiglu_decode) on rmsnorm(h, gamma).  Replaces
  * tools/glm_model_q4k_ref.py:797-810 (decoder_block after the attention residual).
  * Arguments as aipu_moe_swiglu_decode with x -> h and gamma[H] added; the workspace is
- * aipu_moe_layer_workspace_bytes(E, H, I, topk) bytes, zero-filled before first use. */
+ * aipu_moe_layer_workspace_bytes(E, H, I, topk) bytes, any contents. */
 int64_t aipu_moe_layer_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
 int aipu_moe_layer_decode(int router_type, const void* router_w, int ggml_type,
                           const void* gate_exps, const void* up_exps, const void* down_exps,

@@ -188,6 +188,32 @@ def test_gemv_fast_tolerance(N, K, M):
     assert np.array_equal(u32(h_f32(yf2)), u32(h_f32(yf)))
 
 
+# Fast-mode batch invariance: row r of an M-row call is bit-identical to the one-row call on
+# that row, fp32 accumulators included, so a speculative-verify batch computes exactly what
+# greedy decoding computes (the reference gates PE_M rows against per-row PE_M = 1 runs,
+# Makefile:1500-1506).  Covers every row count of a verify batch at the BASELINE shape and the
+# other matrix-core shapes (ragged N, passes of 8 + remainder).  It holds while the rows of a
+# batch are served by the matrix-core kernels, i.e. K <= 7168 (every BASELINE shape); above
+# that, batches of 2+ rows fall back to the streaming kernel's different summation order.
+INVARIANCE_CASES = [(6144, 6144, m) for m in (2, 3, 4, 5, 6, 7, 8)] + [
+    (4096, 4096, 4), (1001, 2048, 8), (300, 2304, 3), (512, 4096, 12), (64, 7168, 8)]
+
+
+@pytest.mark.parametrize("N,K,M", INVARIANCE_CASES)
+def test_gemv_fast_batch_invariance(N, K, M):
+    note(f"gemv fast batch invariance N={N} K={K} M={M}")
+    rng = np.random.default_rng(7 * N + K + M)
+    raw = qo.random_q4k_blocks(rng, N * K // 256)
+    x = qo.random_bf16(rng, (M, K))
+    wd = d_u8(raw)
+    y, yf = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(x), mode="fast", out_f32=True)
+    yb, yfb = h_bits(y), u32(h_f32(yf))
+    for r in range(M):
+        y1, yf1 = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(x[r:r + 1]), mode="fast", out_f32=True)
+        assert_bits_equal(u32(h_f32(yf1))[0], yfb[r], f"row {r} of M={M}: fp32 accumulators")
+        assert_bits_equal(h_bits(y1)[0], yb[r], f"row {r} of M={M}: bf16 outputs")
+
+
 # Q6_K / Q8_0 / F16 through the mixed-type kernel: shapes where some waves own no blocks
 # (K = 256, 768), odd block counts (1280), the largest staged K (15360; larger K is served by
 # the exact kernel), ragged row counts and several activation rows.

@@ -154,34 +154,62 @@ def _check_moe_output(y_bits, x, ex, sh, sel, selw, H, I):
     assert np.all(np.abs(a - b) <= 2.0 ** -7 * mag + 2.0 ** -6 * np.abs(b))
 
 
-def test_moe_fast_c2_shape():
-    """BASELINE config 2 shape (hidden 6144, expert intermediate 2048, top-8) over 32 experts."""
-    E, H, I, topk = 32, 6144, 2048, 8
-    note("moe fast C2 shape")
+def _expert_rows(t, E, idx):
+    """Host copies of experts `idx` (in that order) of a device `_exps` stack, as a new stack."""
+    per = t.numel() // E
+    return np.concatenate([t[int(e) * per:(int(e) + 1) * per].cpu().numpy() for e in idx])
+
+
+@pytest.mark.parametrize("mode", ["fast", "ref"])
+def test_moe_c2_full_256_experts(mode):
+    """BASELINE config 2 at its own size -- the benchmarked step: 256 experts, hidden 6144,
+    expert intermediate 2048, top-8, bf16 router (routing in the gate/up kernel in fast mode).
+    Fast: the routing equals the reference tail applied to the fast logits and y is within the
+    MoE bound; ref: routing and y bit-exact vs the oracle.  Only the 8 routed experts are
+    copied to the host."""
+    E, H, I, topk = 256, 6144, 2048, 8
+    note(f"moe C2 E=256 {mode}")
     g = torch.Generator(device="cuda")
-    g.manual_seed(5)
+    g.manual_seed(256)
     ge = random_weights_gpu(Q4K, E * I, H, g)
     ue = random_weights_gpu(Q4K, E * I, H, g)
     de = random_weights_gpu(Q4K, E * H, I, g)
-    rng = np.random.default_rng(5)
+    rng = np.random.default_rng(256)
     rw = qo.random_bf16(rng, (E, H), scale=0.05).view(np.uint8).reshape(-1)
     x = qo.random_bf16(rng, H, scale=0.05)
-    y, sel, sw = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, de, E, H, I, topk, d_bf16(x), mode="fast")
+    y, sel, sw = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, de, E, H, I, topk, d_bf16(x), mode=mode)
+    if mode == "fast":
+        logits = h_bits(dev.gemv(BF16, d_u8(rw), E, H, d_bf16(x[None]), mode="fast"))[0]
+    else:
+        logits = go.router_logits(BF16, rw.view(np.uint16), E, H, x)
+    es, ew, _ = go.router_tail(logits, topk)
+    assert np.array_equal(sel.cpu().numpy(), es)
+    assert_bits_equal(h_bits(sw), ew, "sel_w")
+    sub = tuple(_expert_rows(t, E, es) for t in (ge, ue, de))   # routed experts in slot order
+    if mode == "fast":
+        _check_moe_output(h_bits(y), x, sub, None, np.arange(topk), ew, H, I)
+    else:
+        ys = [go.swiglu_expert(x, sub[0].reshape(topk, -1)[s], sub[1].reshape(topk, -1)[s],
+                               sub[2].reshape(topk, -1)[s], Q4K, H, I)[0] for s in range(topk)]
+        yref, _ = go.moe_combine(ew, ys)
+        assert_bits_equal(h_bits(y), yref, "moe ref C2 E=256")
+
+
+@pytest.mark.parametrize("H,E", [(512, 300), (1280, 256), (1536, 512)])
+def test_moe_fast_router_wider_than_gateup_plan(H, E):
+    """Expert counts that the gate/up plan cannot rank in-kernel (one key per thread and fewer
+    threads than keys) take the separate router-tail launch and stay correct."""
+    I, topk = 256, 8
+    note(f"moe fast wide router H={H} E={E}")
+    rng = np.random.default_rng(H + E)
+    rw, ex, sh, x = _moe_case(rng, E, H, I, BF16, False)
+    y, sel, sw = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, d_u8(ex[0]), d_u8(ex[1]), d_u8(ex[2]), E, H, I, topk,
+                                       d_bf16(x), mode="fast")
     lf = h_bits(dev.gemv(BF16, d_u8(rw), E, H, d_bf16(x[None]), mode="fast"))[0]
     es, ew, _ = go.router_tail(lf, topk)
     assert np.array_equal(sel.cpu().numpy(), es)
     assert_bits_equal(h_bits(sw), ew, "sel_w")
-    ex = tuple(t.cpu().numpy() for t in (ge, ue, de))
     _check_moe_output(h_bits(y), x, ex, None, es, ew, H, I)
-    # reference mode on the same inputs: exact vs oracle for the routing it picks
-    yr, selr, swr = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, de, E, H, I, topk, d_bf16(x), mode="ref")
-    lr = go.router_logits(BF16, rw.view(np.uint16), E, H, x)
-    er, ewr, _ = go.router_tail(lr, topk)
-    assert np.array_equal(selr.cpu().numpy(), er)
-    ys = [go.swiglu_expert(x, ex[0].reshape(E, -1)[e], ex[1].reshape(E, -1)[e], ex[2].reshape(E, -1)[e], Q4K, H,
-                           I)[0] for e in er]
-    yref, _ = go.moe_combine(ewr, ys)
-    assert_bits_equal(h_bits(yr), yref, "moe ref C2")
 
 
 # ----------------------------------------------------------------- tiles

@@ -125,3 +125,34 @@ def test_batched_fast_c2_shape(M):
     ex = tuple(t.cpu().numpy() for t in exd)
     sh = tuple(t.cpu().numpy() for t in shd)
     _check_fast(h_bits(y), sel.cpu().numpy(), h_bits(sw), X, BF16, rw, ex, sh, E, H, I, topk)
+
+
+@pytest.mark.parametrize("H,I,topk", [(512, 256, 4), (6144, 2048, 8)])
+def test_batched_fast_rows_independent_of_batch(H, I, topk):
+    """Fast mode: a row's output, routing and weights do not depend on which other rows share
+    its batch (M >= 2, where every row combines its experts in ascending index): the rows of an
+    8-row batch equal the same rows run as batches of 2, 3 and 5 (the batch sizes that split
+    into different passes), bit for bit."""
+    E, M = 32, 8
+    note(f"moe batched fast batch composition H={H} I={I} topk={topk}")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(H + topk)
+    exd = tuple(random_weights_gpu(Q4K, E * I, H, gen) if k < 2 else random_weights_gpu(Q4K, E * H, I, gen)
+                for k in range(3))
+    shd = (random_weights_gpu(Q4K, I, H, gen), random_weights_gpu(Q4K, I, H, gen), random_weights_gpu(Q4K, H, I, gen))
+    rng = np.random.default_rng(H + topk)
+    rw = qo.random_bf16(rng, (E, H), scale=0.05).view(np.uint8).reshape(-1)
+    X = qo.random_bf16(rng, (M, H), scale=0.05)
+
+    def run(rows):
+        y, sel, sw = dev.moe_swiglu_decode_batched(BF16, d_u8(rw), Q4K, *exd, E, H, I, topk, d_bf16(X[rows]),
+                                                   mode="fast", shared=shd)
+        return h_bits(y), sel.cpu().numpy(), h_bits(sw)
+
+    y8, sel8, sw8 = run(list(range(M)))
+    for rows in ([0, 1], [2, 3, 4], [3, 4, 5, 6, 7], [7, 0]):
+        y, sel, sw = run(rows)
+        for i, r in enumerate(rows):
+            assert np.array_equal(sel[i], sel8[r]), f"row {r} routing in batch {rows}"
+            assert_bits_equal(sw[i], sw8[r], f"row {r} sel_w in batch {rows}")
+            assert_bits_equal(y[i], y8[r], f"row {r} y in batch {rows}")
