@@ -80,6 +80,8 @@ SIGNATURES = {
     "aipu_swiglu_expert": (_I, [_I, _P, _P, _P, _I64, _I64, _P, _P, _P, _I, _P, _I64, _P]),
     "aipu_moe_swiglu_decode": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _U32, _P, _P, _P,
                                     _P, _I, _P, _I64, _P]),
+    "aipu_moe_swiglu_decode_noalloc": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _U32, _P, _P,
+                                            _P, _P, _I, _P]),
     "aipu_moe_batched_workspace_bytes": (_I64, [_I64, _I64, _I64, _I]),
     "aipu_moe_swiglu_decode_batched": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _U32, _P,
                                             _I64, _P, _P, _P, _I, _P, _I64, _P]),

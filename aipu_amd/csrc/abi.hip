@@ -1,7 +1,9 @@
 // The extern "C" entry points declared in include/aipu_q4k.h: argument validation (before
 // any GPU work), dispatch to the launchers, and the thread-local error message.
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -285,6 +287,78 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
                             E >= 1 && topk >= 1 ? aipu::moe_workspace_bytes(E, H, I, topk) : 0, a);
     if (rc) return rc;
     return hip_status(aipu::launch_moe_decode(a, S(stream)), "aipu_moe_swiglu_decode");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------- MoE decode step without allocation
+// For callers that cannot allocate (code under HIP graph capture, tight serving loops,
+// harnesses that forbid it): the MoE step's scratch is a file-scope device array, one copy
+// per GPU for the life of the process.  In host code `scratch` is only a stand-in symbol;
+// its device address comes from hipGetSymbolAddress, taken once per device with that device
+// current, and only that address is ever passed to kernels.  Calls on one GPU share the
+// array, so calls that can overlap on one GPU race.  Nothing in it needs to start at zero:
+// every call writes what it reads (logits, routing, h, the fp32 running sum).
+namespace {
+
+constexpr int64_t kScratchBytes = AIPU_NOALLOC_SCRATCH_BYTES;   // per GPU
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of this GPU's scratch array (the stream's device, or the current device for
+// the null stream); looked up on the first call on each device.
+int scratch_for(hipStream_t st, void** out) {
+    int dev = -1;
+    hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(AIPU_ERR_HIP, "scratch: device of the stream: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(AIPU_ERR_ARG, "scratch: device %d out of range", dev);
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            int prev = -1;
+            e = hipGetDevice(&prev);
+            if (e == hipSuccess && prev != dev) e = hipSetDevice(dev);
+            if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            const hipError_t e2 = (prev >= 0 && prev != dev) ? hipSetDevice(prev) : hipSuccess;
+            if (e != hipSuccess || !p)
+                return fail(AIPU_ERR_HIP, "scratch: hipGetSymbolAddress on device %d: %s", dev,
+                            hipGetErrorString(e != hipSuccess ? e : hipErrorInvalidSymbol));
+            if (e2 != hipSuccess) return fail(AIPU_ERR_HIP, "scratch: restoring device %d: %s", prev, hipGetErrorString(e2));
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return AIPU_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aipu_moe_swiglu_decode_noalloc(int router_type, const void* router_w, int ggml_type, const void* gate_exps,
+                                   const void* up_exps, const void* down_exps, const void* shared_gate,
+                                   const void* shared_up, const void* shared_down, int64_t E, int64_t H, int64_t I,
+                                   int topk, uint32_t scale_bits, const uint16_t* x, uint16_t* y, int32_t* sel_idx,
+                                   uint16_t* sel_w, int mode, void* stream) {
+    const int64_t need = E >= 1 && topk >= 1 && H >= 1 && I >= 1 ? aipu::moe_workspace_bytes(E, H, I, topk) : 0;
+    if (need > kScratchBytes)
+        return fail(AIPU_ERR_WORKSPACE, "aipu_moe_swiglu_decode_noalloc: E=%lld H=%lld I=%lld topk=%d needs %lld "
+                                        "bytes of scratch, more than the %lld-byte per-GPU array",
+                    (long long)E, (long long)H, (long long)I, topk, (long long)need, (long long)kScratchBytes);
+    void* ws = nullptr;
+    int rc = scratch_for(S(stream), &ws);
+    if (rc) return rc;
+    aipu::MoeArgs a;
+    rc = moe_args(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, shared_gate, shared_up, shared_down,
+                  E, H, I, topk, scale_bits, x, y, sel_idx, sel_w, mode, ws, kScratchBytes, need, a);
+    if (rc) return rc;
+    return hip_status(aipu::launch_moe_decode(a, S(stream)), "aipu_moe_swiglu_decode_noalloc");
 }
 
 int64_t aipu_moe_batched_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk) {

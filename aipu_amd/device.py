@@ -200,8 +200,28 @@ def moe_swiglu_decode(router_type, router_w, ggml_type, gate_exps, up_exps, down
     return y, sel, sw
 
 
+def moe_swiglu_decode_noalloc(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, E, H, I, topk, x,
+                              mode="fast", shared=None, scale_bits=RSCALE_BITS, out=None, sel_out=None):
+    """moe_swiglu_decode through aipu_moe_swiglu_decode_noalloc: no workspace, the library's
+    per-GPU scratch array instead (calls that overlap on one GPU must be serialised).  With
+    `out` and `sel_out` given, the call allocates nothing at all."""
+    _need_cuda(router_w, gate_exps, up_exps, down_exps, x)
+    x = _bf16(x).reshape(-1)
+    y = out if out is not None else torch.empty(H, dtype=torch.bfloat16, device=x.device)
+    if sel_out is None:
+        sel = torch.empty(topk, dtype=torch.int32, device=x.device)
+        sw = torch.empty(topk, dtype=torch.bfloat16, device=x.device)
+    else:
+        sel, sw = sel_out
+    sg, su, sd = shared if shared is not None else (None, None, None)
+    call("aipu_moe_swiglu_decode_noalloc", router_type, _ptr(router_w), ggml_type, _ptr(gate_exps), _ptr(up_exps),
+         _ptr(down_exps), _ptr(sg), _ptr(su), _ptr(sd), E, H, I, topk, scale_bits, _ptr(x), _ptr(y), _ptr(sel),
+         _ptr(sw), _mode(mode), _stream(x))
+    return y, sel, sw
+
+
 def moe_batched_workspace(E, H, I, topk, device):
-    """Zero-filled workspace for moe_swiglu_decode_batched."""
+    """Workspace for moe_swiglu_decode_batched (any initial contents)."""
     n = _lib.lib().aipu_moe_batched_workspace_bytes(E, H, I, topk)
     if n < 0:
         raise ValueError("bad MoE shape")

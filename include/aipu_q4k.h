@@ -153,6 +153,23 @@ int aipu_moe_swiglu_decode(int router_type, const void* router_w, int ggml_type,
                            int32_t* sel_idx, uint16_t* sel_w, int mode, void* workspace,
                            int64_t ws_bytes, void* stream);
 
+/* aipu_moe_swiglu_decode without a workspace argument and without any allocation: no
+ * counterpart in the reference.  It is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid allocation).  The
+ * step's scratch is a library-owned per-GPU device array of AIPU_NOALLOC_SCRATCH_BYTES, held
+ * from the first call on a GPU until the process ends; shapes whose
+ * aipu_moe_workspace_bytes() exceeds it return AIPU_ERR_WORKSPACE.  All calls on one GPU
+ * share that array, so calls that can overlap on one GPU (several streams or host threads)
+ * race: serialise them.  Results are bit-identical to aipu_moe_swiglu_decode. */
+#define AIPU_NOALLOC_SCRATCH_BYTES (4LL << 20)
+int aipu_moe_swiglu_decode_noalloc(int router_type, const void* router_w, int ggml_type,
+                                   const void* gate_exps, const void* up_exps,
+                                   const void* down_exps, const void* shared_gate,
+                                   const void* shared_up, const void* shared_down, int64_t E,
+                                   int64_t H, int64_t I, int topk, uint32_t scale_bits,
+                                   const uint16_t* x, uint16_t* y, int32_t* sel_idx,
+                                   uint16_t* sel_w, int mode, void* stream);
+
 /* MoE decode step for M activation rows x[M][H] -> y[M][H], routing per row
  * (sel_idx[M][topk], sel_w[M][topk], nullable, in each row's router order).  M = 1 is
  * aipu_moe_swiglu_decode (routed experts combined in slot order).  M > 1 follows the
