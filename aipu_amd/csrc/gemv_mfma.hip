@@ -5,9 +5,12 @@
 // Workgroup.  A workgroup owns T tiles of 16 rows (T = 1 plain, 2 gate/up, nslots down) and
 // splits each tile's K into KP equal parts of bpk blocks; wave w computes part w % KP of
 // tile w / KP, so W = T * KP waves.  The activations are staged once per workgroup in LDS
-// in the MFMA operand order.  Per-wave partial sums are reduced across the wave's four
-// K-groups with two cross-lane adds, then across the KP parts in fixed order through LDS,
-// so every result is deterministic.
+// in the MFMA operand order.  The MoE legs (k_gemv1, k_mfma_gemv) reduce per-wave partial
+// sums across the wave's four K-groups with two cross-lane adds, then across the KP parts in
+// fixed order through LDS; the plain and batched-union kernels for M = 2..8 (k_gemvs, k_gemvm)
+// keep every block term and sum them in the fast-mode order of mfma_gemv.hpp, the order of the
+// single-row kernel (gemv_persist.hip), so a row of a batch equals its single-row result.
+// Every result is deterministic.
 //
 // Memory order.  Every thread issues its activation loads first, then the wave's first PD
 // blocks of weights (buffer loads, streaming cache policy), and only then waits for the
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* _
     constexpr int kPieces = MR * BPK * 32;   // 16-B activation pieces per wave
     constexpr int kXL = (kPieces + 63) / 64;
     __shared__ __align__(16) uint8_t s_act[kMaxW * kWave];
-    __shared__ float red[kMaxW * kTR * MR];
+    static_assert(kTR * MR * kMaxW * BPK * 4 <= kMaxW * kWave, "the block terms fit over the operand entries");
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nsb = K / QK_K;
@@ -618,9 +621,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* _
     const HdrSel hs = hdr_sel(g);
     const CodeK ck = code_k();
     u32x4_t A[NH][8];
-    float acc[MR];
-#pragma unroll
-    for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+    float bt[BPK][NH];   // block terms: lane 16i + n holds row n, activation row 4h + i
     f32x4_t dlo[NH], dhi[NH];
 #pragma unroll
     for (int h = 0; h < NH; ++h) dlo[h] = dhi[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -659,29 +660,37 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* _
         }
         const Hdr H = hdr_decode(R[b].h, hs);
 #pragma unroll
-        for (int h = 0; h < NH; ++h)
+        for (int h = 0; h < NH; ++h) {
+            float t[4];
 #pragma unroll
-            for (int r = 0; r < MRQ; ++r) {
-                const int m = 4 * h + r;
-                const float t1 = __builtin_fmaf(H.sc1, dhi[h][r], H.sc0 * dlo[h][r]);
-                const float v = __builtin_fmaf(H.m1, ahi[m], H.m0 * alo[m]);
-                acc[m] = __builtin_fmaf(H.d, t1, acc[m]);
-                acc[m] = __builtin_fmaf(-H.dm, v, acc[m]);
-            }
+            for (int r = 0; r < 4; ++r) t[r] = r < MRQ ? block_term(H, dlo[h][r], dhi[h][r], alo[4 * h + r], ahi[4 * h + r]) : 0.f;
+            bt[b][h] = MRQ == 4 ? block_sum4(t[0], t[1], t[2], t[3]) : block_sum2(t[0], t[1]);
+        }
     }
 
-    // 5. reduce over the four K-groups, then across the K parts
+    // 5. the block terms of all K parts into LDS (over the operand entries, once every wave
+    // is past its block loop), then each output in the fast-mode order
+    float* terms = (float*)s_act;   // [n][m][b], b < nsb
+    __syncthreads();
+    {
+        const int i = lane >> 4;   // activation row within the set (MRQ = 2: rows 0, 1 twice)
+        if (i < MRQ) {
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-        acc[r] += __shfl_xor(acc[r], 16, 64);
-        acc[r] += __shfl_xor(acc[r], 32, 64);
-    }
-    if (lane < kTR) {
+            for (int b = 0; b < BPK; ++b)
 #pragma unroll
-        for (int r = 0; r < MR; ++r) red[(w * kTR + lane) * MR + r] = acc[r];
+                for (int h = 0; h < NH; ++h) terms[(n * MR + 4 * h + i) * nsb + kb0 + b] = bt[b][h];
+        }
     }
     __syncthreads();
-    pb.finish(wg, red, KP, tid);
+    // eight lanes per output (uniform trip count: every lane takes part in the cross-lane adds)
+    const int per = (int)(blockDim.x >> 3);
+    for (int o0 = 0; o0 < kTR * MR; o0 += per) {
+        const int o = o0 + (tid >> 3), rn = o / MR, m = o - rn * MR;
+        const bool valid = o < kTR * MR && m < pb.M;
+        const float* te = terms + (valid ? (rn * MR + m) * nsb : 0);
+        const float y = canon_sum8(nsb, lane & 7, [&](int b) { return te[b]; });
+        if (valid && (lane & 7) == 0) pb.store(wg, rn, m, y);
+    }
 }
 
 // ------------------------------------------------- small-batch kernel (M = 2 .. 4)
@@ -694,7 +703,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* _
 // ([b][t][g][m & 1], 16 B) sit in two places: rows 0, 1 in the wave's static region, staged
 // while the weights are in flight, and rows 2, 3 in the wave's own weight slice, free once
 // the blocks are in registers.  The sub-block activation sums stay in registers (each lane
-// fetches its own from the staging lanes) and the cross-wave partial sums go through the
+// fetches its own from the staging lanes) and the block terms go through the
 // slices.  At K = 6144 eight waves of three blocks take 57,344 + 24,576 B, exactly half the
 // CU's LDS, so two workgroups share a CU as in the M = 1 kernel.
 constexpr int kSmallMaxRows = 4;
@@ -705,8 +714,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     constexpr int XP = GS * 32;              // 16-B pieces per activation row and wave
     constexpr int XI = (2 * XP + 63) / 64;   // pieces per lane for a pair of rows
     constexpr uint32_t kPair = GS * 1024u;   // operand entries of a pair of rows
-    constexpr uint32_t kRed = kPair;         // partial sums [n][row], after the entries in the slice
-    static_assert(kRed + kTR * kSmallMaxRows * 4 <= (uint32_t)Dma<GS>::kBytes, "slice holds a pair and the sums");
+    constexpr uint32_t kRed = kPair;         // block terms [n][column][block], after the entries in the slice
+    static_assert(kRed + kTR * kSmallMaxRows * GS * 4 <= (uint32_t)Dma<GS>::kBytes, "slice holds a pair and the block terms");
     static_assert(!Prob::kTwoTiles || MR == 2, "the second tile's copy reuses the slice rows 2, 3 would use");
     __shared__ __align__(16) uint8_t s_act[NW * kPair];
     extern __shared__ __align__(16) uint8_t s_w[];
@@ -800,11 +809,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     const uint32_t abase = lds_addr((md < 2 ? wA : wW) + 16u * (uint32_t)(g * 2 + (md & 1)));
     const uint64_t mask = ((1ull << rows) - 1) * 0x1000010000100001ull;   // diag_mask(rows)
     constexpr int NT = Prob::kTwoTiles ? 2 : 1;
-    float acc[NT][MR];
-#pragma unroll
-    for (int k = 0; k < NT; ++k)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[k][m] = 0.f;
+    float bt[NT][GS];   // block terms: lane 16i + n holds row n, activation row i
 #pragma unroll
     for (int tile = 0; tile < NT; ++tile) {
     if (tile > 0) {   // the second tile's weights (the compiler waits for the copies)
@@ -839,44 +844,42 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
 #pragma unroll
         for (int t = 0; t < 4; ++t) dhi = mfma(A[t], codes_hi(qd[2 * t], qd[2 * t + 1], ck), dhi);
         const Hdr H = hdr_decode(R[b].h, hs);
+        float t[MR];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const float t1 = __builtin_fmaf(H.sc1, dhi[m], H.sc0 * dlo[m]);
-            const float v = __builtin_fmaf(H.m1, hi[m], H.m0 * lo[m]);
-            acc[tile][m] = __builtin_fmaf(H.d, t1, acc[tile][m]);
-            acc[tile][m] = __builtin_fmaf(-H.dm, v, acc[tile][m]);
-        }
+        for (int m = 0; m < MR; ++m) t[m] = block_term(H, dlo[m], dhi[m], lo[m], hi[m]);
+        if constexpr (MR == 4) bt[tile][b] = block_sum4(t[0], t[1], t[2], t[3]);
+        else bt[tile][b] = block_sum2(t[0], t[1]);
     }
     }
 
-    // 4. reduce over the four K-groups, then across the K parts in wave order; a two-tile
-    // problem keeps its tiles' sums in columns 0..1 and 2..3 of the four per row
+    // 4. the wave's block terms into its slice ([row][column][block], column 2 * tile + m of
+    // the four per row), then each output in the fast-mode order over all K parts
+    {
+        const int i = lane >> 4;   // activation row (MR = 2: rows 0, 1 twice)
+        if (i < MR) {
+            float* te = (float*)(wW + kRed) + kSmallMaxRows * GS * n;
 #pragma unroll
-    for (int k = 0; k < NT; ++k)
+            for (int k = 0; k < NT; ++k)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            acc[k][m] += __shfl_xor(acc[k][m], 16, 64);
-            acc[k][m] += __shfl_xor(acc[k][m], 32, 64);
+                for (int b = 0; b < GS; ++b) te[(2 * k + i) * GS + b] = bt[k][b];
         }
-    if (lane < kTR) {
-        float* red = (float*)(wW + kRed) + kSmallMaxRows * lane;
-#pragma unroll
-        for (int k = 0; k < NT; ++k)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) red[2 * k + m] = acc[k][m];
     }
     __syncthreads();
-    for (int e = tid; e < kTR * kSmallMaxRows; e += (int)blockDim.x) {
-        const int rn = e >> 2, r = e & 3;
-        if (r < rows) {
-            float v = 0.f, v2 = 0.f;
-            for (int k = 0; k < KP; ++k) {
-                const float* red = (const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes + kRed) + rn * kSmallMaxRows;
-                v += red[r];
-                if constexpr (Prob::kTwoTiles) v2 += red[2 + r];
-            }
-            if constexpr (Prob::kTwoTiles) pb.store2(wg, rn, r, v, v2);
-            else pb.store(wg, rn, r, v);
+    // eight lanes per output (uniform trip count: every lane takes part in the cross-lane adds)
+    const int per = (int)(blockDim.x >> 3);
+    for (int o0 = 0; o0 < kTR * kSmallMaxRows; o0 += per) {
+        const int o = o0 + (tid >> 3), rn = (o >> 2) & (kTR - 1), r = o & 3;
+        const bool valid = o < kTR * kSmallMaxRows && r < rows;
+        auto term = [&](int c, int b) {
+            const int k = b / GS;   // the K part (wave) holding block b
+            return ((const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes + kRed))[(kSmallMaxRows * rn + c) * GS + (b - k * GS)];
+        };
+        const float v = canon_sum8(nsb, lane & 7, [&](int b) { return term(r, b); });
+        if constexpr (Prob::kTwoTiles) {
+            const float v2 = canon_sum8(nsb, lane & 7, [&](int b) { return term(2 + r, b); });
+            if (valid && (lane & 7) == 0) pb.store2(wg, rn, r, v, v2);
+        } else if (valid && (lane & 7) == 0) {
+            pb.store(wg, rn, r, v);
         }
     }
 }
@@ -1058,6 +1061,7 @@ hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x,
     const ProbPlain<MR> pb{W, N, row_bytes(T_Q4_K, K), y, yf, ystride, M};
     const unsigned nwg = (unsigned)((N + kTR - 1) / kTR);
     if constexpr (MR == 1) {
+        if (gemv_persist_supported(N, K)) return launch_gemv_persist(W, N, K, x, y, yf, st);
         Plan1 p1;
         if (make_plan1(nsb, 1, kMaxW, p1)) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
     } else {
@@ -1231,15 +1235,6 @@ struct ProbUGateUp {
         const uint8_t* base = e < 0 ? (part ? shU : shG) : (part ? U : G) + (int64_t)e * ebytes;
         return TileRef{base + (int64_t)it * kTR * rb, kTR, 0};
     }
-    __device__ void finish(int wg, const float* red, int KP, int tid) const {
-        if (tid >= kTR * MR) return;
-        const int n = tid / MR, r = tid % MR;
-        if (r >= M) return;
-        const int u = wg / (2 * itiles), part = (wg / itiles) & 1, it = wg % itiles;
-        float v = 0.f;
-        for (int k = 0; k < KP; ++k) v += red[(k * kTR + n) * MR + r];
-        gu[(((int64_t)u * 2 + part) * M + r) * I + (int64_t)it * kTR + n] = (uint16_t)bf16_rne(v);
-    }
     __device__ void store(int wg, int n, int r, float v) const {
         if (r >= M) return;
         const int u = wg / (2 * itiles), part = (wg / itiles) & 1, it = wg % itiles;
@@ -1269,16 +1264,6 @@ struct ProbUDown {
         const uint8_t* base = e < 0 ? shD : D + (int64_t)e * ebytes;
         const int64_t nv = H - (int64_t)it * kTR;
         return TileRef{base + (int64_t)it * kTR * rb, (int)(nv < kTR ? nv : kTR), 0};
-    }
-    __device__ void finish(int wg, const float* red, int KP, int tid) const {
-        if (tid >= kTR * MR) return;
-        const int n = tid / MR, r = tid % MR;
-        const int u = wg / htiles, it = wg % htiles;
-        const int64_t d = (int64_t)it * kTR + n;
-        if (r >= M || d >= H) return;
-        float v = 0.f;
-        for (int k = 0; k < KP; ++k) v += red[(k * kTR + n) * MR + r];
-        y[((int64_t)u * M + r) * H + d] = (uint16_t)bf16_rne(v);
     }
     __device__ void store(int wg, int n, int r, float v) const {
         const int u = wg / htiles, it = wg % htiles;
@@ -1320,7 +1305,7 @@ struct ProbUGateUpH {
 
 bool moe_union_supported(int64_t H, int64_t I, int M) {
     const int mr = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
-    return M >= 2 && M <= 8 && I % kTR == 0 && gemvm_supported((int)(H / QK_K), mr) &&
+    return M >= 1 && M <= 8 && I % kTR == 0 && gemvm_supported((int)(H / QK_K), mr) &&
            gemvm_supported((int)(I / QK_K), mr);
 }
 

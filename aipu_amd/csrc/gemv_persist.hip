@@ -1,0 +1,351 @@
+// Persistent single-row Q4_K GEMV (tolerance mode) for K <= 8192: the M = 1 hot path.
+//
+// Workgroup.  One workgroup per CU owns TT tiles of 8 rows (tiles wg, wg + G, ...), G =
+// #tiles / TT workgroups.  Wave NCW copies the tiles into LDS with direct-to-LDS buffer loads
+// (16 B per lane, 1 KB of consecutive row bytes per instruction) in rounds of 1 KB per row,
+// keeps Q rounds in flight and posts each round to an LDS counter as it lands.  The copy
+// schedule is unrolled at compile time, so every vmcnt wait is static and no wait drains the
+// whole pipeline.  Compute waves 0 .. NCW-1 own block pairs: wave w owns pairs w, w + NCW
+// (XPW of them), stages those pairs' activations itself and keeps their block-diagonal MFMA
+// operands in registers for the whole kernel; for every tile it computes its pairs (8 rows x
+// 2 blocks, one MFMA set) as soon as the round holding them has landed.  The last wave to
+// finish a tile reduces it and stores the 8 outputs; the copy wave reuses a tile buffer once
+// that tile is reduced (NB buffers).
+//
+// MFMA set (v_mfma_f32_16x16x32_bf16, lane 16g + n): column n = row n & 7 of the tile, block
+// 2p + (n >> 3) of the pair; K-group g = qs bytes 32g .. 32g+31 of the block (sub-blocks 2g,
+// 2g+1).  A rows 4g + h carry block 2p + h's activations on group g, so D[4g + h][n] is the
+// sub-block sum of column n for h = n >> 3.  Codes, seeds and epilogue are those of
+// mfma_gemv.hpp, and the reduction follows its fast-mode order: block terms (block_sum),
+// pair sums (a row shift by 8), then the balanced tree over the pairs with three cross-lane
+// adds -- bit-identical to the M = 2..8 kernels' canon_sum.
+#include "common.hpp"
+#include "launch.hpp"
+#include "mfma_gemv.hpp"
+
+namespace aipu {
+
+using namespace mg;
+
+namespace {
+
+constexpr int kPR = 8;            // rows per tile
+constexpr int kPMaxCW = 12;       // compute waves per workgroup
+constexpr int kPMaxTT = 8;        // tiles per workgroup
+constexpr int kPMaxNsb = 32;      // K <= 8192
+constexpr int kPMaxPairs = kPMaxNsb / 2;
+constexpr int kPStage = 1088;     // per pair: 1 KB of operand entries + 16 sub-block sums
+
+// Row pitch in LDS: the row bytes rounded so that consecutive rows start 32 B apart modulo
+// 256, which spreads the 8 rows' reads of one column over different banks.
+__host__ __device__ constexpr uint32_t tile_pitch(uint32_t rb) { return rb + ((32u - rb % 256u) + 256u) % 256u; }
+
+template <int N>
+struct IC {
+    static constexpr int value = N;
+};
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(IC<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// LDS counters.  A post is one ds_add from lane 0 (exec = 1); DS operations of a wave
+// execute in order, so a post issued after a wave's LDS writes makes them visible to a wave
+// that reads the counter first.  The polls wait inside the asm, so the compiler never
+// orders them behind direct-to-LDS copies still in flight.
+// Counter addresses are LDS byte addresses (uint32_t): a constant generic pointer cast to
+// LDS inside an asm operand makes the compiler emit an invalid null check.
+__device__ __forceinline__ void lds_post(uint32_t c) {
+    uint64_t saved;
+    asm volatile("s_mov_b64 %0, exec\n\ts_mov_b64 exec, 1\n\tds_add_u32 %1, %2\n\ts_mov_b64 exec, %0"
+                 : "=&s"(saved) : "v"(c), "v"(1u) : "memory");
+}
+__device__ __forceinline__ void lds_post(uint32_t* c) { lds_post(lds_addr(c)); }
+__device__ __forceinline__ uint32_t lds_add_rtn(uint32_t* c) {
+    uint64_t saved;
+    uint32_t old;
+    asm volatile(
+        "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 1\n\tds_add_rtn_u32 %0, %2, %3\n\ts_waitcnt lgkmcnt(0)\n\ts_mov_b64 exec, %1"
+        : "=&v"(old), "=&s"(saved) : "v"(lds_addr(c)), "v"(1u) : "memory");
+    return __builtin_amdgcn_readfirstlane(old);
+}
+__device__ __forceinline__ uint32_t lds_poll(const uint32_t* c) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(c)) : "memory");
+    return __builtin_amdgcn_readfirstlane(v);
+}
+// Bounded wait for a counter: every wave reaches the end of the kernel even if a post were
+// lost (the result would then be wrong, never a hang).
+__device__ __forceinline__ void spin_ge(const uint32_t* c, uint32_t v) {
+    for (uint32_t it = 0; lds_poll(c) < v && it < (1u << 22); ++it) __builtin_amdgcn_s_sleep(1);
+}
+
+// R rounds per tile (ceil(row bytes / 1 KB)), TT tiles per workgroup, XPW pairs per compute
+// wave.  nsb = K / 256 is a runtime value with ceil(144 * nsb / 1024) == R.
+template <int R, int TT, int XPW>
+__global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __restrict__ W, int64_t N, int nsb,
+                                                             const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+                                                             float* __restrict__ Yf, int ntiles) {
+    constexpr int NB = TT < 3 ? TT : 3;                        // tile buffers
+    constexpr int Q = 4 < (NB - 1) * R + 1 ? 4 : (NB - 1) * R + 1;   // rounds in flight (see the reuse wait)
+    static_assert(Q >= 1 && 8 * Q <= 63, "rounds in flight within vmcnt");
+    extern __shared__ __align__(16) uint8_t s_tile[];          // NB * 8 * pitch (direct-to-LDS targets only)
+    __shared__ __align__(16) uint8_t s_stage[kPMaxPairs * kPStage];
+    __shared__ __align__(16) float s_red[NB * kPR * kPMaxPairs];
+    __shared__ uint32_t s_cnt[TT * R];                          // rounds landed
+    __shared__ uint32_t s_done[TT];                             // pairs finished per tile
+    __shared__ uint32_t s_freed[TT];                            // tile reduced, buffers free
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int NCW = (int)(blockDim.x >> 6) - 1;
+    const int wg = blockIdx.x, G = gridDim.x;
+    const int T = (ntiles - wg + G - 1) / G;                    // tiles of this workgroup
+    const int np = (nsb + 1) >> 1;
+    const uint32_t rb = (uint32_t)nsb * 144u;
+    const uint32_t P = tile_pitch(rb);
+    const uint32_t TB = kPR * P;
+    for (int i = tid; i < TT * R; i += blockDim.x) s_cnt[i] = 0u;
+    if (tid < TT) {
+        s_done[tid] = 0u;
+        s_freed[tid] = 0u;
+    }
+
+    // activation loads of the wave's own pairs go out before any weight copy
+    uint4 xv[XPW];
+    if (w < NCW) {
+        const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)nsb * 512u);   // an odd nsb's last pair reads zeros
+#pragma unroll
+        for (int i = 0; i < XPW; ++i) {
+            const int p = w + NCW * i;
+            xv[i] = buf_load16(xr, p < np ? (uint32_t)p * 1024u + 16u * (uint32_t)lane : kOOB);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
+
+    if (w == NCW) {
+        // ---- copy wave: round u = t * R + k, posted in order once landed
+        const uint32_t last = rb - 1024u * (R - 1);             // bytes per row in the last round
+        uint32_t cnt0 = lds_addr(s_cnt);
+        asm volatile("" : "+v"(cnt0));                           // a runtime base (see lds_post)
+        constexpr int U = TT * R;
+        static_for<0, U + Q - 1>([&](auto sI) {
+            constexpr int step = decltype(sI)::value;
+            if constexpr (step < U) {
+                constexpr int t = step / R, k = step - t * R;
+                // A buffer is reused once its previous tile is reduced.  That tile's last
+                // round is posted by now: Q <= (NB - 1) * R + 1 keeps it at least Q rounds back.
+                if constexpr (k == 0 && t >= NB) spin_ge(&s_freed[t - NB], 1u);
+                const int64_t r0 = (int64_t)(wg + t * G) * kPR;
+                const int nvalid = t < T ? (int)(N - r0 < kPR ? N - r0 : kPR) : 0;
+                const __amdgpu_buffer_rsrc_t wr =
+                    buf_rsrc(W + (nvalid > 0 ? r0 * (int64_t)rb : 0), (uint32_t)(nvalid > 0 ? nvalid : 0) * rb);
+                uint8_t* tb = s_tile + (uint32_t)(t % NB) * TB;
+#pragma unroll
+                for (int rr = 0; rr < kPR; ++rr)
+                    if (k < R - 1 || 16u * (uint32_t)lane < last)
+                        lds_dma16<kNT>(wr, tb + (uint32_t)rr * P + 1024u * k, (uint32_t)rr * rb + 1024u * k + 16u * (uint32_t)lane);
+            }
+            constexpr int pu = step - (Q - 1);
+            if constexpr (pu >= 0) {
+                constexpr int after = (U - 1 < step ? U - 1 : step) - pu;   // rounds issued after pu
+                __builtin_amdgcn_s_waitcnt(wait_vm(kPR * after));
+                lds_post(cnt0 + 4u * (uint32_t)pu);
+            }
+        });
+        return;
+    }
+
+    // ---- compute waves: stage the own pairs, keep their operands in registers
+    const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
+    u32x4_t A[XPW][8];
+    float2 as[XPW];
+#pragma unroll
+    for (int i = 0; i < XPW; ++i) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) A[i][t] = u32x4_t{0u, 0u, 0u, 0u};
+        as[i] = float2{0.f, 0.f};
+        const int p = w + NCW * i;
+        if (p >= np) continue;
+        // piece q = lane: 8 activations of block 2p + (q >> 5), K-group (q >> 3) & 3, MFMA q & 7
+        uint8_t* st = s_stage + (uint32_t)p * kPStage;
+        float* sS = (float*)(st + 1024u);
+        const uint32_t ones = 0x3F803F80u;
+        float sm = 0.f;
+        sm = dot2(xv[i].x, ones, sm);
+        sm = dot2(xv[i].y, ones, sm);
+        sm = dot2(xv[i].z, ones, sm);
+        sm = dot2(xv[i].w, ones, sm);
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+        const int hh = lane >> 5, gg = (lane >> 3) & 3, tt = lane & 7;
+        *(u32x4_t*)(st + 16u * (uint32_t)((tt * 4 + gg) * 2 + hh)) = act_perm(xv[i]);
+        if ((lane & 3) == 0) sS[(gg * 2 + hh) * 2 + ((lane >> 2) & 1)] = sm;
+        // the operands (diagonal lanes 16g + 4g + h, h < 2) and this lane's sums
+        const uint32_t aa = lds_addr(st) + 32u * (uint32_t)g + 16u * (uint32_t)((n - 4 * g) & 1);
+        uint64_t saved;
+        asm volatile(
+            "s_waitcnt lgkmcnt(0)\n\t"
+            "s_mov_b64 %[sv], exec\n\t"
+            "s_and_b64 exec, exec, %[mask]\n\t"
+            "ds_read_b128 %[a0], %[aa]\n\t"
+            "ds_read_b128 %[a1], %[aa] offset:128\n\t"
+            "ds_read_b128 %[a2], %[aa] offset:256\n\t"
+            "ds_read_b128 %[a3], %[aa] offset:384\n\t"
+            "ds_read_b128 %[a4], %[aa] offset:512\n\t"
+            "ds_read_b128 %[a5], %[aa] offset:640\n\t"
+            "ds_read_b128 %[a6], %[aa] offset:768\n\t"
+            "ds_read_b128 %[a7], %[aa] offset:896\n\t"
+            "s_mov_b64 exec, %[sv]\n\t"
+            "ds_read_b64 %[as], %[sa]\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : [a0] "+v"(A[i][0]), [a1] "+v"(A[i][1]), [a2] "+v"(A[i][2]), [a3] "+v"(A[i][3]), [a4] "+v"(A[i][4]),
+              [a5] "+v"(A[i][5]), [a6] "+v"(A[i][6]), [a7] "+v"(A[i][7]), [as] "=&v"(as[i]), [sv] "=&s"(saved)
+            : [aa] "v"(aa), [mask] "s"(diag_mask(2)), [sa] "v"(lds_addr(st) + 1024u + 8u * (uint32_t)(g * 2 + h))
+            : "memory", "scc");   // s_and_b64 writes SCC
+    }
+    const HdrSel hs = hdr_sel(g);
+    const CodeK ck = code_k();
+    int seen = -1;   // highest round known to have landed
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int i = 0; i < XPW; ++i) {
+            const int p = w + NCW * i;
+            if (p >= np) break;
+            const uint32_t pend = 288u * (uint32_t)p + 287u < rb ? 288u * (uint32_t)p + 287u : rb - 1u;
+            const int u = t * R + (int)(pend / 1024u);         // the round holding the pair's last byte
+            const uint32_t blk = 2u * (uint32_t)p + (uint32_t)h;
+            const uint32_t wrow = lds_addr(s_tile) + (uint32_t)(t % NB) * TB + (uint32_t)r * P + 144u * blk;
+            // the round counter and the operands in one LDS batch: a posted counter proves that
+            // the operands read after it (in DS order) had landed; otherwise wait and read again
+            u32x4_t hv, q0, q1;
+            uint32_t cv;
+            asm volatile(
+                "ds_read_b32 %3, %6\n\t"
+                "ds_read_b128 %0, %4\n\t"
+                "ds_read_b128 %1, %5\n\t"
+                "ds_read_b128 %2, %5 offset:16\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(hv), "=&v"(q0), "=&v"(q1), "=&v"(cv)
+                : "v"(wrow), "v"(wrow + 16u + 32u * (uint32_t)g), "v"(lds_addr(&s_cnt[u]))
+                : "memory");
+            if (seen < u && __builtin_amdgcn_readfirstlane(cv) < 1u) {
+                spin_ge(&s_cnt[u], 1u);
+                asm volatile(
+                    "ds_read_b128 %0, %3\n\t"
+                    "ds_read_b128 %1, %4\n\t"
+                    "ds_read_b128 %2, %4 offset:16\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(hv), "=&v"(q0), "=&v"(q1)
+                    : "v"(wrow), "v"(wrow + 16u + 32u * (uint32_t)g)
+                    : "memory");
+            }
+            seen = seen < u ? u : seen;
+            f32x4_t dlo, dhi;
+            dlo[0] = dlo[1] = -kCodeBiasF * as[i].x;
+            dhi[0] = dhi[1] = -kCodeBiasF * as[i].y;
+            dlo[2] = dlo[3] = dhi[2] = dhi[3] = 0.f;
+            const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                dlo = mfma(A[i][tt], codes_lo(qd[2 * tt], qd[2 * tt + 1], ck), dlo);
+                dhi = mfma(A[i][4 + tt], codes_hi(qd[2 * tt], qd[2 * tt + 1], ck), dhi);
+            }
+            const Hdr H = hdr_decode(make_uint4(hv.x, hv.y, hv.z, hv.w), hs);
+            const float bt = block_sum(block_term(H, h ? dlo[1] : dlo[0], h ? dhi[1] : dhi[0], as[i].x, as[i].y));
+            // pair sum on lanes 0..7 (row r): block 2p, then block 2p+1 from lane r + 8
+            const float b1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bt), 0x108, 0xF, 0xF, false));
+            const float ps = bt + (2 * p + 1 < nsb ? b1 : 0.0f);
+            float* rt = s_red + (t % NB) * (kPR * kPMaxPairs);
+            if (lane < kPR) rt[lane * kPMaxPairs + p] = ps;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lds_add_rtn(&s_done[t]) == (uint32_t)np - 1u) {
+                // last pair of tile t: v_k on lane 8 * row + k, then the tree (xor 1, xor 2, mirror)
+                const int rr = lane >> 3, k = lane & 7;
+                float v = k < np ? rt[rr * kPMaxPairs + k] : 0.0f;
+                for (int j = k + 8; j < np; j += 8) v += rt[rr * kPMaxPairs + j];
+                v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+                v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+                v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+                const int64_t row = (int64_t)(wg + t * G) * kPR + rr;
+                if (k == 0 && row < N) {
+                    Y[row] = (uint16_t)bf16_rne(v);
+                    if (Yf) Yf[row] = v;
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads of rt done before the buffer is reused
+                lds_post(&s_freed[t]);
+            }
+        }
+    }
+}
+
+int cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
+template <int R, int XPW>
+hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16_t* y, float* yf, int TT, int G,
+                 int ntiles, int ncw, size_t lds, hipStream_t st) {
+    const dim3 grid(G), block(64 * (ncw + 1));
+    switch (TT) {
+#define AIPU_P(TV) \
+    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, XPW>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles); break;
+        AIPU_P(1)
+        AIPU_P(2)
+        AIPU_P(3)
+        AIPU_P(4)
+        AIPU_P(5)
+        AIPU_P(6)
+        AIPU_P(7)
+        AIPU_P(8)
+#undef AIPU_P
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemv_persist_supported(int64_t N, int64_t K) {
+    return N >= 1 && K >= QK_K && K % QK_K == 0 && K / QK_K <= kPMaxNsb && N <= ((int64_t)1 << 31);
+}
+
+// y[0 .. N) = x . W^T for one activation row (Q4_K, K <= 8192).
+hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
+                               hipStream_t st) {
+    if (!gemv_persist_supported(N, K)) return hipErrorInvalidValue;
+    const int nsb = (int)(K / QK_K);
+    const int ntiles = (int)((N + kPR - 1) / kPR);
+    const int cus = cu_count();
+    int TT = (ntiles + cus - 1) / cus;
+    TT = TT > kPMaxTT ? kPMaxTT : TT;
+    const int G = (ntiles + TT - 1) / TT;
+    const int R = (144 * nsb + 1023) / 1024;
+    const int np = (nsb + 1) / 2;
+    const int xpw = np > kPMaxCW ? 2 : 1;
+    const int ncw = (np + xpw - 1) / xpw;
+    const int nb = TT < 3 ? TT : 3;
+    const size_t lds = (size_t)nb * kPR * tile_pitch((uint32_t)nsb * 144u);
+    switch (R * 4 + xpw) {
+        case 1 * 4 + 1: return run_p<1, 1>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+        case 2 * 4 + 1: return run_p<2, 1>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+        case 3 * 4 + 1: return run_p<3, 1>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+        case 4 * 4 + 1: return run_p<4, 1>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+        case 4 * 4 + 2: return run_p<4, 2>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+        case 5 * 4 + 2: return run_p<5, 2>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace aipu

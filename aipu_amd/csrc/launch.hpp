@@ -54,6 +54,11 @@ bool gemv_mixed_supported(int type, int64_t K);
 hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K, const uint16_t* x, uint16_t* y,
                              float* y_f32, hipStream_t st);
 
+// gemv_persist.hip -- persistent single-row Q4_K GEMV (tolerance mode, K <= 8192)
+bool gemv_persist_supported(int64_t N, int64_t K);
+hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
+                               hipStream_t st);
+
 // gemv_mfma.hip -- matrix-core Q4_K GEMV (tolerance mode)
 bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M);
 hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,

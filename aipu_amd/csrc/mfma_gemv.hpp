@@ -277,5 +277,82 @@ struct ActLayout {
     static constexpr int kZeroBytes = kEntriesPerBlock * 16;
 };
 
+// ------------------------------------------------------------- fast-mode reduction order
+// Every plain Q4_K GEMV kernel of the tolerance mode (M = 1 and the M = 2..8 batches) forms
+// an output the same way, so a row of a batch equals the single-row result bit for bit:
+//   1. per block b and K-group g (lane 16g + n): S_lo, S_hi from the MFMA chain (seeded with
+//      -128 * the sub-block activation sums), then
+//         term_g = fma(-dmin, fma(m1, A_hi, m0 * A_lo), d * fma(sc1, S_hi, sc0 * S_lo));
+//   2. block term B_b = (term_0 + term_1) + (term_2 + term_3)       (block_sum)
+//   3. pair sums s_p = B_2p + B_2p+1 (B_nsb = 0 for odd nsb);
+//   4. v_k = s_k + s_k+8 + s_k+16 + ... (left to right; v_k = 0 for k >= #pairs), k < 8;
+//   5. y = ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)).
+// Steps 3-5 are a balanced tree over the pairs that a wave-per-pair kernel evaluates with
+// three cross-lane adds and a kernel holding all block terms evaluates with canon_sum.
+
+__device__ __forceinline__ float block_term(const Hdr& H, float slo, float shi, float alo, float ahi) {
+    const float t1 = __builtin_fmaf(H.sc1, shi, H.sc0 * slo);
+    const float v = __builtin_fmaf(H.m1, ahi, H.m0 * alo);
+    return __builtin_fmaf(-H.dm, v, H.d * t1);
+}
+
+// Sum over the four K-groups (lanes n, n + 16, n + 32, n + 48), in every lane.
+__device__ __forceinline__ float block_sum(float a) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    const float s = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// block_sum of four values at once, transposed: lane 16i + n returns a_i's sum over the lanes
+// n, n + 16, n + 32, n + 48.  permlane16_swap(X, Y) swaps X's odd 16-lane rows with Y's even
+// rows, so X + Y holds (g0 + g1) of X, Y, X, Y in rows 0..3 ... of (X, Y) = (a0, a1), and
+// (g2 + g3) in rows 2, 3; permlane32_swap then pairs each (g0 + g1) with its (g2 + g3).  The
+// additions are those of block_sum, so the bits are too.
+__device__ __forceinline__ float block_sum4(float a0, float a1, float a2, float a3) {
+    const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(a0), __float_as_uint(a1), false, false);
+    const auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(a2), __float_as_uint(a3), false, false);
+    const float s01 = __uint_as_float(x[0]) + __uint_as_float(x[1]);   // rows: a0 g01, a1 g01, a0 g23, a1 g23
+    const float s23 = __uint_as_float(y[0]) + __uint_as_float(y[1]);   // rows: a2 g01, a3 g01, a2 g23, a3 g23
+    const auto z = __builtin_amdgcn_permlane32_swap(__float_as_uint(s01), __float_as_uint(s23), false, false);
+    return __uint_as_float(z[0]) + __uint_as_float(z[1]);               // rows: a0, a1, a2, a3
+}
+// Two values: lane 16i + n returns a_(i & 1)'s sum.
+__device__ __forceinline__ float block_sum2(float a0, float a1) {
+    const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(a0), __float_as_uint(a1), false, false);
+    const float s = __uint_as_float(x[0]) + __uint_as_float(x[1]);     // rows: a0 g01, a1 g01, a0 g23, a1 g23
+    const auto z = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(z[0]) + __uint_as_float(z[1]);               // rows: a0, a1, a0, a1
+}
+
+// Steps 3-5 over block terms bt(b), b < nsb.
+template <class F>
+__device__ __forceinline__ float canon_sum(int nsb, F&& bt) {
+    const int np = (nsb + 1) >> 1;
+    auto pair = [&](int p) { return bt(2 * p) + (2 * p + 1 < nsb ? bt(2 * p + 1) : 0.0f); };
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        v[k] = k < np ? pair(k) : 0.0f;
+        for (int i = k + 8; i < np; i += 8) v[k] += pair(i);
+    }
+    return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+}
+
+// The same sum on eight lanes (k = lane & 7 of an aligned group of eight, all lanes active):
+// lane k forms v_k, then xor 1, xor 2 and the half-row mirror add the tree; every lane of the
+// group ends with y.  Bit-identical to canon_sum (IEEE addition commutes).
+template <class F>
+__device__ __forceinline__ float canon_sum8(int nsb, int k, F&& bt) {
+    const int np = (nsb + 1) >> 1;
+    auto pair = [&](int p) { return bt(2 * p) + (2 * p + 1 < nsb ? bt(2 * p + 1) : 0.0f); };
+    float v = k < np ? pair(k) : 0.0f;
+    for (int i = k + 8; i < np; i += 8) v += pair(i);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));    // xor 1
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));    // xor 2
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));   // half-row mirror
+    return v;
+}
+
 }  // namespace mg
 }  // namespace aipu

@@ -227,7 +227,9 @@ hipError_t launch_moe_decode_batched(const MoeArgs& a, int64_t M, hipStream_t st
     int64_t r0 = 0;
     while (r0 < M) {
         const int rows = (int)(M - r0 < per ? M - r0 : per);
-        if (fast && rows >= 2 && moe_union_supported(a.H, a.I, rows)) {
+        // a leftover single row of the batch takes a one-row union pass too: the same kernels
+        // and summation order as the batch's other rows (the single-row step's legs differ)
+        if (fast && moe_union_supported(a.H, a.I, rows)) {
             AIPU_TRY(fast_pass(a, r0, rows, L, st));
         } else {
             // one row at a time with its experts reordered by index (still the M > 1 order)

@@ -441,7 +441,7 @@ def cpu_baseline(budget_s=12.0):
 
 
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_gemv_q4k_6144.json")
-HEADLINE_KERNEL = "k_gemv1"
+HEADLINE_KERNEL = "k_gemv1p"
 COPY_BYTES = 256 << 20
 
 
