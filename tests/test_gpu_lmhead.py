@@ -148,3 +148,21 @@ def test_lm_head_abi_rejects():
     x = torch.zeros(12, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(_lib.AipuError):
         dev.lm_head(w, x)          # K = 12 is not a multiple of 8
+
+
+def test_lm_head_detects_corrupted_row():
+    """Must-fail twin: one bf16 weight of row 17 raised to 8.0 against an activation of 8.0
+    changes that logit and makes row 17 the argmax, so both bit-exact checks fail."""
+    note("lm_head corruption twin")
+    rng = np.random.default_rng(901)
+    V, K = 300, 1024
+    w = qo.random_bf16(rng, (V, K), scale=0.02)
+    x = qo.random_bf16(rng, K)
+    x[10] = qo.bf16_round_bits(np.float32(8.0))
+    bad = w.copy()
+    bad[17, 10] = qo.bf16_round_bits(np.float32(8.0))
+    got, am = _run(bad, x)
+    exp, eam = co.lm_head(w, x)
+    assert not np.array_equal(got, exp), "logits of a corrupted head equal the oracle's"
+    assert am == 17 and eam != 17, (am, eam)
+    _check(w, x, "clean twin")

@@ -131,6 +131,38 @@ def test_moe_fast_small(router_type, shared, topk):
     _check_moe_output(h_bits(y), x, ex, sh, es, ew, H, I)
 
 
+
+@pytest.mark.parametrize("mode", ["ref", "fast"])
+def test_moe_detects_corrupted_expert(mode):
+    """Must-fail twin: the d of every block in row 0 of the first selected expert's down
+    matrix raised to 4.0 moves y[0] past the check (bit-exact in ref mode, the MoE tolerance in
+    fast mode); the clean step passes the same check."""
+    E, H, I, topk = 16, 512, 256, 4
+    note(f"moe corruption twin {mode}")
+    rng = np.random.default_rng(4040)
+    rw, ex, sh, x = _moe_case(rng, E, H, I, BF16, False)
+    r = go.moe_decode_ref(x, BF16, rw, ex, Q4K, E, H, I, topk)
+    e0 = int(r["sel_idx"][0])
+    bad_down = ex[2].copy().reshape(E, H, I // 256, 144)
+    bad_down[e0, 0, :, 0:2] = np.asarray(qo.f32_to_f16_bits(np.array([4.0], np.float32)), np.uint16).view(np.uint8)
+    bad = (ex[0], ex[1], bad_down.reshape(-1))
+    for weights, expect_pass in ((bad, False), (ex, True)):
+        y, sel, sw = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, *(d_u8(a) for a in weights), E, H, I, topk,
+                                           d_bf16(x), mode=mode)
+        yb = h_bits(y)
+        if mode == "ref":
+            passed = np.array_equal(yb, r["y"])
+        else:
+            # the fast step routes from the fast router logits (exactly the reference tail)
+            lf = h_bits(dev.gemv(BF16, d_u8(rw), E, H, d_bf16(x[None]), mode="fast"))[0]
+            es, ew, _ = go.router_tail(lf, topk)
+            try:
+                _check_moe_output(yb, x, ex, None, es, ew, H, I)
+                passed = True
+            except AssertionError:
+                passed = False
+        assert passed == expect_pass, f"{mode}: check {'passed' if passed else 'failed'} on {'clean' if expect_pass else 'corrupted'} weights"
+
 def _check_moe_output(y_bits, x, ex, sh, sel, selw, H, I):
     """y within 2^-7 of sum_s g_s sum_k |h_k w_dk| (+2 bf16 ulp) of the reference-order
     combine of the same routing decision."""
@@ -282,6 +314,27 @@ def test_mixed_tiles_ragged_fast():
     assert np.all(got_f[~covered] == np.float32(-3.0))
     assert np.all(got_y[~covered] == qo.bf16_round_bits(np.float32(7.0)))
 
+
+
+def test_mixed_tiles_detect_corruption():
+    """Must-fail twin for the tile path: one Q6_K weight of tile 1 changed (its qh bits) moves
+    that output past the gate; the clean tiles pass it."""
+    note("tiles corruption twin")
+    rng = np.random.default_rng(36)
+    K, rows = 1024, 64
+    types = [Q4K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16]
+    raws = [qo.random_weights(rng, t, rows, K) for t in types]
+    N = rows * len(types)
+    x = qo.random_bf16(rng, (1, K))
+    w = np.concatenate([qo.dequant_matrix(t, r, rows, K) for t, r in zip(types, raws)])
+    bad1 = raws[1].copy()
+    rb = bad1.size // rows
+    bad1[3 * rb + 128 + 5] ^= 0x30
+    for rs, expect in ((raws[:1] + [bad1] + raws[2:], False), (raws, True)):
+        tiles = [(t, d_u8(r), i * rows, rows) for i, (t, r) in enumerate(zip(types, rs))]
+        _, yf = dev.gemv_tiles(tiles, N, K, d_bf16(x), mode="fast", out_f32=True)
+        ok, _ = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
+        assert ok == expect, "tile check on " + ("clean" if expect else "corrupted") + " weights"
 
 # --------------------------------------------------- reference-interface mirrors
 def test_q4k_ref_mirror_selftest():

@@ -134,3 +134,26 @@ def test_prefill_config4_shape_sampled():
     yfs = h_f32(yf)[:, cols]
     worst = _check(raw, len(cols), K, xb, ys, yfs, "config-4 sampled")
     note(f"config-4 worst tolerance ratio {worst:.3g}")
+
+
+def test_prefill_detects_corrupted_weights():
+    """Must-fail twin: one nibble of row 5 changed from 0 to 15 (under a large scale, against an
+    activation of 4 in every row) moves column 5 of every output row past the tolerance gate."""
+    note("prefill corruption twin")
+    rng = np.random.default_rng(501)
+    M, N, K = 64, 96, 768
+    raw = qo.random_q4k_blocks(rng, N * K // 256)
+    off = 5 * 144 * (K // 256)                      # row 5, block 0
+    raw[off + 4:off + 16] = qo.pack_scales_q4k([32] * 8, [1] * 8)
+    raw[off + 16 + 3] &= 0xF0                       # weight 3 has code 0 ...
+    x = qo.random_bf16(rng, (M, K))
+    x[:, 3] = qo.bf16_round_bits(np.float32(4.0))
+    wdeq = qo.dequant_q4k(raw).reshape(N, K)
+    bad = raw.copy()
+    bad[off + 16 + 3] |= 0x0F                       # ... and 15 in the corrupted copy
+    y, yf = _prefill(bad, N, K, x)
+    ok, _ = qo.tolerance_gate(wdeq, qo.bf16_bits_to_f32(x), yf)
+    assert not ok, "the tolerance gate passed a corrupted weight"
+    # the clean weights pass the same gate (the twin's other half)
+    y, yf = _prefill(raw, N, K, x)
+    assert qo.tolerance_gate(wdeq, qo.bf16_bits_to_f32(x), yf)[0]
