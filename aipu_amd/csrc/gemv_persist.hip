@@ -22,10 +22,12 @@
 #include "common.hpp"
 #include "launch.hpp"
 #include "mfma_gemv.hpp"
+#include "persist.hpp"
 
 namespace aipu {
 
 using namespace mg;
+using namespace pst;
 
 namespace {
 
@@ -35,53 +37,6 @@ constexpr int kPMaxTT = 8;        // tiles per workgroup
 constexpr int kPMaxNsb = 32;      // K <= 8192
 constexpr int kPMaxPairs = kPMaxNsb / 2;
 constexpr int kPStage = 1088;     // per pair: 1 KB of operand entries + 16 sub-block sums
-
-// Row pitch in LDS: the row bytes rounded so that consecutive rows start 32 B apart modulo
-// 256, which spreads the 8 rows' reads of one column over different banks.
-__host__ __device__ constexpr uint32_t tile_pitch(uint32_t rb) { return rb + ((32u - rb % 256u) + 256u) % 256u; }
-
-template <int N>
-struct IC {
-    static constexpr int value = N;
-};
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (B < E) {
-        f(IC<B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
-// LDS counters.  A post is one ds_add from lane 0 (exec = 1); DS operations of a wave
-// execute in order, so a post issued after a wave's LDS writes makes them visible to a wave
-// that reads the counter first.  The polls wait inside the asm, so the compiler never
-// orders them behind direct-to-LDS copies still in flight.
-// Counter addresses are LDS byte addresses (uint32_t): a constant generic pointer cast to
-// LDS inside an asm operand makes the compiler emit an invalid null check.
-__device__ __forceinline__ void lds_post(uint32_t c) {
-    uint64_t saved;
-    asm volatile("s_mov_b64 %0, exec\n\ts_mov_b64 exec, 1\n\tds_add_u32 %1, %2\n\ts_mov_b64 exec, %0"
-                 : "=&s"(saved) : "v"(c), "v"(1u) : "memory");
-}
-__device__ __forceinline__ void lds_post(uint32_t* c) { lds_post(lds_addr(c)); }
-__device__ __forceinline__ uint32_t lds_add_rtn(uint32_t* c) {
-    uint64_t saved;
-    uint32_t old;
-    asm volatile(
-        "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 1\n\tds_add_rtn_u32 %0, %2, %3\n\ts_waitcnt lgkmcnt(0)\n\ts_mov_b64 exec, %1"
-        : "=&v"(old), "=&s"(saved) : "v"(lds_addr(c)), "v"(1u) : "memory");
-    return __builtin_amdgcn_readfirstlane(old);
-}
-__device__ __forceinline__ uint32_t lds_poll(const uint32_t* c) {
-    uint32_t v;
-    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(c)) : "memory");
-    return __builtin_amdgcn_readfirstlane(v);
-}
-// Bounded wait for a counter: every wave reaches the end of the kernel even if a post were
-// lost (the result would then be wrong, never a hang).
-__device__ __forceinline__ void spin_ge(const uint32_t* c, uint32_t v) {
-    for (uint32_t it = 0; lds_poll(c) < v && it < (1u << 22); ++it) __builtin_amdgcn_s_sleep(1);
-}
 
 // R rounds per tile (ceil(row bytes / 1 KB)), TT tiles per workgroup, XPW pairs per compute
 // wave.  nsb = K / 256 is a runtime value with ceil(144 * nsb / 1024) == R.
