@@ -77,14 +77,6 @@ struct MoeRoute {
     uint16_t* selw_api;
 };
 bool moe_route_in_kernel(int64_t E, int topk, int64_t H);
-// moe_persist.hip -- persistent MoE legs at the config-2 shape class
-bool moe_persist_supported(int nslots, int topk, int64_t E, int64_t H, int64_t I);
-hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
-                                     const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
-                                     const uint16_t* x, uint16_t* h, hipStream_t st);
-hipError_t launch_moe_down_persist(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
-                                   int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h,
-                                   uint16_t* y, const uint16_t* resid, hipStream_t st);
 hipError_t launch_moe_gateup_mfma(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
                                   const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
                                   const uint16_t* x, uint16_t* h, hipStream_t st);

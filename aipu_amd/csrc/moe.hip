@@ -125,15 +125,7 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
         AIPU_TRY(launch_gemv_ref(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
 
     // 2-3. fast path: the gate/up kernel routes from the logits in every workgroup and
-    // publishes the decision for the down kernel (no separate router-tail launch); the
-    // persistent legs at the config-2 shape class, the per-tile legs elsewhere
-    if (fast && !a.ascending && moe_persist_supported(nslots, a.topk, a.E, a.H, a.I)) {
-        const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};
-        AIPU_TRY(launch_moe_gateup_persist(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E,
-                                           a.H, a.I, a.x, h, st));
-        return launch_moe_down_persist(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y,
-                                       a.resid, st);
-    }
+    // publishes the decision for the down kernel (no separate router-tail launch)
     if (fast && !a.ascending && moe_mfma_supported(nslots, a.H, a.I) && moe_route_in_kernel(a.E, a.topk, a.H)) {
         const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};
         AIPU_TRY(launch_moe_gateup_mfma(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
