@@ -1092,6 +1092,13 @@ hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t*
     const bool small = make_plans(nsb, ps);
     for (int64_t m0 = 0; m0 < M;) {
         const int left = (int)(M - m0 < 8 ? M - m0 : 8);
+        if (left >= 2 && gemv_persist_m_supported(N, K, left)) {   // two to eight rows, one persistent pass
+            const hipError_t e = launch_gemv_persist_m(W, N, K, x + m0 * K, left, y + m0 * ystride,
+                                                       y_f32 ? y_f32 + m0 * ystride : nullptr, ystride, st);
+            if (e != hipSuccess) return e;
+            m0 += left;
+            continue;
+        }
         if (left >= 5 && gemvm_supported(nsb, 8)) {   // five to eight rows in one pass
             const ProbPlain<8> pb{W, N, row_bytes(T_Q4_K, K), y + m0 * ystride, y_f32 ? y_f32 + m0 * ystride : nullptr,
                                   ystride, left};

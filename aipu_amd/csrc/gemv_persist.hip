@@ -125,20 +125,8 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
         as[i] = float2{0.f, 0.f};
         const int p = w + NCW * i;
         if (p >= np) continue;
-        // piece q = lane: 8 activations of block 2p + (q >> 5), K-group (q >> 3) & 3, MFMA q & 7
         uint8_t* st = s_stage + (uint32_t)p * kPStage;
-        float* sS = (float*)(st + 1024u);
-        const uint32_t ones = 0x3F803F80u;
-        float sm = 0.f;
-        sm = dot2(xv[i].x, ones, sm);
-        sm = dot2(xv[i].y, ones, sm);
-        sm = dot2(xv[i].z, ones, sm);
-        sm = dot2(xv[i].w, ones, sm);
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
-        const int hh = lane >> 5, gg = (lane >> 3) & 3, tt = lane & 7;
-        *(u32x4_t*)(st + 16u * (uint32_t)((tt * 4 + gg) * 2 + hh)) = act_perm(xv[i]);
-        if ((lane & 3) == 0) sS[(gg * 2 + hh) * 2 + ((lane >> 2) & 1)] = sm;
+        stage_pair(xv[i], st, lane);
         // the operands (diagonal lanes 16g + 4g + h, h < 2) and this lane's sums
         const uint32_t aa = lds_addr(st) + 32u * (uint32_t)g + 16u * (uint32_t)((n - 4 * g) & 1);
         uint64_t saved;

@@ -27,6 +27,34 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
+// Staging of one block pair's activations (512 bf16, 1 KB) for the block-diagonal MFMA
+// operand: entry e = 8t + 2g + h (16 B) holds activations 8t' .. 8t'+7 of sub-block 2g + (t >> 2)
+// of block h, t' = t & 3 -- the operand of MFMA t on K-group g -- followed by the 16 sub-block
+// sums (float, index 2(2g + h) + (t >> 2)).  xv is lane L's contiguous 16-B chunk of the pair
+// (chunk L = 32h + 8g + t); a lane permute hands lane e the chunk of entry e, so the entry
+// writes are linear in the lane and free of bank conflicts while the loads stay contiguous.
+// Each sub-block sum is ((c0 + c1) + (c2 + c3)) over its four chunks' sums c_t' (lanes
+// 2g + h + 8t), the order every fast-mode kernel uses.
+__device__ __forceinline__ void stage_pair(const uint4& xl, uint8_t* st, int L) {
+    const int src = 4 * (32 * (L & 1) + 8 * ((L >> 1) & 3) + (L >> 3));   // byte index of the chunk's lane
+    uint4 xv;
+    xv.x = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xl.x);
+    xv.y = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xl.y);
+    xv.z = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xl.z);
+    xv.w = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xl.w);
+    const uint32_t ones = 0x3F803F80u;
+    float c = 0.f;
+    c = mg::dot2(xv.x, ones, c);
+    c = mg::dot2(xv.y, ones, c);
+    c = mg::dot2(xv.z, ones, c);
+    c = mg::dot2(xv.w, ones, c);
+    const float c2 = c + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x108, 0xF, 0xF, false));   // + lane L + 8
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(c2), __float_as_uint(c2), false, false);
+    const float c4 = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);                                              // + lane L +- 16
+    *(u32x4_t*)(st + 16u * (uint32_t)L) = mg::act_perm(xv);
+    if ((L & 16) == 0 && (L & 8) == 0) ((float*)(st + 1024u))[2 * (L & 7) + (L >> 5)] = c4;
+}
+
 // LDS counters.  A post is one ds_add from lane 0 (exec = 1); DS operations of a wave
 // execute in order, so a post issued after a wave's LDS writes makes them visible to a wave
 // that reads the counter first.  The polls wait inside the asm, so the compiler never

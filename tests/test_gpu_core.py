@@ -196,7 +196,10 @@ def test_gemv_fast_tolerance(N, K, M):
 # batch are served by the matrix-core kernels, i.e. K <= 7168 (every BASELINE shape); above
 # that, batches of 2+ rows fall back to the streaming kernel's different summation order.
 INVARIANCE_CASES = [(6144, 6144, m) for m in (2, 3, 4, 5, 6, 7, 8)] + [
-    (4096, 4096, 4), (1001, 2048, 8), (300, 2304, 3), (512, 4096, 12), (64, 7168, 8)]
+    (4096, 4096, 4), (1001, 2048, 8), (300, 2304, 3), (512, 4096, 12), (64, 7168, 8),
+    # persistent multi-row kernel: three tiles per CU with a ragged last tile, two tiles per
+    # CU, a single tile, and one tile too many for it (the per-tile kernels take over)
+    (6100, 6144, 3), (2050, 4096, 6), (8, 2048, 2), (6144 + 24, 6144, 8)]
 
 
 @pytest.mark.parametrize("N,K,M", INVARIANCE_CASES)
