@@ -36,7 +36,7 @@ constexpr int kPMaxCW = 12;       // compute waves per workgroup
 constexpr int kPMaxTT = 8;        // tiles per workgroup
 constexpr int kPMaxNsb = 32;      // K <= 8192
 constexpr int kPMaxPairs = kPMaxNsb / 2;
-constexpr int kPStage = 1088;     // per pair: 1 KB of operand entries + 16 sub-block sums
+constexpr int kPStage = kStgBytes; // per pair: operand entries + 16 sub-block sums
 
 // R rounds per tile (ceil(row bytes / 1 KB)), TT tiles per workgroup, XPW pairs per compute
 // wave.  nsb = K / 256 is a runtime value with ceil(144 * nsb / 1024) == R.
@@ -135,19 +135,19 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
             "s_mov_b64 %[sv], exec\n\t"
             "s_and_b64 exec, exec, %[mask]\n\t"
             "ds_read_b128 %[a0], %[aa]\n\t"
-            "ds_read_b128 %[a1], %[aa] offset:128\n\t"
-            "ds_read_b128 %[a2], %[aa] offset:256\n\t"
-            "ds_read_b128 %[a3], %[aa] offset:384\n\t"
-            "ds_read_b128 %[a4], %[aa] offset:512\n\t"
-            "ds_read_b128 %[a5], %[aa] offset:640\n\t"
-            "ds_read_b128 %[a6], %[aa] offset:768\n\t"
-            "ds_read_b128 %[a7], %[aa] offset:896\n\t"
+            "ds_read_b128 %[a1], %[aa] offset:144\n\t"
+            "ds_read_b128 %[a2], %[aa] offset:288\n\t"
+            "ds_read_b128 %[a3], %[aa] offset:432\n\t"
+            "ds_read_b128 %[a4], %[aa] offset:576\n\t"
+            "ds_read_b128 %[a5], %[aa] offset:720\n\t"
+            "ds_read_b128 %[a6], %[aa] offset:864\n\t"
+            "ds_read_b128 %[a7], %[aa] offset:1008\n\t"
             "s_mov_b64 exec, %[sv]\n\t"
             "ds_read_b64 %[as], %[sa]\n\t"
             "s_waitcnt lgkmcnt(0)"
             : [a0] "+v"(A[i][0]), [a1] "+v"(A[i][1]), [a2] "+v"(A[i][2]), [a3] "+v"(A[i][3]), [a4] "+v"(A[i][4]),
               [a5] "+v"(A[i][5]), [a6] "+v"(A[i][6]), [a7] "+v"(A[i][7]), [as] "=&v"(as[i]), [sv] "=&s"(saved)
-            : [aa] "v"(aa), [mask] "s"(diag_mask(2)), [sa] "v"(lds_addr(st) + 1024u + 8u * (uint32_t)(g * 2 + h))
+            : [aa] "v"(aa), [mask] "s"(diag_mask(2)), [sa] "v"(lds_addr(st) + kStgSums + 8u * (uint32_t)(g * 2 + h))
             : "memory", "scc");   // s_and_b64 writes SCC
     }
     const HdrSel hs = hdr_sel(g);

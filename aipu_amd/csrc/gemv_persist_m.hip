@@ -35,7 +35,7 @@ constexpr int kMaxNp = 12;       // block pairs per row (K <= 6144)
 constexpr int kLoads = 9;        // direct-to-LDS loads per round
 constexpr uint32_t kRoundRow = 128u * kLoads;   // bytes of a row per round (4 block pairs)
 constexpr uint32_t kSlot = kTR8 * kRoundRow;    // bytes of a round
-constexpr uint32_t kStg = 1088;  // staged pair: 1 KB of operand entries + 16 sub-block sums
+constexpr uint32_t kStg = kStgBytes;   // staged pair: operand entries + 16 sub-block sums
 constexpr int kNS = 4;           // round slots
 constexpr int kReaders = 4;      // sets that read a round
 
@@ -46,19 +46,19 @@ __device__ __forceinline__ void read_rows(u32x4_t (&A)[4], u32x4_t (&B)[4], floa
                                           uint32_t st1, int g, int n, int h) {
     const int j = n - 4 * g;   // 0 .. 3 on the operand lanes
     const uint32_t aa = ((j >> 1) & 1 ? st1 : st0) + 32u * (uint32_t)g + 16u * (uint32_t)(j & 1);
-    const uint32_t so = 1024u + 8u * (uint32_t)(g * 2 + h);
+    const uint32_t so = kStgSums + 8u * (uint32_t)(g * 2 + h);
     uint64_t saved;
     asm volatile(
         "s_mov_b64 %[sv], exec\n\t"
         "s_and_b64 exec, exec, %[mask]\n\t"
         "ds_read_b128 %[a0], %[aa]\n\t"
-        "ds_read_b128 %[a1], %[aa] offset:128\n\t"
-        "ds_read_b128 %[a2], %[aa] offset:256\n\t"
-        "ds_read_b128 %[a3], %[aa] offset:384\n\t"
-        "ds_read_b128 %[b0], %[aa] offset:512\n\t"
-        "ds_read_b128 %[b1], %[aa] offset:640\n\t"
-        "ds_read_b128 %[b2], %[aa] offset:768\n\t"
-        "ds_read_b128 %[b3], %[aa] offset:896\n\t"
+        "ds_read_b128 %[a1], %[aa] offset:144\n\t"
+        "ds_read_b128 %[a2], %[aa] offset:288\n\t"
+        "ds_read_b128 %[a3], %[aa] offset:432\n\t"
+        "ds_read_b128 %[b0], %[aa] offset:576\n\t"
+        "ds_read_b128 %[b1], %[aa] offset:720\n\t"
+        "ds_read_b128 %[b2], %[aa] offset:864\n\t"
+        "ds_read_b128 %[b3], %[aa] offset:1008\n\t"
         "s_mov_b64 exec, %[sv]\n\t"
         "ds_read_b64 %[s0], %[p0]\n\t"
         "ds_read_b64 %[s1], %[p1]\n\t"
@@ -111,16 +111,23 @@ __global__ __launch_bounds__(64 * (4 * 3 + 1)) void k_gemvmp(const uint8_t* __re
         // ---- copy wave
         uint32_t cnt0 = lds_addr(s_cnt);
         asm volatile("" : "+v"(cnt0));   // a runtime base (see lds_post)
-        // round u is issued once its slot is free (round u - kNS read by its four readers) and
-        // posted, in order, once kNS - 1 later rounds are in flight behind it
+        // Round u is issued once its slot is free (round u - kNS read by its four readers) and
+        // posted, in order, once kNS - 1 later rounds are in flight behind it.  While a slot is
+        // still being read, every round but the newest is posted first, so no reader waits for
+        // a round that has landed.
         int posted = 0;
         for (int u = 0; u < U; ++u) {
-            if (u >= kNS) spin_ge(&s_read[u - kNS], (uint32_t)kReaders);
+            if (u >= kNS && lds_poll(&s_read[u - kNS]) < (uint32_t)kReaders) {
+                if (posted < u - 1) {
+                    __builtin_amdgcn_s_waitcnt(wait_vm(kLoads));
+                    while (posted < u - 1) lds_post(cnt0 + 4u * (uint32_t)posted++);
+                }
+                spin_ge(&s_read[u - kNS], (uint32_t)kReaders);
+            }
             issue(u);
-            if (u >= kNS - 1) {
+            if (posted <= u - (kNS - 1)) {
                 __builtin_amdgcn_s_waitcnt(wait_vm(kLoads * (kNS - 1)));
-                lds_post(cnt0 + 4u * (uint32_t)posted);
-                ++posted;
+                while (posted <= u - (kNS - 1)) lds_post(cnt0 + 4u * (uint32_t)posted++);
             }
         }
         const int left = U - posted;   // the oldest of `left` unposted rounds has landed once kLoads * (left - 1) loads remain

@@ -28,31 +28,28 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // Staging of one block pair's activations (512 bf16, 1 KB) for the block-diagonal MFMA
-// operand: entry e = 8t + 2g + h (16 B) holds activations 8t' .. 8t'+7 of sub-block 2g + (t >> 2)
-// of block h, t' = t & 3 -- the operand of MFMA t on K-group g -- followed by the 16 sub-block
-// sums (float, index 2(2g + h) + (t >> 2)).  xv is lane L's contiguous 16-B chunk of the pair
-// (chunk L = 32h + 8g + t); a lane permute hands lane e the chunk of entry e, so the entry
-// writes are linear in the lane and free of bank conflicts while the loads stay contiguous.
-// Each sub-block sum is ((c0 + c1) + (c2 + c3)) over its four chunks' sums c_t' (lanes
-// 2g + h + 8t), the order every fast-mode kernel uses.
-__device__ __forceinline__ void stage_pair(const uint4& xl, uint8_t* st, int L) {
-    const int src = 4 * (32 * (L & 1) + 8 * ((L >> 1) & 3) + (L >> 3));   // byte index of the chunk's lane
-    uint4 xv;
-    xv.x = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xl.x);
-    xv.y = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xl.y);
-    xv.z = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xl.z);
-    xv.w = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xl.w);
+// operand.  The operand of MFMA t (t < 4: low nibbles, sub-block 2g; t >= 4: high nibbles,
+// sub-block 2g + 1) on K-group g for block h is the 16-B chunk 32h + 8g + t of the pair; it is
+// stored at entry 9t + 2g + h (kStgStride = 144 B per t), so lane L = 32h + 8g + t writes its own
+// contiguously loaded chunk and the eight lanes with equal (g, h) land on eight different bank
+// groups.  A reader takes MFMA t's operand at 32g + 16h + 144t.  The 16 sub-block sums follow at
+// kStgSums (float, index 2(2g + h) + (t >> 2)), each ((c0 + c1) + (c2 + c3)) over its four
+// chunks' sums, the order every fast-mode kernel uses.
+constexpr uint32_t kStgStride = 144;
+constexpr uint32_t kStgSums = 1136;
+constexpr uint32_t kStgBytes = 1200;
+__device__ __forceinline__ void stage_pair(const uint4& xv, uint8_t* st, int L) {
     const uint32_t ones = 0x3F803F80u;
     float c = 0.f;
     c = mg::dot2(xv.x, ones, c);
     c = mg::dot2(xv.y, ones, c);
     c = mg::dot2(xv.z, ones, c);
     c = mg::dot2(xv.w, ones, c);
-    const float c2 = c + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x108, 0xF, 0xF, false));   // + lane L + 8
-    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(c2), __float_as_uint(c2), false, false);
-    const float c4 = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);                                              // + lane L +- 16
-    *(u32x4_t*)(st + 16u * (uint32_t)L) = mg::act_perm(xv);
-    if ((L & 16) == 0 && (L & 8) == 0) ((float*)(st + 1024u))[2 * (L & 7) + (L >> 5)] = c4;
+    c += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0xB1, 0xF, 0xF, false));   // xor 1
+    c += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x4E, 0xF, 0xF, false));   // xor 2
+    const int h = L >> 5, g = (L >> 3) & 3, t = L & 7;
+    *(u32x4_t*)(st + 16u * (uint32_t)(9 * t + 2 * g + h)) = mg::act_perm(xv);
+    if ((L & 3) == 0) ((float*)(st + kStgSums))[(g * 2 + h) * 2 + (t >> 2)] = c;
 }
 
 // LDS counters.  A post is one ds_add from lane 0 (exec = 1); DS operations of a wave
