@@ -716,14 +716,10 @@ hipError_t launch_gemv_fast(int type, const void* w, int64_t N, int64_t K, const
         case T_Q6_K:
         case T_Q8_0:
         case T_F16: {
-            // one tile covering all N rows, one launch per activation row
+            // one tile covering all N rows; the activation rows share each weight pass
             if (!gemv_mixed_supported(type, K)) return hipErrorInvalidValue;
             const aipu_tile_desc d{type, 0, w, 0, N};
-            for (int64_t m = 0; m < M; ++m) {
-                const hipError_t e = launch_gemv_mixed(&d, 1, K, x + m * K, y + m * N, y_f32 ? y_f32 + m * N : nullptr, st);
-                if (e != hipSuccess) return e;
-            }
-            return hipSuccess;
+            return launch_gemv_mixed(&d, 1, K, x, M, y, y_f32, N, st);
         }
         default: return hipErrorInvalidValue;
     }

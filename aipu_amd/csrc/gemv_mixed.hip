@@ -1,4 +1,4 @@
-// Mixed-type GEMV (tolerance mode, one activation row): one launch over a list of tiles,
+// Mixed-type GEMV (tolerance mode, MR <= 4 activation rows per launch): one launch over a list of tiles,
 // each a run of output rows stored as Q4_K, Q6_K, Q8_0, F16 or BF16 -- the per-column
 // w_type mux of src/glm_matmul_q4k.v:76-101,197-259 over the tile sequence of
 // tools/q4k_mixed_gen.py:382-440.  A single-tile call serves the plain GEMV of the types
@@ -9,7 +9,10 @@
 // rows group by group (GS blocks per group) into its own LDS slice with direct-to-LDS buffer
 // loads (16 consecutive bytes per lane, so one instruction covers ~1 KB of row bytes), and
 // copies a group into registers before the next group's loads are issued into the slice.
-// The four parts are added in fixed order, so results are deterministic.
+// The four parts are added in fixed order, so results are deterministic.  With MR rows each
+// wave stages every row's activations and applies each group of weights, decoded once in
+// registers, to all of them: the weights are read once per launch, and each row's sums are
+// formed exactly as in a one-row launch (the rows of a batch equal their single-row results).
 //
 // Lane layout: lane 16g + n works on row n of the group and on weights 64g..64g+63 of every
 // block (a Q6_K lane instead takes half g>>1, positions l = 16(g&1)..+15 of the four
@@ -261,9 +264,9 @@ struct ActRegion {
     static constexpr int kSumOffQ = kBlocks * 512;    // Q4_K: sums32
 };
 
-template <int TYPE, int XI>
-__device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16_t* __restrict__ X, int K,
-                                         uint8_t* wA, uint8_t* wW, float* red, uint16_t* Y, float* Yf) {
+template <int TYPE, int XI, int MR>
+__device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16_t* __restrict__ X, int K, int M,
+                                         uint8_t* wA, uint8_t* wW, float* red, uint16_t* Y, float* Yf, int64_t ys) {
     typedef Geom<TYPE> G;
     typedef ActRegion<XI> AR;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -276,66 +279,74 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
     const int r0 = grp * kTR;
     const int nvalid = T.nrows - r0 < kTR ? T.nrows - r0 : kTR;
 
-    // 1. this wave's activations (pieces past its blocks read as zero), 2. its first group
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)K * 2u);
+    // 1. this wave's activations of every row (pieces past its blocks, and rows past M, read
+    // as zero), 2. its first group
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)(M * K) * 2u);
     const uint32_t xbase = 2u * (uint32_t)(kb0 * QK_K);
     const int XP = bpk * 32;
-    uint4 xv[XI];
+    uint4 xv[MR][XI];
 #pragma unroll
-    for (int i = 0; i < XI; ++i) {
-        const int q = lane + 64 * i;
-        xv[i] = buf_load16(xr, q < XP ? xbase + 16u * q : kOOB);
-    }
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int q = lane + 64 * i;
+            xv[m][i] = buf_load16(xr, q < XP && m < M ? 2u * (uint32_t)(m * K) + xbase + 16u * q : kOOB);
+        }
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(T.w + (int64_t)r0 * rb, (uint32_t)(nvalid * rb));
     MixDma<TYPE> dma;
     dma.init(lane, rb);
     dma.issue(wr, wW, kb0, bpk < G::GS ? bpk : G::GS);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. stage (every piece of the region, so blocks past bpk hold zeros)
-    if constexpr (TYPE == T_Q4_K) {
-        float* wS = (float*)(wA + AR::kSumOffQ);
+    // 3. stage (every piece of the region, so blocks past bpk hold zeros); row m at m * kBytes
 #pragma unroll
-        for (int i = 0; i < XI; ++i) {
-            const int q = lane + 64 * i;
-            const uint32_t ones = 0x3F803F80u;
-            float sm = 0.f;
-            sm = dot2(xv[i].x, ones, sm);
-            sm = dot2(xv[i].y, ones, sm);
-            sm = dot2(xv[i].z, ones, sm);
-            sm = dot2(xv[i].w, ones, sm);
-            sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
-            sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
-            const int bb = q >> 5, gg = (q >> 3) & 3, t = q & 7;
-            *(u32x4_t*)(wA + 16u * (uint32_t)((bb * 8 + t) * 4 + gg)) = act_perm(xv[i]);
-            if ((q & 3) == 0) wS[(bb * 4 + gg) * 2 + ((q >> 2) & 1)] = sm;
-        }
-    } else {
-        float* wF = (float*)wA;
-        float* wS = (float*)(wA + AR::kSumOffF);
+    for (int m = 0; m < MR; ++m) {
+        uint8_t* rA = wA + m * AR::kBytes;
+        if constexpr (TYPE == T_Q4_K) {
+            float* wS = (float*)(rA + AR::kSumOffQ);
 #pragma unroll
-        for (int i = 0; i < XI; ++i) {
-            const int q = lane + 64 * i;
-            const uint32_t v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-            float f[8];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                f[2 * k] = __uint_as_float(v[k] << 16);
-                f[2 * k + 1] = __uint_as_float(v[k] & 0xFFFF0000u);
+            for (int i = 0; i < XI; ++i) {
+                const int q = lane + 64 * i;
+                const uint32_t ones = 0x3F803F80u;
+                float sm = 0.f;
+                sm = dot2(xv[m][i].x, ones, sm);
+                sm = dot2(xv[m][i].y, ones, sm);
+                sm = dot2(xv[m][i].z, ones, sm);
+                sm = dot2(xv[m][i].w, ones, sm);
+                sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+                sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+                const int bb = q >> 5, gg = (q >> 3) & 3, t = q & 7;
+                *(u32x4_t*)(rA + 16u * (uint32_t)((bb * 8 + t) * 4 + gg)) = act_perm(xv[m][i]);
+                if ((q & 3) == 0) wS[(bb * 4 + gg) * 2 + ((q >> 2) & 1)] = sm;
             }
-            float sm = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
-            sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
-            *(float4*)(wF + 8 * q) = make_float4(f[0], f[1], f[2], f[3]);
-            *(float4*)(wF + 8 * q + 4) = make_float4(f[4], f[5], f[6], f[7]);
-            if ((q & 1) == 0) wS[q >> 1] = sm;
+        } else {
+            float* wF = (float*)rA;
+            float* wS = (float*)(rA + AR::kSumOffF);
+#pragma unroll
+            for (int i = 0; i < XI; ++i) {
+                const int q = lane + 64 * i;
+                const uint32_t v[4] = {xv[m][i].x, xv[m][i].y, xv[m][i].z, xv[m][i].w};
+                float f[8];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    f[2 * k] = __uint_as_float(v[k] << 16);
+                    f[2 * k + 1] = __uint_as_float(v[k] & 0xFFFF0000u);
+                }
+                float sm = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+                sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+                *(float4*)(wF + 8 * q) = make_float4(f[0], f[1], f[2], f[3]);
+                *(float4*)(wF + 8 * q + 4) = make_float4(f[4], f[5], f[6], f[7]);
+                if ((q & 1) == 0) wS[q >> 1] = sm;
+            }
         }
     }
 
-    // 4. group loop
+    // 4. group loop: the lane's weights of a group, decoded once, against every row
     const int n = lane & 15, g = lane >> 4;
-    float acc = 0.f;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.f;
     if constexpr (TYPE == T_Q4_K) {
-        const float* wS = (const float*)(wA + AR::kSumOffQ);
         u32x4_t A[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) A[t] = u32x4_t{0u, 0u, 0u, 0u};
@@ -361,14 +372,16 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
 #pragma unroll
             for (int bb = 0; bb < G::GS; ++bb) {
                 const int b = gi * G::GS + bb;
-                a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
-                const float2 as = *(const float2*)(wS + (b * 4 + g) * 2);
-                acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    const uint8_t* rA = wA + m * AR::kBytes;
+                    a_reads(A, lds_addr(rA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
+                    const float2 as = *(const float2*)((const float*)(rA + AR::kSumOffQ) + (b * 4 + g) * 2);
+                    acc[m] = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc[m]);
+                }
             }
         }
     } else {
-        const float* wF = (const float*)wA;
-        const float* wS = (const float*)(wA + AR::kSumOffF);
         const uint32_t rrow = (uint32_t)n * (uint32_t)(G::kPitch * G::GS);
         for (int gi = 0; gi < NG; ++gi) {
             __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -385,7 +398,11 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
 #pragma unroll
                 for (int bb = 0; bb < G::GS; ++bb) {
                     const int b = gi * G::GS + bb;
-                    acc = q6_block(R[bb], wF + 256 * b, wS + 16 * b, g, acc);
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) {
+                        const uint8_t* rA = wA + m * AR::kBytes;
+                        acc[m] = q6_block(R[bb], (const float*)rA + 256 * b, (const float*)(rA + AR::kSumOffF) + 16 * b, g, acc[m]);
+                    }
                 }
             } else if constexpr (TYPE == T_Q8_0) {
                 RawQ8 R[G::GS];
@@ -399,7 +416,11 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
 #pragma unroll
                 for (int bb = 0; bb < G::GS; ++bb) {
                     const int b = gi * G::GS + bb;
-                    acc = q8_block(R[bb], wF + 256 * b, wS + 16 * b, g, acc);
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) {
+                        const uint8_t* rA = wA + m * AR::kBytes;
+                        acc[m] = q8_block(R[bb], (const float*)rA + 256 * b, (const float*)(rA + AR::kSumOffF) + 16 * b, g, acc[m]);
+                    }
                 }
             } else {
                 Raw128 R[G::GS];
@@ -415,7 +436,9 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
 #pragma unroll
                 for (int bb = 0; bb < G::GS; ++bb) {
                     const int b = gi * G::GS + bb;
-                    acc = f16_block<TYPE>(R[bb], wF + 256 * b, g, acc);
+#pragma unroll
+                    for (int m = 0; m < MR; ++m)
+                        acc[m] = f16_block<TYPE>(R[bb], (const float*)(wA + m * AR::kBytes) + 256 * b, g, acc[m]);
                 }
             }
         }
@@ -423,30 +446,35 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
     // a wave with no blocks still has its (all-zero) first group in flight
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
-    // 5. reduce over the four K-groups, then across the four parts in order
-    acc += __shfl_xor(acc, 16, 64);
-    acc += __shfl_xor(acc, 32, 64);
-    if (lane < kTR) red[w * kTR + lane] = acc;
+    // 5. per row: reduce over the four K-groups, then across the four parts in order
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        float a = acc[m];
+        a += __shfl_xor(a, 16, 64);
+        a += __shfl_xor(a, 32, 64);
+        if (lane < kTR) red[(m * kMixW + w) * kTR + lane] = a;
+    }
     __syncthreads();
-    if (tid < nvalid) {
+    const int m = tid / kTR, rr = tid - m * kTR;
+    if (m < MR && m < M && rr < nvalid) {
         float v = 0.f;
 #pragma unroll
-        for (int k = 0; k < kMixW; ++k) v += red[k * kTR + tid];
-        const int64_t row = T.row0 + r0 + tid;
-        Y[row] = (uint16_t)bf16_rne(v);
-        if (Yf) Yf[row] = v;
+        for (int k = 0; k < kMixW; ++k) v += red[(m * kMixW + k) * kTR + rr];
+        const int64_t row = T.row0 + r0 + rr;
+        Y[(int64_t)m * ys + row] = (uint16_t)bf16_rne(v);
+        if (Yf) Yf[(int64_t)m * ys + row] = v;
     }
 }
 
-template <int XI>
-__global__ __launch_bounds__(kMixW * 64) void k_mixed(MixArgs args, const uint16_t* __restrict__ X, int K,
-                                                      uint16_t* __restrict__ Y, float* __restrict__ Yf) {
+template <int XI, int MR>
+__global__ __launch_bounds__(kMixW * 64) void k_mixed(MixArgs args, const uint16_t* __restrict__ X, int K, int M,
+                                                      uint16_t* __restrict__ Y, float* __restrict__ Yf, int64_t ys) {
     typedef ActRegion<XI> AR;
     // the staged activations live in a static LDS object of their own and the weight
     // slices in the dynamic one, so the compiler can tell the staging writes from the
     // direct-to-LDS loads in flight and does not make them wait for those
-    __shared__ __align__(16) uint8_t s_act[kMixW * AR::kBytes];
-    __shared__ float red[kMixW * kTR];
+    __shared__ __align__(16) uint8_t s_act[kMixW * MR * AR::kBytes];
+    __shared__ float red[MR * kMixW * kTR];
     extern __shared__ __align__(16) uint8_t s_w[];
     const int wg = blockIdx.x;
     int t = 0;
@@ -454,25 +482,29 @@ __global__ __launch_bounds__(kMixW * 64) void k_mixed(MixArgs args, const uint16
     const MixTile T = args.t[t];
     const int grp = wg - T.wg0;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    uint8_t* wA = s_act + w * AR::kBytes;
+    uint8_t* wA = s_act + w * MR * AR::kBytes;
     uint8_t* wW = s_w + w * kSliceBytes;
     switch (T.type) {
-        case T_Q4_K: mix_body<T_Q4_K, XI>(T, grp, X, K, wA, wW, red, Y, Yf); break;
-        case T_Q6_K: mix_body<T_Q6_K, XI>(T, grp, X, K, wA, wW, red, Y, Yf); break;
-        case T_Q8_0: mix_body<T_Q8_0, XI>(T, grp, X, K, wA, wW, red, Y, Yf); break;
-        case T_F16: mix_body<T_F16, XI>(T, grp, X, K, wA, wW, red, Y, Yf); break;
-        default: mix_body<T_BF16, XI>(T, grp, X, K, wA, wW, red, Y, Yf); break;
+        case T_Q4_K: mix_body<T_Q4_K, XI, MR>(T, grp, X, K, M, wA, wW, red, Y, Yf, ys); break;
+        case T_Q6_K: mix_body<T_Q6_K, XI, MR>(T, grp, X, K, M, wA, wW, red, Y, Yf, ys); break;
+        case T_Q8_0: mix_body<T_Q8_0, XI, MR>(T, grp, X, K, M, wA, wW, red, Y, Yf, ys); break;
+        case T_F16: mix_body<T_F16, XI, MR>(T, grp, X, K, M, wA, wW, red, Y, Yf, ys); break;
+        default: mix_body<T_BF16, XI, MR>(T, grp, X, K, M, wA, wW, red, Y, Yf, ys); break;
     }
 }
 
 // Blocks per wave the activation region of k_mixed<XI> holds (every type's groups rounded
-// up to whole groups must fit).
+// up to whole groups must fit): 2 XI blocks.
 int mix_xi(int64_t K) {
     const int nsb = (int)(K / QK_K);
     const int bpk = (nsb + kMixW - 1) / kMixW;
     const int need = (bpk + 2) / 3 * 3 > (bpk + 1) / 2 * 2 ? (bpk + 2) / 3 * 3 : (bpk + 1) / 2 * 2;
-    return need <= 4 ? 2 : need <= 8 ? 4 : need <= 16 ? 8 : 0;
+    return need <= 4 ? 2 : need <= 6 ? 3 : need <= 8 ? 4 : need <= 16 ? 8 : 0;
 }
+
+// Activation rows per launch that the LDS holds beside the weight slices (160 KB): four up
+// to 6 blocks per wave (K <= 6144), two up to 8 (K <= 8192), one beyond.
+int mix_rows(int xi) { return xi <= 3 ? 4 : xi == 4 ? 2 : 1; }
 
 bool mix_type(int t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0 || t == T_F16 || t == T_BF16; }
 
@@ -482,10 +514,11 @@ bool gemv_mixed_supported(int type, int64_t K) {
     return mix_type(type) && K >= QK_K && K % QK_K == 0 && mix_xi(K) != 0;
 }
 
-// One launch over all tiles (one activation row).  Rows of y outside the tiles are untouched.
-hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K, const uint16_t* x, uint16_t* y,
-                             float* y_f32, hipStream_t st) {
-    if (n_tiles < 1 || n_tiles > AIPU_MAX_TILES) return hipErrorInvalidValue;
+// One launch over all tiles per pass of up to mix_rows(XI) activation rows; row m of the
+// output starts at y + m * ys.  Rows of y outside the tiles are untouched.
+hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K, const uint16_t* x, int64_t M,
+                             uint16_t* y, float* y_f32, int64_t ys, hipStream_t st) {
+    if (n_tiles < 1 || n_tiles > AIPU_MAX_TILES || M < 1) return hipErrorInvalidValue;
     MixArgs a{};
     int64_t nwg = 0;
     for (int i = 0; i < n_tiles; ++i) {
@@ -498,13 +531,25 @@ hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K
     a.n = n_tiles;
     const dim3 grid((unsigned)nwg), block(kMixW * 64);
     const size_t lds = (size_t)kMixW * kSliceBytes;
-    switch (mix_xi(K)) {
-        case 2: hipLaunchKernelGGL(k_mixed<2>, grid, block, lds, st, a, x, (int)K, y, y_f32); break;
-        case 4: hipLaunchKernelGGL(k_mixed<4>, grid, block, lds, st, a, x, (int)K, y, y_f32); break;
-        case 8: hipLaunchKernelGGL(k_mixed<8>, grid, block, lds, st, a, x, (int)K, y, y_f32); break;
-        default: return hipErrorInvalidValue;
+    const int xi = mix_xi(K), mrmax = mix_rows(xi);
+    for (int64_t m0 = 0; m0 < M;) {
+        const int rows = (int)(M - m0 < mrmax ? M - m0 : mrmax);
+        const uint16_t* xm = x + m0 * K;
+        uint16_t* ym = y + m0 * ys;
+        float* yfm = y_f32 ? y_f32 + m0 * ys : nullptr;
+        const int mr = rows > 2 ? 4 : rows;
+#define AIPU_MIX(XV, MV) \
+    if (xi == XV && mr == MV) hipLaunchKernelGGL((k_mixed<XV, MV>), grid, block, lds, st, a, xm, (int)K, rows, ym, yfm, ys);
+        AIPU_MIX(2, 1) AIPU_MIX(2, 2) AIPU_MIX(2, 4)
+        AIPU_MIX(3, 1) AIPU_MIX(3, 2) AIPU_MIX(3, 4)
+        AIPU_MIX(4, 1) AIPU_MIX(4, 2)
+        AIPU_MIX(8, 1)
+#undef AIPU_MIX
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        m0 += rows;
     }
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 }  // namespace aipu

@@ -49,10 +49,10 @@ hipError_t launch_gemv_tiles(const aipu_tile_desc* tiles, int n_tiles, int64_t N
                              int64_t M, uint16_t* y, float* y_f32, int mode, hipStream_t st);
 
 // gemv_mixed.hip -- one-launch GEMV over tiles of Q4_K / Q6_K / Q8_0 / F16 / BF16 rows
-// (tolerance mode, one activation row per launch)
+// (tolerance mode, up to four activation rows per weight pass; row m of y at y + m * ys)
 bool gemv_mixed_supported(int type, int64_t K);
-hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K, const uint16_t* x, uint16_t* y,
-                             float* y_f32, hipStream_t st);
+hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K, const uint16_t* x, int64_t M,
+                             uint16_t* y, float* y_f32, int64_t ys, hipStream_t st);
 
 // gemv_persist.hip -- persistent single-row Q4_K GEMV (tolerance mode, K <= 8192)
 bool gemv_persist_supported(int64_t N, int64_t K);

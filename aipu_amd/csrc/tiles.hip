@@ -13,17 +13,10 @@ hipError_t launch_gemv_tiles(const aipu_tile_desc* tiles, int n_tiles, int64_t N
     // an [M][nrows] block of the [M][N] output with row stride N, which the per-row
     // kernels express by running once per activation row.
     if (mode == AIPU_MODE_FAST) {
-        // every tile in one launch per activation row (gemv_mixed.hip)
+        // every tile in one launch, the activation rows in passes of up to four (gemv_mixed.hip)
         bool all = true;
         for (int t = 0; t < n_tiles; ++t) all = all && gemv_mixed_supported(tiles[t].ggml_type, K);
-        if (all) {
-            for (int64_t m = 0; m < M; ++m) {
-                const hipError_t e =
-                    launch_gemv_mixed(tiles, n_tiles, K, x + m * K, y + m * N, y_f32 ? y_f32 + m * N : nullptr, st);
-                if (e != hipSuccess) return e;
-            }
-            return hipSuccess;
-        }
+        if (all) return launch_gemv_mixed(tiles, n_tiles, K, x, M, y, y_f32, N, st);
     }
     for (int t = 0; t < n_tiles; ++t) {
         const aipu_tile_desc& d = tiles[t];

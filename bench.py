@@ -321,10 +321,11 @@ def gen_blocks(ggml_type, n_rows, K, gen, device):
     raise ValueError(ggml_type)
 
 
-def bench_tiles(dev, torch, steps=200, rot_bytes=1.05e9):
+def bench_tiles(dev, torch, steps=200, rot_bytes=1.05e9, M=1):
     """24 column tiles of 256 rows cycling Q4_K, Q6_K, Q8_0, F16 at K=6144,
-    generated on the device.  Cold: the launches rotate over enough distinct tile sets (>= 1 GB)
-    that every launch streams its 42 MB from HBM; hot (labelled): one set, cache-resident."""
+    generated on the device, for M activation rows (M > 1: a verify batch, all rows in one weight
+    pass).  Cold: the launches rotate over enough distinct tile sets (>= 1 GB) that every launch
+    streams its 42 MB from HBM; hot (labelled): one set, cache-resident."""
     K, rows = 6144, 256
     types = [Q4K, 14, 8, 1] * 6
     gen = torch.Generator(device="cuda")
@@ -336,8 +337,8 @@ def bench_tiles(dev, torch, steps=200, rot_bytes=1.05e9):
     sets = [one] + [[gen_blocks(t, rows, K, gen, "cuda") for t in types] for _ in range(nset - 1)]
     tsets = [[(t, w, i * rows, rows) for i, (t, w) in enumerate(zip(types, ws))] for ws in sets]
     nx = 16
-    xs = torch.randn((nx, 1, K), device="cuda", generator=gen).to(torch.bfloat16)
-    y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+    xs = torch.randn((nx, M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     nl = max(steps, nset)
     ms, _ = time_graph([(lambda j=i: dev.gemv_tiles(tsets[j % nset], N, K, xs[j % nx], mode="fast", out=y))
                         for i in range(nl)], reps=REPS)
@@ -345,11 +346,11 @@ def bench_tiles(dev, torch, steps=200, rot_bytes=1.05e9):
     hot_ms, _ = time_graph([(lambda j=i: dev.gemv_tiles(tsets[0], N, K, xs[j % nx], mode="fast", out=y))
                             for i in range(steps)], reps=REPS)
     hot = 1000.0 * pct(hot_ms, 50) / steps
-    alg = wbytes + 2 * K + 2 * N
+    alg = wbytes + 2 * M * K + 2 * M * N
     del sets, tsets
     torch.cuda.empty_cache()
-    log(f"mixed tiles: cold {us:.1f} us ({alg / (us * 1e-6) / 1e9:.0f} GB/s), hot {hot:.1f} us")
-    return dict(N=N, K=K, us=us, alg_bytes=alg, gbs=alg / (us * 1e-6) / 1e9,
+    log(f"mixed tiles M={M}: cold {us:.1f} us ({alg / (us * 1e-6) / 1e9:.0f} GB/s), hot {hot:.1f} us")
+    return dict(N=N, K=K, M=M, us=us, alg_bytes=alg, gbs=alg / (us * 1e-6) / 1e9,
                 pct_peak=100.0 * alg / (us * 1e-6) / 1e9 / PEAK_GBS, rotation_sets=nset,
                 rotation_bytes=nset * wbytes, timing=f"median of {REPS} replays of one HIP graph of {nl} launches",
                 hot_us_cache_resident=hot, hot_gbs_cache_resident=alg / (hot * 1e-6) / 1e9)
@@ -579,7 +580,7 @@ def main():
         print(json.dumps(bench_moe(dev, torch, args.moe_steps)))
         return
     if args.only == "tiles":
-        print(json.dumps(bench_tiles(dev, torch)))
+        print(json.dumps({"m1": bench_tiles(dev, torch), "m4": bench_tiles(dev, torch, M=4)}))
         return
     if args.only == "prefill":
         print(json.dumps(bench_prefill(dev, torch)))
@@ -617,6 +618,7 @@ def main():
         for M in (2, 4, 8):
             extra[f"gemv_c1_m{M}"] = bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, label="C1")
         extra["mixed_tiles_c3"] = bench_tiles(dev, torch)
+        extra["mixed_tiles_c3_m4"] = bench_tiles(dev, torch, M=4)
         extra["prefill_c4"] = bench_prefill(dev, torch)
         log(f"prefill: {extra['prefill_c4']['ms']:.2f} ms, {extra['prefill_c4']['tflops']:.1f} TFLOP/s")
         extra["lm_head_f4"] = bench_lmhead(dev, torch)

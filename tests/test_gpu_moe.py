@@ -288,6 +288,33 @@ def test_mixed_tiles_c3_full_shape():
     assert qo.bf16_parity(h_bits(y), acc, w, qo.bf16_bits_to_f32(x))[0]
 
 
+# Mixed-type batches share each weight pass: K = 6144 and 2048 run four (or three) rows in one
+# launch, K = 8192 two passes of two rows.  Every row must equal its single-row launch bit for
+# bit (the rows are formed independently from the same decoded weights) and pass the gate.
+@pytest.mark.parametrize("K,M", [(6144, 4), (2048, 3), (8192, 4)])
+def test_mixed_tiles_batch(K, M):
+    note(f"tiles fast batch K={K} M={M}")
+    rng = np.random.default_rng(K + M)
+    rows = 48
+    types = [Q4K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16] * 2
+    raws = [qo.random_weights(rng, t, rows, K) for t in types]
+    tiles = [(t, d_u8(r), i * rows, rows) for i, (t, r) in enumerate(zip(types, raws))]
+    N = rows * len(types)
+    x = qo.random_bf16(rng, (M, K))
+    y, yf = dev.gemv_tiles(tiles, N, K, d_bf16(x), mode="fast", out_f32=True)
+    yb, yfb = h_bits(y), u32(h_f32(yf))
+    for r in range(M):
+        y1, yf1 = dev.gemv_tiles(tiles, N, K, d_bf16(x[r:r + 1]), mode="fast", out_f32=True)
+        assert_bits_equal(u32(h_f32(yf1))[0], yfb[r], f"row {r} of M={M}: fp32 accumulators")
+        assert_bits_equal(h_bits(y1)[0], yb[r], f"row {r} of M={M}: bf16 outputs")
+    acc = np.concatenate([co.gemv_ref(t, r, rows, K, x)[0] for t, r in zip(types, raws)], axis=1)
+    w = np.concatenate([qo.dequant_matrix(t, r, rows, K) for t, r in zip(types, raws)])
+    ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
+    note(f"  worst |delta| = {worst:.4f} of the 1e-5*sum|a*w| bound")
+    assert ok, worst
+    assert qo.bf16_parity(h_bits(y), acc, w, qo.bf16_bits_to_f32(x))[0]
+
+
 def test_mixed_tiles_ragged_fast():
     """Tiles of odd row counts, out of order, with uncovered rows that must stay untouched."""
     note("tiles fast ragged")
