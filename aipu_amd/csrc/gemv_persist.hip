@@ -8,9 +8,10 @@
 // whole pipeline.  Compute waves 0 .. NCW-1 own block pairs: wave w owns pairs w, w + NCW
 // (XPW of them), stages those pairs' activations itself and keeps their block-diagonal MFMA
 // operands in registers for the whole kernel; for every tile it computes its pairs (8 rows x
-// 2 blocks, one MFMA set) as soon as the round holding them has landed.  The last wave to
-// finish a tile reduces it and stores the 8 outputs; the copy wave reuses a tile buffer once
-// that tile is reduced (NB buffers).
+// 2 blocks, one MFMA set) as soon as the round holding them has landed.  Compute wave 0
+// reduces each tile once all its pairs are in and stores the 8 outputs; the copy wave reuses
+// a tile buffer once that tile is reduced (NB buffers).  The copy wave issues its first Q
+// rounds before it joins the workgroup barrier.
 //
 // MFMA set (v_mfma_f32_16x16x32_bf16, lane 16g + n): column n = row n & 7 of the tile, block
 // 2p + (n >> 3) of the pair; K-group g = qs bytes 32g .. 32g+31 of the block (sub-blocks 2g,
@@ -79,7 +80,8 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
+    // the copy wave joins the barrier after issuing its first Q rounds (before its first post)
+    if (w != NCW) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
 
     if (w == NCW) {
         // ---- copy wave: round u = t * R + k, posted in order once landed
@@ -105,6 +107,7 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
                         lds_dma16<kNT>(wr, tb + (uint32_t)rr * P + 1024u * k, (uint32_t)rr * rb + 1024u * k + 16u * (uint32_t)lane);
             }
             constexpr int pu = step - (Q - 1);
+            if constexpr (pu == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
             if constexpr (pu >= 0) {
                 constexpr int after = (U - 1 < step ? U - 1 : step) - pu;   // rounds issued after pu
                 __builtin_amdgcn_s_waitcnt(wait_vm(kPR * after));
@@ -204,9 +207,17 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
             const float ps = bt + (2 * p + 1 < nsb ? b1 : 0.0f);
             float* rt = s_red + (t % NB) * (kPR * kPMaxPairs);
             if (lane < kPR) rt[lane * kPMaxPairs + p] = ps;
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lds_add_rtn(&s_done[t]) == (uint32_t)np - 1u) {
-                // last pair of tile t: v_k on lane 8 * row + k, then the tree (xor 1, xor 2, mirror)
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
+            lds_post(&s_done[t]);
+        }
+        // Wave 0 reduces the tile once every pair is in.  Its own pairs sit in the tile's first
+        // round, so it has time to spare; the waves of the last round, whose sets finish a tile,
+        // go straight on to the next tile.
+        if (w == 0) {
+            spin_ge(&s_done[t], (uint32_t)np);
+            const float* rt = s_red + (t % NB) * (kPR * kPMaxPairs);
+            {
+                // v_k on lane 8 * row + k, then the tree (xor 1, xor 2, mirror)
                 const int rr = lane >> 3, k = lane & 7;
                 float v = k < np ? rt[rr * kPMaxPairs + k] : 0.0f;
                 for (int j = k + 8; j < np; j += 8) v += rt[rr * kPMaxPairs + j];
