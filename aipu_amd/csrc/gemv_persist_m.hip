@@ -15,7 +15,8 @@
 // K-group g, so D[4g + 2m' + h][n] is the sub-block sum of column n for that row.  Every
 // output is formed exactly as in the single-row kernels (codes, seeds, MFMA order, epilogue,
 // block_sum, pair sum, the balanced tree over the pairs), so row m of a batch is bit-identical
-// to the single-row launch on that row.
+// to the single-row launch on that row.  From five rows on, compute wave 0 reduces each tile
+// once all its pairs are in; below that the tile's last wave does.
 #include "common.hpp"
 #include "launch.hpp"
 #include "mfma_gemv.hpp"
@@ -233,8 +234,18 @@ __global__ __launch_bounds__(64 * (4 * 3 + 1)) void k_gemvmp(const uint8_t* __re
             if (h == 0 && (2 * q + 1 < M2 || g < 2)) rt[((4 * q + i) * kTR8 + r) * kMaxNp + p] = bs + b1;   // (nsb is even)
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
-        if (lds_add_rtn(&s_done[t]) != (uint32_t)np - 1u) continue;
-        // the tile's last pair: per row, v_k on lane 8 * tile row + k, then the tree
+        if constexpr (M2 >= 3) {
+            // Five rows or more: wave 0 reduces the tile once every pair is in.  Its pair sits in
+            // the tile's first round, so it has time to spare, and the waves of the last round go
+            // straight on instead of reducing rows first.
+            lds_post(&s_done[t]);
+            if (w != 0) continue;
+            spin_ge(&s_done[t], (uint32_t)np);
+        } else {
+            // fewer rows: the tile's last wave reduces it (cheaper than a waiting reducer)
+            if (lds_add_rtn(&s_done[t]) != (uint32_t)np - 1u) continue;
+        }
+        // per row, v_k on lane 8 * tile row + k, then the tree
         const int rr = lane >> 3, k = lane & 7;
         const int64_t row = (int64_t)(wg + t * G) * kTR8 + rr;
         float v[2 * M2];
