@@ -21,7 +21,8 @@ OBJDIR = os.path.join(ROOT, "_build", "obj")
 ARCH = "gfx950"
 
 SOURCES = ["abi.hip", "elementwise.hip", "router.hip", "gemv_ref.hip", "gemv_fast.hip", "moe.hip", "tiles.hip", "gemv_mfma.hip",
-           "gemv_persist.hip", "gemv_persist_m.hip", "gemv_mixed.hip", "prefill.hip", "lmhead.hip", "norm.hip", "moe_batched.hip"]
+           "gemv_persist.hip", "gemv_persist_m.hip", "gemv_mixed.hip", "prefill.hip", "lmhead.hip", "norm.hip", "moe_batched.hip",
+           "moe_persist.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

@@ -1,0 +1,476 @@
+// Persistent matrix-core MoE expert legs for the single-row decode step (tolerance mode):
+// routed slots only (no shared expert), topk <= 8, H = 2048 R (R <= 3), I = 2048.
+// Mirrors the expert half of decoder_block (tools/glm_model_q4k_ref.py:797-809) with
+// swiglu_expert (:702-708); the routing decision is route.hpp's (:663-699).
+//
+// Both legs run one workgroup per CU over a list of jobs, with the memory plan of the
+// persistent multi-row GEMV: the copy waves (12, and 13 in the gate/up leg) take turns copying
+// rounds of 8 rows x 1152 B (4 block pairs, nine direct-to-LDS loads of 64 lanes x 16 B,
+// chunk-major: 16-B chunk c of row r at 16 (8c + r)) into a ring of NS LDS slots, post each
+// round to an LDS counter once it has landed, and refill a slot once the four sets that read
+// it hold their weights in registers.  Compute
+// wave w = 4 gamma + p takes block pair p (a set: 8 rows x 2 blocks, one pass of 8 MFMAs) of
+// the rounds of group gamma; the last set of a job reduces the job.
+//
+// Gate/up (k_moe_gu_p): job = (slot s, rows i0 .. i0+7 of I); round q = 0 .. 2R-1 holds K
+// segment k = q % R of the gate rows (q < R) or the up rows (q >= R) of expert sel[s].  Group
+// gamma takes the rounds with k = gamma, so wave 4k + p always meets block pair 4k + p of x
+// and keeps that pair's operands in registers for the whole kernel.  Reduction per row: the
+// 4R pair sums in a fixed order, then h = bf16(silu(bf16(g)) * bf16(u)).  Every workgroup
+// routes from the router logits itself before its first weight copy; workgroup 0 publishes
+// the decision for the down leg and the caller.
+//
+// Down (k_moe_down_p): job = output rows d0 .. d0+7; round q = slot q (8 rows x 1152 B of
+// expert sel[q], all I = 2048 weights of the rows); group gamma takes the slots q = gamma
+// mod 3 and stages those slots' activation pairs h[q] in LDS.  Reduction per row: per slot
+// y_s = (s0 + s1) + (s2 + s3) over its pair sums, then the slot-ordered combine
+//     facc = f32(facc + f32(w_s * bf16(y_s)))   (tools/glm_model_q4k_ref.py:799-809),
+// y = bf16(facc), or bf16(resid + bf16(facc)) with the decoder block's residual.
+#include "common.hpp"
+#include "glm_act.hpp"
+#include "launch.hpp"
+#include "mfma_gemv.hpp"
+#include "persist.hpp"
+#include "route.hpp"
+
+namespace aipu {
+
+using namespace mg;
+using namespace pst;
+
+namespace {
+
+constexpr int kJR = 8;                        // rows per job tile
+constexpr int kLoads = 9;                     // direct-to-LDS loads per round
+constexpr uint32_t kRoundRow = 128u * kLoads; // bytes of a row per round (4 block pairs)
+constexpr uint32_t kSlot = kJR * kRoundRow;   // bytes of a round
+constexpr int kReaders = 4;                   // sets that read a round
+constexpr int kNCW = 12;                      // compute waves
+constexpr int kGroups = 3;                    // compute wave groups of 4
+constexpr int kMaxJobs = 8;                   // jobs per workgroup
+constexpr int kMaxSlots = 8;                  // routed slots
+constexpr int kMaxRJ = 8;                     // rounds per job
+constexpr int kRedJob = 256;                  // pair sums per job (floats)
+constexpr int kGuNp = 12;                     // pair-sum stride of a gate/up row (4R <= 12)
+
+// Copy wave c of CW: rounds u = c, c + CW, ... < U into slots u % NS, at most Q of its own
+// in flight.  Round u is issued once its slot is free (round u - NS read by its four readers)
+// and posted, in order among the wave's rounds, once Q - 1 later rounds of the wave are in
+// flight behind it.  With CW * Q < NS a landed round has time to be read before a copy wave
+// needs its slot.  While a slot is still being read, every round of the wave but the newest
+// is posted first, so no reader waits for a round that has landed; the round a copy wave
+// waits on is then never the other wave's unposted newest one (that would need NS = CW).
+template <int NS, int Q, int CW, class Issue>
+__device__ __forceinline__ void copy_rounds(int c, int U, uint32_t* s_cnt, uint32_t* s_read, Issue&& issue) {
+    static_assert(Q >= 2 && CW * Q <= NS && kLoads * (Q - 1) <= 63, "rounds in flight within vmcnt and the ring");
+    uint32_t cnt0 = lds_addr(s_cnt);
+    asm volatile("" : "+v"(cnt0));   // a runtime base (see lds_post)
+    const int nr = U > c ? (U - c + CW - 1) / CW : 0;   // this wave's rounds
+    int posted = 0;                                      // of this wave's rounds
+    for (int i = 0; i < nr; ++i) {
+        const int u = c + CW * i;
+        if (u >= NS && lds_poll(&s_read[u - NS]) < (uint32_t)kReaders) {
+            if (posted < i - 1) {
+                __builtin_amdgcn_s_waitcnt(wait_vm(kLoads));
+                while (posted < i - 1) lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted++));
+            }
+            spin_ge(&s_read[u - NS], (uint32_t)kReaders);
+        }
+        issue(u);
+        if (posted <= i - (Q - 1)) {
+            __builtin_amdgcn_s_waitcnt(wait_vm(kLoads * (Q - 1)));
+            while (posted <= i - (Q - 1)) lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted++));
+        }
+    }
+    const int left = nr - posted;   // the oldest of `left` unposted rounds has landed once kLoads * (left - 1) loads remain
+    static_for<0, Q - 1>([&](auto sI) {
+        constexpr int j = Q - 2 - decltype(sI)::value;
+        if (j < left) {
+            __builtin_amdgcn_s_waitcnt(wait_vm(kLoads * j));
+            lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted));
+            ++posted;
+        }
+    });
+}
+
+// Nine loads of round k of 8 rows (row stride rb) at `base` into the LDS slot `dst`.
+template <uint32_t POL>
+__device__ __forceinline__ void issue_round(const uint8_t* base, int nvalid, uint32_t rb, uint32_t k, uint8_t* dst,
+                                            int lane) {
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(base, (uint32_t)nvalid * rb);
+    const uint32_t off = (uint32_t)(lane & 7) * rb + 16u * (uint32_t)(lane >> 3) + kRoundRow * k;
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) lds_dma16<POL>(wr, dst + 1024u * j, off + 128u * j);
+}
+
+// The weights of one set (block pair pp of the round in slot address sl; lane 16g + n reads
+// the header and qs chunk g of block 2pp + h, row r) and the round counter, in one LDS batch:
+// a posted counter proves that the weights read after it (in DS order) had landed;
+// otherwise wait for the post and read again.
+__device__ __forceinline__ void set_weights(uint32_t sl, uint32_t cnt, int pp, int h, int r, int g, bool known,
+                                            u32x4_t& hv, u32x4_t& q0, u32x4_t& q1) {
+    const uint32_t oh = 288u * (uint32_t)pp + 144u * (uint32_t)h;
+    const uint32_t tl = sl + 16u * (uint32_t)r;
+    const uint32_t ah = tl + 8u * oh, aq = tl + 8u * (oh + 16u + 32u * (uint32_t)g);
+    uint32_t cv;
+    asm volatile(
+        "ds_read_b32 %3, %6\n\t"
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %5\n\t"
+        "ds_read_b128 %2, %5 offset:128\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(hv), "=&v"(q0), "=&v"(q1), "=&v"(cv)
+        : "v"(ah), "v"(aq), "v"(cnt)
+        : "memory");
+    if (!known && __builtin_amdgcn_readfirstlane(cv) < 1u) {
+        for (uint32_t it = 0; it < (1u << 22); ++it) {
+            uint32_t c;
+            asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(c) : "v"(cnt) : "memory");
+            if (__builtin_amdgcn_readfirstlane(c) >= 1u) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile(
+            "ds_read_b128 %0, %3\n\t"
+            "ds_read_b128 %1, %4\n\t"
+            "ds_read_b128 %2, %4 offset:128\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(hv), "=&v"(q0), "=&v"(q1)
+            : "v"(ah), "v"(aq)
+            : "memory");
+    }
+}
+
+// The block-diagonal operands of a staged pair (diagonal lanes 16g + 4g + h, h < 2; every
+// other lane keeps its zeros) and this lane's sub-block sums.
+__device__ __forceinline__ void pair_operands(uint32_t st, int g, int n, int h, u32x4_t (&A)[8], float2& as) {
+    const uint32_t aa = st + 32u * (uint32_t)g + 16u * (uint32_t)((n - 4 * g) & 1);
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %[sv], exec\n\t"
+        "s_and_b64 exec, exec, %[mask]\n\t"
+        "ds_read_b128 %[a0], %[aa]\n\t"
+        "ds_read_b128 %[a1], %[aa] offset:144\n\t"
+        "ds_read_b128 %[a2], %[aa] offset:288\n\t"
+        "ds_read_b128 %[a3], %[aa] offset:432\n\t"
+        "ds_read_b128 %[a4], %[aa] offset:576\n\t"
+        "ds_read_b128 %[a5], %[aa] offset:720\n\t"
+        "ds_read_b128 %[a6], %[aa] offset:864\n\t"
+        "ds_read_b128 %[a7], %[aa] offset:1008\n\t"
+        "s_mov_b64 exec, %[sv]\n\t"
+        "ds_read_b64 %[as], %[sa]\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : [a0] "+v"(A[0]), [a1] "+v"(A[1]), [a2] "+v"(A[2]), [a3] "+v"(A[3]), [a4] "+v"(A[4]), [a5] "+v"(A[5]),
+          [a6] "+v"(A[6]), [a7] "+v"(A[7]), [as] "=&v"(as), [sv] "=&s"(saved)
+        : [aa] "v"(aa), [mask] "s"(diag_mask(2)), [sa] "v"(st + kStgSums + 8u * (uint32_t)(g * 2 + h))
+        : "memory", "scc");   // s_and_b64 writes SCC
+}
+
+// One set: the pair sum (block 2pp + block 2pp + 1) of tile row r on lanes 0 .. 7.
+__device__ __forceinline__ float set_sum(const u32x4_t (&A)[8], float2 as, const u32x4_t& hv, const u32x4_t& q0,
+                                         const u32x4_t& q1, const HdrSel& hs, const CodeK& ck, int h) {
+    f32x4_t dlo, dhi;
+    dlo[0] = dlo[1] = -kCodeBiasF * as.x;
+    dhi[0] = dhi[1] = -kCodeBiasF * as.y;
+    dlo[2] = dlo[3] = dhi[2] = dhi[3] = 0.f;
+    const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+        dlo = mfma(A[tt], codes_lo(qd[2 * tt], qd[2 * tt + 1], ck), dlo);
+        dhi = mfma(A[4 + tt], codes_hi(qd[2 * tt], qd[2 * tt + 1], ck), dhi);
+    }
+    const Hdr H = hdr_decode(make_uint4(hv.x, hv.y, hv.z, hv.w), hs);
+    const float bt = block_sum(block_term(H, h ? dlo[1] : dlo[0], h ? dhi[1] : dhi[0], as.x, as.y));
+    const float b1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bt), 0x108, 0xF, 0xF, false));
+    return bt + b1;
+}
+
+// ------------------------------------------------------------------ gate/up
+template <int R, int NS, int Q, int CW, uint32_t POL>
+__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(const uint8_t* __restrict__ Gw,
+                                                            const uint8_t* __restrict__ Uw, int64_t ebytes,
+                                                            MoeRoute route, int E, int topk,
+                                                            const uint16_t* __restrict__ X, uint16_t* __restrict__ Hout,
+                                                            int I, int njobs) {
+    constexpr int RJ = 2 * R, np = 4 * R, nsb = 8 * R;
+    constexpr uint32_t rb = R * kRoundRow;
+    extern __shared__ __align__(16) uint8_t s_dyn[];   // ring | staged pairs
+    __shared__ float s_red[kMaxJobs * kRedJob];
+    __shared__ uint32_t s_cnt[kMaxJobs * kMaxRJ], s_read[kMaxJobs * kMaxRJ], s_done[kMaxJobs];
+    __shared__ __align__(16) uint32_t r_keys[kRouteMaxE];
+    __shared__ uint32_t r_win[kRouteMaxTopk];
+    __shared__ int32_t r_sel[kRouteMaxTopk];
+    __shared__ uint16_t r_selw[kRouteMaxTopk];
+    uint8_t* const s_ring = s_dyn;
+    uint8_t* const s_stage = s_dyn + NS * kSlot;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = blockIdx.x, G = gridDim.x;
+    const int T = (njobs - wg + G - 1) / G;   // <= kMaxJobs
+    const int it8 = I / kJR;
+    const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
+    const int gam = w >> 2, p = w & 3;
+    for (int i = tid; i < kMaxJobs * kMaxRJ; i += blockDim.x) s_cnt[i] = s_read[i] = 0u;
+    if (tid < kMaxJobs) s_done[tid] = 0u;
+
+    // this wave's activation pair goes out before the routing
+    uint4 xv = make_uint4(0u, 0u, 0u, 0u);
+    const int pr = 4 * gam + p;   // the wave's block pair of x
+    if (w < kNCW && pr < np) {
+        const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)nsb * 512u);
+        xv = buf_load16(xr, (uint32_t)pr * 1024u + 16u * (uint32_t)lane);
+    }
+    // routing decision (its barriers also publish the zeroed counters)
+    route_workgroup(route.logits, E, topk, route.scale_bits, r_keys, r_win, r_sel, r_selw, wg == 0);
+    if (wg == 0 && tid < topk) {
+        route.sel_pub[tid] = r_sel[tid];
+        route.selw_pub[tid] = r_selw[tid];
+        if (route.sel_api) route.sel_api[tid] = r_sel[tid];
+        if (route.selw_api) route.selw_api[tid] = r_selw[tid];
+    }
+
+    if (w >= kNCW) {
+        // ---- copy wave c: lane s holds slot s's expert
+        const int c = w - kNCW;
+        int ev = 0;
+        if (lane < topk) {
+            const int e = (int)(0xFFFFu - (r_win[lane] & 0xFFFFu));
+            ev = e < 0 ? 0 : (e >= E ? E - 1 : e);
+        }
+        // round u = job t * RJ + q; the job's slot js and row group ji advance with u
+        int q = c, js = wg / it8, ji = wg - js * it8;
+        const auto norm = [&]() {
+            while (q >= RJ) {
+                q -= RJ;
+                ji += G;
+                while (ji >= it8) {
+                    ji -= it8;
+                    ++js;
+                }
+            }
+        };
+        norm();
+        copy_rounds<NS, Q, CW>(c, T * RJ, s_cnt, s_read, [&](int u) {
+            const int64_t e = __builtin_amdgcn_readlane(ev, js);
+            const int half = q >= R ? 1 : 0, k = q - half * R;
+            const uint8_t* base = (half ? Uw : Gw) + e * ebytes + (int64_t)ji * kJR * rb;
+            issue_round<POL>(base, kJR, rb, (uint32_t)k, s_ring + (uint32_t)(u % NS) * kSlot, lane);
+            q += CW;
+            norm();
+        });
+        return;
+    }
+    if (pr >= np) return;
+
+    // ---- compute wave (gam, p): pair pr of x, operands in registers
+    uint8_t* const st = s_stage + (uint32_t)pr * kStgBytes;
+    stage_pair(xv, st, lane);
+    u32x4_t A[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) A[i] = u32x4_t{0u, 0u, 0u, 0u};
+    float2 as;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    pair_operands(lds_addr(st), g, n, h, A, as);
+    const HdrSel hs = hdr_sel(g);
+    const CodeK ck = code_k();
+    int seen = -1;
+    for (int t = 0; t < T; ++t) {
+        float* rt = s_red + t * kRedJob;   // [gate rows 0..7, up rows 8..15][pair]
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int u = t * RJ + half * R + gam;
+            u32x4_t hv, q0, q1;
+            set_weights(lds_addr(s_ring) + (uint32_t)(u % NS) * kSlot, lds_addr(&s_cnt[u]), p, h, r, g, seen >= u, hv,
+                        q0, q1);
+            seen = seen < u ? u : seen;
+            lds_post(&s_read[u]);   // the weights are in registers: one reader fewer
+            const float ps = set_sum(A, as, hv, q0, q1, hs, ck, h);
+            if (lane < kJR) rt[(half * kJR + lane) * kGuNp + pr] = ps;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
+        if (lds_add_rtn(&s_done[t]) != (uint32_t)np - 1u) continue;   // one post per wave and job
+        // the job's last set: lane 4 * row + k (rows 0..7 gate, 8..15 up) sums pairs k, k + 4, ...
+        const int row = lane >> 2, k = lane & 3;
+        float v = rt[row * kGuNp + k];
+#pragma unroll
+        for (int jj = k + 4; jj < np; jj += 4) v += rt[row * kGuNp + jj];
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // xor 1
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // xor 2
+        const float uvl = __shfl_xor(v, 32, 64);   // up row i sits 32 lanes above gate row i
+        const int j = wg + t * G;
+        const int s = j / it8, i0 = (j - s * it8) * kJR;
+        if (lane < 32 && k == 0) {
+            const uint32_t gb = bf16_rne(v), ub = bf16_rne(uvl);
+            Hout[(int64_t)s * I + i0 + row] = (uint16_t)bf16_rne(bf16_to_f32(glm_silu_bf16(gb)) * bf16_to_f32(ub));
+        }
+    }
+}
+
+// ------------------------------------------------------------------ down
+template <int NS, int Q, int CW, uint32_t POL>
+__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(const uint8_t* __restrict__ Dw, int64_t ebytes,
+                                                              const int32_t* __restrict__ sel,
+                                                              const uint16_t* __restrict__ selw, int E, int S,
+                                                              const uint16_t* __restrict__ Hin, int I, int64_t Hd,
+                                                              uint16_t* __restrict__ Y,
+                                                              const uint16_t* __restrict__ resid, int njobs) {
+    constexpr uint32_t rb = kRoundRow;   // I = 2048: one round per slot
+    extern __shared__ __align__(16) uint8_t s_dyn[];   // ring | staged pairs [slot][pair]
+    __shared__ float s_red[kMaxJobs * kRedJob];         // [job][slot][row][pair]
+    __shared__ uint32_t s_cnt[kMaxJobs * kMaxRJ], s_read[kMaxJobs * kMaxRJ], s_done[kMaxJobs];
+    uint8_t* const s_ring = s_dyn;
+    uint8_t* const s_stage = s_dyn + NS * kSlot;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = blockIdx.x, G = gridDim.x;
+    const int T = (njobs - wg + G - 1) / G;   // <= kMaxJobs
+    const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
+    const int gam = w >> 2, p = w & 3;
+    for (int i = tid; i < kMaxJobs * kMaxRJ; i += blockDim.x) s_cnt[i] = s_read[i] = 0u;
+    if (tid < kMaxJobs) s_done[tid] = 0u;
+
+    // the activation pairs of this wave's slots (q = gam, gam + 3, ...) go out first
+    constexpr int kMaxQ = (kMaxSlots + kGroups - 1) / kGroups;
+    uint4 xv[kMaxQ];
+    if (w < kNCW) {
+        const __amdgpu_buffer_rsrc_t hr = buf_rsrc(Hin, (uint32_t)S * (uint32_t)I * 2u);
+#pragma unroll
+        for (int i = 0; i < kMaxQ; ++i) {
+            const int q = gam + kGroups * i;
+            xv[i] = buf_load16(hr, q < S ? (uint32_t)q * (uint32_t)I * 2u + (uint32_t)p * 1024u + 16u * (uint32_t)lane : kOOB);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
+
+    if (w >= kNCW) {
+        // ---- copy wave c: lane s holds slot s's expert; round u = job t * S + slot q
+        const int c = w - kNCW;
+        const int ev = lane < S ? (sel[lane] < 0 ? 0 : (sel[lane] >= E ? E - 1 : sel[lane])) : 0;
+        int q = c;
+        int64_t d0 = (int64_t)wg * kJR;
+        const auto norm = [&]() {
+            while (q >= S) {
+                q -= S;
+                d0 += (int64_t)G * kJR;
+            }
+        };
+        norm();
+        copy_rounds<NS, Q, CW>(c, T * S, s_cnt, s_read, [&](int u) {
+            const int nvalid = (int)(Hd - d0 < kJR ? Hd - d0 : kJR);
+            const int64_t e = __builtin_amdgcn_readlane(ev, q);
+            issue_round<POL>(Dw + e * ebytes + d0 * (int64_t)rb, nvalid, rb, 0u, s_ring + (uint32_t)(u % NS) * kSlot,
+                             lane);
+            q += CW;
+            norm();
+        });
+        return;
+    }
+
+    // ---- compute wave (gam, p): pair p of slots gam, gam + 3, ...
+#pragma unroll
+    for (int i = 0; i < kMaxQ; ++i) {
+        const int q = gam + kGroups * i;
+        if (q < S) stage_pair(xv[i], s_stage + (uint32_t)(4 * q + p) * kStgBytes, lane);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const HdrSel hs = hdr_sel(g);
+    const CodeK ck = code_k();
+    u32x4_t A[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) A[i] = u32x4_t{0u, 0u, 0u, 0u};
+    int seen = -1;
+    for (int t = 0; t < T; ++t) {
+        float* rt = s_red + t * kRedJob;
+        for (int q = gam; q < S; q += kGroups) {
+            const int u = t * S + q;
+            u32x4_t hv, q0, q1;
+            set_weights(lds_addr(s_ring) + (uint32_t)(u % NS) * kSlot, lds_addr(&s_cnt[u]), p, h, r, g, seen >= u, hv,
+                        q0, q1);
+            seen = seen < u ? u : seen;
+            lds_post(&s_read[u]);   // the weights are in registers: one reader fewer
+            float2 as;
+            pair_operands(lds_addr(s_stage) + (uint32_t)(4 * q + p) * kStgBytes, g, n, h, A, as);
+            const float ps = set_sum(A, as, hv, q0, q1, hs, ck, h);
+            if (lane < kJR) rt[(q * kJR + lane) * 4 + p] = ps;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
+        // every wave posts once per slot it took
+        const int mine = (S - gam + kGroups - 1) / kGroups;
+        uint32_t before = 0;
+        for (int i = 0; i < mine; ++i) before = lds_add_rtn(&s_done[t]);
+        if (mine == 0 || before != (uint32_t)(4 * S) - 1u) continue;
+        // the job's last set: lane 8 * row + slot
+        const int row = lane >> 3, s = lane & 7;
+        float pw = 0.f;
+        if (s < S) {
+            const float* qp = rt + (s * kJR + row) * 4;
+            const float ys = (qp[0] + qp[1]) + (qp[2] + qp[3]);
+            pw = bf16_to_f32(selw[s]) * bf16_to_f32(bf16_rne(ys));
+        }
+        float facc = 0.f;
+        for (int s2 = 0; s2 < S; ++s2) facc = facc + __shfl(pw, (lane & ~7) + s2, 64);
+        const int64_t d = (int64_t)(wg + t * G) * kJR + row;
+        if (s == 0 && d < Hd) {
+            uint32_t yb = bf16_rne(facc);
+            if (resid) yb = bf16_rne(bf16_to_f32(resid[d]) + bf16_to_f32(yb));
+            Y[d] = (uint16_t)yb;
+        }
+    }
+}
+
+// Ring slots, rounds in flight per copy wave, copy waves (measured: 1 or 2 copy waves, 4 to 7
+// rounds each, are within 1 us of each other; these were the fastest).  The ring takes more
+// than half the CU's LDS, so the workgroups spread one per CU.
+constexpr int kGuNS = 12, kGuQ = 5, kGuCW = 2;
+constexpr int kDnNS = 12, kDnQ = 7, kDnCW = 1;
+
+size_t gu_lds(int R) { return (size_t)kGuNS * kSlot + (size_t)(4 * R) * kStgBytes; }
+size_t dn_lds(int S) { return (size_t)kDnNS * kSlot + (size_t)(4 * S) * kStgBytes; }
+
+}  // namespace
+
+bool moe_persist_supported(int64_t E, int topk, int nslots, int64_t H, int64_t I) {
+    if (nslots != topk || topk < 1 || topk > kMaxSlots || E < 1 || E > kRouteMaxE || topk > E) return false;
+    if (H % 2048 != 0 || H < 2048 || H > 6144 || I != 2048) return false;
+    if ((E + 7) / 8 * 8 > 64 * (kNCW + 1)) return false;   // in-kernel routing: one key per thread
+    const int64_t cus = device_cu_count();
+    const int64_t gu_jobs = (int64_t)topk * (I / kJR), dn_jobs = (H + kJR - 1) / kJR;
+    return gu_jobs <= kMaxJobs * cus && dn_jobs <= kMaxJobs * cus;
+}
+
+hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const MoeRoute& route, int topk, int64_t E,
+                                     int64_t H, int64_t I, const uint16_t* x, uint16_t* h, hipStream_t st) {
+    if (!moe_persist_supported(E, topk, topk, H, I) || !route.logits) return hipErrorInvalidValue;
+    const int R = (int)(H / 2048);
+    const int64_t rb = row_bytes(T_Q4_K, H);
+    const int njobs = (int)(topk * (I / kJR));
+    const int cus = device_cu_count();
+    const int tpw = (njobs + cus - 1) / cus;
+    const int G2 = (njobs + tpw - 1) / tpw;
+    const dim3 grid(G2), block(64 * (kNCW + kGuCW));
+#define AIPU_GU(RV)                                                                                              \
+    if (R == RV) {                                                                                               \
+        hipLaunchKernelGGL((k_moe_gu_p<RV, kGuNS, kGuQ, kGuCW, kNT>), grid, block, gu_lds(RV), st, G, U, rb * I, route, (int)E, topk, \
+                           x, h, (int)I, njobs);                                                                 \
+        return hipGetLastError();                                                                                \
+    }
+    AIPU_GU(1) AIPU_GU(2) AIPU_GU(3)
+#undef AIPU_GU
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_moe_down_persist(const uint8_t* D, const int32_t* sel, const uint16_t* selw, int topk, int64_t E,
+                                   int64_t H, int64_t I, const uint16_t* h, uint16_t* y, const uint16_t* resid,
+                                   hipStream_t st) {
+    if (!moe_persist_supported(E, topk, topk, H, I)) return hipErrorInvalidValue;
+    const int64_t rb = row_bytes(T_Q4_K, I);
+    const int njobs = (int)((H + kJR - 1) / kJR);
+    const int cus = device_cu_count();
+    const int tpw = (njobs + cus - 1) / cus;
+    const int G2 = (njobs + tpw - 1) / tpw;
+    hipLaunchKernelGGL((k_moe_down_p<kDnNS, kDnQ, kDnCW, 0>), dim3(G2), dim3(64 * (kNCW + kDnCW)), dn_lds(topk), st, D, rb * H, sel,
+                       selw, (int)E, topk, h, (int)I, H, y, resid, njobs);
+    return hipGetLastError();
+}
+
+}  // namespace aipu
