@@ -4,10 +4,10 @@
 // Workgroup.  One workgroup per CU owns tiles wg, wg + G, wg + 2G.  Wave NCW copies them into
 // a ring of LDS round slots with direct-to-LDS buffer loads: a round is 9 loads of 64 lanes x
 // 16 B = 1152 bytes of each of the tile's 8 rows (block pairs 4k .. 4k+3), laid out chunk-
-// major (16-byte chunk c of row r at 16 (8c + r)), up to four rounds in flight, each posted
-// to an LDS counter once its loads have landed.  A slot is refilled once the 4 sets that read its round
-// hold their weights in registers.  The copy schedule is a runtime loop with one fixed vmcnt
-// wait, so the wave's code stays small.
+// major (16-byte chunk c of row r at 16 (8c + r)), up to four rounds in flight in four slots,
+// each posted to an LDS counter once its loads have landed.  A slot is refilled once the 4 sets that read its round hold their weights in
+// registers.  The copy schedule is a runtime loop with fixed vmcnt waits, so the wave's code
+// stays small.
 //
 // Compute wave w owns block pair w (np = 4R waves).  It stages pair w of every activation row
 // in LDS, and for every tile builds the pair's codes once (8 rows x 2 blocks) and runs them
@@ -37,8 +37,12 @@ constexpr int kLoads = 9;        // direct-to-LDS loads per round
 constexpr uint32_t kRoundRow = 128u * kLoads;   // bytes of a row per round (4 block pairs)
 constexpr uint32_t kSlot = kTR8 * kRoundRow;    // bytes of a round
 constexpr uint32_t kStg = kStgBytes;   // staged pair: operand entries + 16 sub-block sums
-constexpr int kNS = 4;           // round slots
 constexpr int kReaders = 4;      // sets that read a round
+// Round slots and rounds in flight.  Deeper rings (up to 12 slots with 7 rounds in flight
+// where the staged rows leave room) measured no faster here: the sets, not the copies, bound
+// these launches.
+__host__ __device__ constexpr int ring_slots(int) { return 4; }
+__host__ __device__ constexpr int ring_depth(int) { return 4; }
 
 // A operands of a set for two activation rows (A: MFMAs t = 0..3 from entries t, B: entries
 // 4 + t), the rows staged at st0 on lanes 16g + 4g + h and st1 on lanes 16g + 4g + 2 + h; every
@@ -79,11 +83,11 @@ __global__ __launch_bounds__(64 * (4 * 3 + 1)) void k_gemvmp(const uint8_t* __re
     constexpr int np = 4 * R, nsb = 8 * R;
     constexpr uint32_t rb = R * kRoundRow;
     constexpr int NCW = np;
-    static_assert(kLoads * (kNS - 1) <= 63, "rounds in flight within vmcnt");
+    constexpr int NS = ring_slots(M2), Q = ring_depth(M2);
     extern __shared__ __align__(16) uint8_t s_dyn[];   // ring | staged rows | pair sums
     __shared__ uint32_t s_cnt[kMaxTT * R], s_read[kMaxTT * R], s_done[kMaxTT];
     uint8_t* const s_ring = s_dyn;
-    uint8_t* const s_stage = s_dyn + kNS * kSlot;                             // [pair][row] kStg each
+    uint8_t* const s_stage = s_dyn + NS * kSlot;                             // [pair][row] kStg each
     float* const s_red = (float*)(s_stage + (uint32_t)np * 2 * M2 * kStg);    // [t][row m][tile row][pair]
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -92,13 +96,13 @@ __global__ __launch_bounds__(64 * (4 * 3 + 1)) void k_gemvmp(const uint8_t* __re
     const int U = T * R;                        // rounds of this workgroup
     const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
     const uint32_t loff = (uint32_t)(lane & 7) * rb + 16u * (uint32_t)(lane >> 3);
-    // round u: 9 loads of 128 B of each tile row into slot u % kNS
+    // round u: 9 loads of 128 B of each tile row into slot u % NS
     auto issue = [&](int u) {
         const int t = u / R, k = u - t * R;
         const int64_t r0 = (int64_t)(wg + t * G) * kTR8;
         const int nvalid = (int)(N - r0 < kTR8 ? N - r0 : kTR8);
         const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W + r0 * (int64_t)rb, (uint32_t)nvalid * rb);
-        uint8_t* dst = s_ring + (uint32_t)(u % kNS) * kSlot;
+        uint8_t* dst = s_ring + (uint32_t)(u % NS) * kSlot;
         const uint32_t off = loff + kRoundRow * (uint32_t)k;
 #pragma unroll
         for (int j = 0; j < kLoads; ++j) lds_dma16<kNT>(wr, dst + 1024u * j, off + 128u * j);
@@ -109,37 +113,7 @@ __global__ __launch_bounds__(64 * (4 * 3 + 1)) void k_gemvmp(const uint8_t* __re
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
 
     if (w == NCW) {
-        // ---- copy wave
-        uint32_t cnt0 = lds_addr(s_cnt);
-        asm volatile("" : "+v"(cnt0));   // a runtime base (see lds_post)
-        // Round u is issued once its slot is free (round u - kNS read by its four readers) and
-        // posted, in order, once kNS - 1 later rounds are in flight behind it.  While a slot is
-        // still being read, every round but the newest is posted first, so no reader waits for
-        // a round that has landed.
-        int posted = 0;
-        for (int u = 0; u < U; ++u) {
-            if (u >= kNS && lds_poll(&s_read[u - kNS]) < (uint32_t)kReaders) {
-                if (posted < u - 1) {
-                    __builtin_amdgcn_s_waitcnt(wait_vm(kLoads));
-                    while (posted < u - 1) lds_post(cnt0 + 4u * (uint32_t)posted++);
-                }
-                spin_ge(&s_read[u - kNS], (uint32_t)kReaders);
-            }
-            issue(u);
-            if (posted <= u - (kNS - 1)) {
-                __builtin_amdgcn_s_waitcnt(wait_vm(kLoads * (kNS - 1)));
-                while (posted <= u - (kNS - 1)) lds_post(cnt0 + 4u * (uint32_t)posted++);
-            }
-        }
-        const int left = U - posted;   // the oldest of `left` unposted rounds has landed once kLoads * (left - 1) loads remain
-        static_for<0, kNS - 1>([&](auto sI) {
-            constexpr int j = kNS - 2 - decltype(sI)::value;
-            if (j < left) {
-                __builtin_amdgcn_s_waitcnt(wait_vm(kLoads * j));
-                lds_post(cnt0 + 4u * (uint32_t)posted);
-                ++posted;
-            }
-        });
+        copy_ring<NS, Q, 1, kLoads, kReaders>(0, U, s_cnt, s_read, issue);   // ---- copy wave
         return;
     }
 
@@ -166,7 +140,7 @@ __global__ __launch_bounds__(64 * (4 * 3 + 1)) void k_gemvmp(const uint8_t* __re
     for (int t = 0; t < T; ++t) {
         const int u = t * R + (p >> 2);
         const uint32_t oh = 288u * (uint32_t)(p & 3) + 144u * (uint32_t)h;   // header of block 2p + h, within the round
-        const uint32_t tl = lds_addr(s_ring) + (uint32_t)(u % kNS) * kSlot + 16u * (uint32_t)r;
+        const uint32_t tl = lds_addr(s_ring) + (uint32_t)(u % NS) * kSlot + 16u * (uint32_t)r;
         const uint32_t ah = tl + 8u * oh, aq = tl + 8u * (oh + 16u + 32u * (uint32_t)g);
         u32x4_t hv, q0, q1;
         uint32_t cv;
@@ -285,7 +259,7 @@ int cus_m() {
 }
 
 size_t lds_bytes(int R, int M2) {
-    return (size_t)kNS * kSlot + (size_t)(4 * R) * 2 * M2 * kStg + (size_t)kMaxTT * kMaxRows * kTR8 * kMaxNp * 4;
+    return (size_t)ring_slots(M2) * kSlot + (size_t)(4 * R) * 2 * M2 * kStg + (size_t)kMaxTT * kMaxRows * kTR8 * kMaxNp * 4;
 }
 
 template <int R, int M2>

@@ -53,46 +53,6 @@ constexpr int kMaxRJ = 8;                     // rounds per job
 constexpr int kRedJob = 256;                  // pair sums per job (floats)
 constexpr int kGuNp = 12;                     // pair-sum stride of a gate/up row (4R <= 12)
 
-// Copy wave c of CW: rounds u = c, c + CW, ... < U into slots u % NS, at most Q of its own
-// in flight.  Round u is issued once its slot is free (round u - NS read by its four readers)
-// and posted, in order among the wave's rounds, once Q - 1 later rounds of the wave are in
-// flight behind it.  With CW * Q < NS a landed round has time to be read before a copy wave
-// needs its slot.  While a slot is still being read, every round of the wave but the newest
-// is posted first, so no reader waits for a round that has landed; the round a copy wave
-// waits on is then never the other wave's unposted newest one (that would need NS = CW).
-template <int NS, int Q, int CW, class Issue>
-__device__ __forceinline__ void copy_rounds(int c, int U, uint32_t* s_cnt, uint32_t* s_read, Issue&& issue) {
-    static_assert(Q >= 2 && CW * Q <= NS && kLoads * (Q - 1) <= 63, "rounds in flight within vmcnt and the ring");
-    uint32_t cnt0 = lds_addr(s_cnt);
-    asm volatile("" : "+v"(cnt0));   // a runtime base (see lds_post)
-    const int nr = U > c ? (U - c + CW - 1) / CW : 0;   // this wave's rounds
-    int posted = 0;                                      // of this wave's rounds
-    for (int i = 0; i < nr; ++i) {
-        const int u = c + CW * i;
-        if (u >= NS && lds_poll(&s_read[u - NS]) < (uint32_t)kReaders) {
-            if (posted < i - 1) {
-                __builtin_amdgcn_s_waitcnt(wait_vm(kLoads));
-                while (posted < i - 1) lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted++));
-            }
-            spin_ge(&s_read[u - NS], (uint32_t)kReaders);
-        }
-        issue(u);
-        if (posted <= i - (Q - 1)) {
-            __builtin_amdgcn_s_waitcnt(wait_vm(kLoads * (Q - 1)));
-            while (posted <= i - (Q - 1)) lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted++));
-        }
-    }
-    const int left = nr - posted;   // the oldest of `left` unposted rounds has landed once kLoads * (left - 1) loads remain
-    static_for<0, Q - 1>([&](auto sI) {
-        constexpr int j = Q - 2 - decltype(sI)::value;
-        if (j < left) {
-            __builtin_amdgcn_s_waitcnt(wait_vm(kLoads * j));
-            lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted));
-            ++posted;
-        }
-    });
-}
-
 // Nine loads of round k of 8 rows (row stride rb) at `base` into the LDS slot `dst`.
 template <uint32_t POL>
 __device__ __forceinline__ void issue_round(const uint8_t* base, int nvalid, uint32_t rb, uint32_t k, uint8_t* dst,
@@ -249,7 +209,7 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(const uint8_t* __
             }
         };
         norm();
-        copy_rounds<NS, Q, CW>(c, T * RJ, s_cnt, s_read, [&](int u) {
+        copy_ring<NS, Q, CW, kLoads, kReaders>(c, T * RJ, s_cnt, s_read, [&](int u) {
             const int64_t e = __builtin_amdgcn_readlane(ev, js);
             const int half = q >= R ? 1 : 0, k = q - half * R;
             const uint8_t* base = (half ? Uw : Gw) + e * ebytes + (int64_t)ji * kJR * rb;
@@ -355,7 +315,7 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(const uint8_t* 
             }
         };
         norm();
-        copy_rounds<NS, Q, CW>(c, T * S, s_cnt, s_read, [&](int u) {
+        copy_ring<NS, Q, CW, kLoads, kReaders>(c, T * S, s_cnt, s_read, [&](int u) {
             const int nvalid = (int)(Hd - d0 < kJR ? Hd - d0 : kJR);
             const int64_t e = __builtin_amdgcn_readlane(ev, q);
             issue_round<POL>(Dw + e * ebytes + d0 * (int64_t)rb, nvalid, rb, 0u, s_ring + (uint32_t)(u % NS) * kSlot,

@@ -1,6 +1,7 @@
-// Helpers of the persistent matrix-core GEMV (gemv_persist.hip): LDS
-// counters that waves post and poll, the compile-time loop that unrolls the copy schedule,
-// and the LDS row pitch of a copied tile.
+// Helpers of the persistent matrix-core kernels (gemv_persist.hip, gemv_persist_m.hip,
+// moe_persist.hip): LDS counters that waves post and poll, the compile-time loop that unrolls
+// a copy schedule, the LDS row pitch of a copied tile, the activation-pair staging, and the
+// copy loop of a ring of round slots.
 #pragma once
 
 #include "common.hpp"
@@ -82,5 +83,46 @@ __device__ __forceinline__ uint32_t lds_poll(const uint32_t* c) {
 __device__ __forceinline__ void spin_ge(const uint32_t* c, uint32_t v) {
     for (uint32_t it = 0; lds_poll(c) < v && it < (1u << 22); ++it) __builtin_amdgcn_s_sleep(1);
 }
+
+// Copy wave c of CW: rounds u = c, c + CW, ... < U (LOADS loads each) into slots u % NS, at
+// most Q of its own in flight.  Round u is issued once its slot is free (round u - NS read by
+// its READERS readers) and posted, in order among the wave's rounds, once Q - 1 later rounds
+// of the wave are in flight behind it.  With CW * Q < NS a landed round has time to be read before a copy wave
+// needs its slot.  While a slot is still being read, every round of the wave but the newest
+// is posted first, so no reader waits for a round that has landed; the round a copy wave
+// waits on is then never the other wave's unposted newest one (that would need NS = CW).
+template <int NS, int Q, int CW, int LOADS, int READERS, class Issue>
+__device__ __forceinline__ void copy_ring(int c, int U, uint32_t* s_cnt, uint32_t* s_read, Issue&& issue) {
+    static_assert(Q >= 2 && CW * Q <= NS && LOADS * (Q - 1) <= 63, "rounds in flight within vmcnt and the ring");
+    uint32_t cnt0 = lds_addr(s_cnt);
+    asm volatile("" : "+v"(cnt0));   // a runtime base (see lds_post)
+    const int nr = U > c ? (U - c + CW - 1) / CW : 0;   // this wave's rounds
+    int posted = 0;                                      // of this wave's rounds
+    for (int i = 0; i < nr; ++i) {
+        const int u = c + CW * i;
+        if (u >= NS && lds_poll(&s_read[u - NS]) < (uint32_t)READERS) {
+            if (posted < i - 1) {
+                __builtin_amdgcn_s_waitcnt(mg::wait_vm(LOADS));
+                while (posted < i - 1) lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted++));
+            }
+            spin_ge(&s_read[u - NS], (uint32_t)READERS);
+        }
+        issue(u);
+        if (posted <= i - (Q - 1)) {
+            __builtin_amdgcn_s_waitcnt(mg::wait_vm(LOADS * (Q - 1)));
+            while (posted <= i - (Q - 1)) lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted++));
+        }
+    }
+    const int left = nr - posted;   // the oldest of `left` unposted rounds has landed once LOADS * (left - 1) loads remain
+    static_for<0, Q - 1>([&](auto sI) {
+        constexpr int j = Q - 2 - decltype(sI)::value;
+        if (j < left) {
+            __builtin_amdgcn_s_waitcnt(mg::wait_vm(LOADS * j));
+            lds_post(cnt0 + 4u * (uint32_t)(c + CW * posted));
+            ++posted;
+        }
+    });
+}
+
 }  // namespace pst
 }  // namespace aipu
