@@ -144,110 +144,101 @@ __device__ __forceinline__ float set_sum(const u32x4_t (&A)[8], float2 as, const
     return bt + b1;
 }
 
-// ------------------------------------------------------------------ gate/up
-template <int R, int NS, int Q, int CW, uint32_t POL>
-__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(const uint8_t* __restrict__ Gw,
-                                                            const uint8_t* __restrict__ Uw, int64_t ebytes,
-                                                            MoeRoute route, int E, int topk,
-                                                            const uint16_t* __restrict__ X, uint16_t* __restrict__ Hout,
-                                                            int I, int njobs) {
-    constexpr int RJ = 2 * R, np = 4 * R, nsb = 8 * R;
-    constexpr uint32_t rb = R * kRoundRow;
-    extern __shared__ __align__(16) uint8_t s_dyn[];   // ring | staged pairs
-    __shared__ float s_red[kMaxJobs * kRedJob];
-    __shared__ uint32_t s_cnt[kMaxJobs * kMaxRJ], s_read[kMaxJobs * kMaxRJ], s_done[kMaxJobs];
-    __shared__ __align__(16) uint32_t r_keys[kRouteMaxE];
-    __shared__ uint32_t r_win[kRouteMaxTopk];
-    __shared__ int32_t r_sel[kRouteMaxTopk];
-    __shared__ uint16_t r_selw[kRouteMaxTopk];
-    uint8_t* const s_ring = s_dyn;
-    uint8_t* const s_stage = s_dyn + NS * kSlot;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wg = blockIdx.x, G = gridDim.x;
-    const int T = (njobs - wg + G - 1) / G;   // <= kMaxJobs
-    const int it8 = I / kJR;
-    const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
-    const int gam = w >> 2, p = w & 3;
-    for (int i = tid; i < kMaxJobs * kMaxRJ; i += blockDim.x) s_cnt[i] = s_read[i] = 0u;
-    if (tid < kMaxJobs) s_done[tid] = 0u;
+// ------------------------------------------------------------------ job loops
+// LDS of a workgroup's ring: slots, per-round landed / read counters, per-job set counters,
+// per-job pair sums.
+struct Ring {
+    uint8_t* slots;
+    uint32_t *cnt, *read, *done;
+    float* red;
+};
 
-    // this wave's activation pair goes out before the routing
-    uint4 xv = make_uint4(0u, 0u, 0u, 0u);
-    const int pr = 4 * gam + p;   // the wave's block pair of x
-    if (w < kNCW && pr < np) {
-        const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)nsb * 512u);
-        xv = buf_load16(xr, (uint32_t)pr * 1024u + 16u * (uint32_t)lane);
+// Copy-wave cursor over the gate/up rounds: round q (0 .. 2R-1) of the job of slot js and row
+// group ji (rows 8 ji .. 8 ji + 7 of I); jobs wg, wg + G, ... in order.
+struct GuCursor {
+    int q, js, ji;
+    __device__ void start(int q0, int wg, int it8, int RJ, int G) {
+        q = q0;
+        js = wg / it8;
+        ji = wg - js * it8;
+        advance(0, it8, RJ, G);
     }
-    // routing decision (its barriers also publish the zeroed counters)
-    route_workgroup(route.logits, E, topk, route.scale_bits, r_keys, r_win, r_sel, r_selw, wg == 0);
-    if (wg == 0 && tid < topk) {
-        route.sel_pub[tid] = r_sel[tid];
-        route.selw_pub[tid] = r_selw[tid];
-        if (route.sel_api) route.sel_api[tid] = r_sel[tid];
-        if (route.selw_api) route.selw_api[tid] = r_selw[tid];
-    }
-
-    if (w >= kNCW) {
-        // ---- copy wave c: lane s holds slot s's expert
-        const int c = w - kNCW;
-        int ev = 0;
-        if (lane < topk) {
-            const int e = (int)(0xFFFFu - (r_win[lane] & 0xFFFFu));
-            ev = e < 0 ? 0 : (e >= E ? E - 1 : e);
-        }
-        // round u = job t * RJ + q; the job's slot js and row group ji advance with u
-        int q = c, js = wg / it8, ji = wg - js * it8;
-        const auto norm = [&]() {
-            while (q >= RJ) {
-                q -= RJ;
-                ji += G;
-                while (ji >= it8) {
-                    ji -= it8;
-                    ++js;
-                }
+    __device__ void advance(int by, int it8, int RJ, int G) {
+        q += by;
+        while (q >= RJ) {
+            q -= RJ;
+            ji += G;
+            while (ji >= it8) {
+                ji -= it8;
+                ++js;
             }
-        };
-        norm();
-        copy_ring<NS, Q, CW, kLoads, kReaders>(c, T * RJ, s_cnt, s_read, [&](int u) {
-            const int64_t e = __builtin_amdgcn_readlane(ev, js);
-            const int half = q >= R ? 1 : 0, k = q - half * R;
-            const uint8_t* base = (half ? Uw : Gw) + e * ebytes + (int64_t)ji * kJR * rb;
-            issue_round<POL>(base, kJR, rb, (uint32_t)k, s_ring + (uint32_t)(u % NS) * kSlot, lane);
-            q += CW;
-            norm();
-        });
-        return;
+        }
     }
-    if (pr >= np) return;
+};
+template <int R, uint32_t POL>
+__device__ __forceinline__ void gu_issue(const GuCursor& cu, int ev, const uint8_t* Gw, const uint8_t* Uw,
+                                         int64_t ebytes, uint8_t* dst, int lane) {
+    constexpr uint32_t rb = R * kRoundRow;
+    const int64_t e = __builtin_amdgcn_readlane(ev, cu.js);
+    const int half = cu.q >= R ? 1 : 0, k = cu.q - half * R;
+    issue_round<POL>((half ? Uw : Gw) + e * ebytes + (int64_t)cu.ji * kJR * rb, kJR, rb, (uint32_t)k, dst, lane);
+}
 
-    // ---- compute wave (gam, p): pair pr of x, operands in registers
-    uint8_t* const st = s_stage + (uint32_t)pr * kStgBytes;
-    stage_pair(xv, st, lane);
-    u32x4_t A[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) A[i] = u32x4_t{0u, 0u, 0u, 0u};
-    float2 as;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    pair_operands(lds_addr(st), g, n, h, A, as);
-    const HdrSel hs = hdr_sel(g);
-    const CodeK ck = code_k();
-    int seen = -1;
+// Copy-wave cursor over the down rounds: slot q of the job of output rows d0 .. d0 + 7.
+struct DnCursor {
+    int q;
+    int64_t d0;
+    __device__ void start(int i, int S, int wg, int G) {   // i-th down round of the workgroup
+        q = i % S;
+        d0 = (int64_t)(wg + (i / S) * G) * kJR;
+    }
+    __device__ void advance(int by, int S, int G) {
+        q += by;
+        while (q >= S) {
+            q -= S;
+            d0 += (int64_t)G * kJR;
+        }
+    }
+};
+template <uint32_t POL>
+__device__ __forceinline__ void dn_issue(const DnCursor& cu, int ev, const uint8_t* Dw, int64_t ebytes, int64_t Hd,
+                                         uint8_t* dst, int lane) {
+    const int nvalid = (int)(Hd - cu.d0 < kJR ? Hd - cu.d0 : kJR);
+    const int64_t e = __builtin_amdgcn_readlane(ev, cu.q);
+    issue_round<POL>(Dw + e * ebytes + cu.d0 * (int64_t)kRoundRow, nvalid, kRoundRow, 0u, dst, lane);
+}
+
+// Lane s < topk: slot s's expert from the winners' keys.
+__device__ __forceinline__ int slot_experts(const uint32_t* win, int topk, int E, int lane) {
+    if (lane >= topk) return 0;
+    const int e = (int)(0xFFFFu - (win[lane] & 0xFFFFu));
+    return e < 0 ? 0 : (e >= E ? E - 1 : e);
+}
+
+// Gate/up jobs of compute wave (gam, p), which holds block pair pr = 4 gam + p of x in A / as:
+// job t's rounds are u0 + 2R t + half R + gam; the job's last set forms its 8 h values.
+template <int R, int NS>
+__device__ __forceinline__ void gu_jobs(const Ring& rg, int T, int u0, int wg, int G, int it8, int I, int gam, int p,
+                                        const u32x4_t (&A)[8], float2 as, const HdrSel& hs, const CodeK& ck,
+                                        int& seen, uint16_t* __restrict__ Hout, int lane) {
+    constexpr int RJ = 2 * R, np = 4 * R;
+    const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
+    const int pr = 4 * gam + p;
     for (int t = 0; t < T; ++t) {
-        float* rt = s_red + t * kRedJob;   // [gate rows 0..7, up rows 8..15][pair]
+        float* rt = rg.red + t * kRedJob;   // [gate rows 0..7, up rows 8..15][pair]
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-            const int u = t * RJ + half * R + gam;
+            const int u = u0 + t * RJ + half * R + gam;
             u32x4_t hv, q0, q1;
-            set_weights(lds_addr(s_ring) + (uint32_t)(u % NS) * kSlot, lds_addr(&s_cnt[u]), p, h, r, g, seen >= u, hv,
-                        q0, q1);
+            set_weights(lds_addr(rg.slots) + (uint32_t)(u % NS) * kSlot, lds_addr(&rg.cnt[u]), p, h, r, g, seen >= u,
+                        hv, q0, q1);
             seen = seen < u ? u : seen;
-            lds_post(&s_read[u]);   // the weights are in registers: one reader fewer
+            lds_post(&rg.read[u]);   // the weights are in registers: one reader fewer
             const float ps = set_sum(A, as, hv, q0, q1, hs, ck, h);
             if (lane < kJR) rt[(half * kJR + lane) * kGuNp + pr] = ps;
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
-        if (lds_add_rtn(&s_done[t]) != (uint32_t)np - 1u) continue;   // one post per wave and job
+        if (lds_add_rtn(&rg.done[t]) != (uint32_t)np - 1u) continue;   // one post per wave and job
         // the job's last set: lane 4 * row + k (rows 0..7 gate, 8..15 up) sums pairs k, k + 4, ...
         const int row = lane >> 2, k = lane & 3;
         float v = rt[row * kGuNp + k];
@@ -265,99 +256,36 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(const uint8_t* __
     }
 }
 
-// ------------------------------------------------------------------ down
-template <int NS, int Q, int CW, uint32_t POL>
-__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(const uint8_t* __restrict__ Dw, int64_t ebytes,
-                                                              const int32_t* __restrict__ sel,
-                                                              const uint16_t* __restrict__ selw, int E, int S,
-                                                              const uint16_t* __restrict__ Hin, int I, int64_t Hd,
-                                                              uint16_t* __restrict__ Y,
-                                                              const uint16_t* __restrict__ resid, int njobs) {
-    constexpr uint32_t rb = kRoundRow;   // I = 2048: one round per slot
-    extern __shared__ __align__(16) uint8_t s_dyn[];   // ring | staged pairs [slot][pair]
-    __shared__ float s_red[kMaxJobs * kRedJob];         // [job][slot][row][pair]
-    __shared__ uint32_t s_cnt[kMaxJobs * kMaxRJ], s_read[kMaxJobs * kMaxRJ], s_done[kMaxJobs];
-    uint8_t* const s_ring = s_dyn;
-    uint8_t* const s_stage = s_dyn + NS * kSlot;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wg = blockIdx.x, G = gridDim.x;
-    const int T = (njobs - wg + G - 1) / G;   // <= kMaxJobs
+// Down jobs of compute wave (gam, p): slots q = gam, gam + 3, ... of job t are rounds
+// u0 + S t + q, against staged pair 4q + p; the job's last set combines the slots.
+template <int NS>
+__device__ __forceinline__ void dn_jobs(const Ring& rg, int T, int u0, int S, int wg, int G, int64_t Hd, int gam, int p,
+                                        uint32_t stage, const HdrSel& hs, const CodeK& ck, int& seen,
+                                        const uint16_t* selw, uint16_t* __restrict__ Y,
+                                        const uint16_t* __restrict__ resid, int lane) {
     const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
-    const int gam = w >> 2, p = w & 3;
-    for (int i = tid; i < kMaxJobs * kMaxRJ; i += blockDim.x) s_cnt[i] = s_read[i] = 0u;
-    if (tid < kMaxJobs) s_done[tid] = 0u;
-
-    // the activation pairs of this wave's slots (q = gam, gam + 3, ...) go out first
-    constexpr int kMaxQ = (kMaxSlots + kGroups - 1) / kGroups;
-    uint4 xv[kMaxQ];
-    if (w < kNCW) {
-        const __amdgpu_buffer_rsrc_t hr = buf_rsrc(Hin, (uint32_t)S * (uint32_t)I * 2u);
-#pragma unroll
-        for (int i = 0; i < kMaxQ; ++i) {
-            const int q = gam + kGroups * i;
-            xv[i] = buf_load16(hr, q < S ? (uint32_t)q * (uint32_t)I * 2u + (uint32_t)p * 1024u + 16u * (uint32_t)lane : kOOB);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
-
-    if (w >= kNCW) {
-        // ---- copy wave c: lane s holds slot s's expert; round u = job t * S + slot q
-        const int c = w - kNCW;
-        const int ev = lane < S ? (sel[lane] < 0 ? 0 : (sel[lane] >= E ? E - 1 : sel[lane])) : 0;
-        int q = c;
-        int64_t d0 = (int64_t)wg * kJR;
-        const auto norm = [&]() {
-            while (q >= S) {
-                q -= S;
-                d0 += (int64_t)G * kJR;
-            }
-        };
-        norm();
-        copy_ring<NS, Q, CW, kLoads, kReaders>(c, T * S, s_cnt, s_read, [&](int u) {
-            const int nvalid = (int)(Hd - d0 < kJR ? Hd - d0 : kJR);
-            const int64_t e = __builtin_amdgcn_readlane(ev, q);
-            issue_round<POL>(Dw + e * ebytes + d0 * (int64_t)rb, nvalid, rb, 0u, s_ring + (uint32_t)(u % NS) * kSlot,
-                             lane);
-            q += CW;
-            norm();
-        });
-        return;
-    }
-
-    // ---- compute wave (gam, p): pair p of slots gam, gam + 3, ...
-#pragma unroll
-    for (int i = 0; i < kMaxQ; ++i) {
-        const int q = gam + kGroups * i;
-        if (q < S) stage_pair(xv[i], s_stage + (uint32_t)(4 * q + p) * kStgBytes, lane);
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const HdrSel hs = hdr_sel(g);
-    const CodeK ck = code_k();
     u32x4_t A[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) A[i] = u32x4_t{0u, 0u, 0u, 0u};
-    int seen = -1;
+    const int mine = gam < S ? (S - gam + kGroups - 1) / kGroups : 0;   // slots this wave takes
     for (int t = 0; t < T; ++t) {
-        float* rt = s_red + t * kRedJob;
+        float* rt = rg.red + t * kRedJob;   // [slot][row][pair]
         for (int q = gam; q < S; q += kGroups) {
-            const int u = t * S + q;
+            const int u = u0 + t * S + q;
             u32x4_t hv, q0, q1;
-            set_weights(lds_addr(s_ring) + (uint32_t)(u % NS) * kSlot, lds_addr(&s_cnt[u]), p, h, r, g, seen >= u, hv,
-                        q0, q1);
+            set_weights(lds_addr(rg.slots) + (uint32_t)(u % NS) * kSlot, lds_addr(&rg.cnt[u]), p, h, r, g, seen >= u,
+                        hv, q0, q1);
             seen = seen < u ? u : seen;
-            lds_post(&s_read[u]);   // the weights are in registers: one reader fewer
+            lds_post(&rg.read[u]);   // the weights are in registers: one reader fewer
             float2 as;
-            pair_operands(lds_addr(s_stage) + (uint32_t)(4 * q + p) * kStgBytes, g, n, h, A, as);
+            pair_operands(stage + (uint32_t)(4 * q + p) * kStgBytes, g, n, h, A, as);
             const float ps = set_sum(A, as, hv, q0, q1, hs, ck, h);
             if (lane < kJR) rt[(q * kJR + lane) * 4 + p] = ps;
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
-        // every wave posts once per slot it took
-        const int mine = (S - gam + kGroups - 1) / kGroups;
+        // one post per set; the wave whose post completes the job's 4S sets reduces it
         uint32_t before = 0;
-        for (int i = 0; i < mine; ++i) before = lds_add_rtn(&s_done[t]);
+        for (int i = 0; i < mine; ++i) before = lds_add_rtn(&rg.done[t]);
         if (mine == 0 || before != (uint32_t)(4 * S) - 1u) continue;
         // the job's last set: lane 8 * row + slot
         const int row = lane >> 3, s = lane & 7;
@@ -376,6 +304,139 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(const uint8_t* 
             Y[d] = (uint16_t)yb;
         }
     }
+}
+
+// Staging of the down activation pairs of compute wave (gam, p): pair p of h[q] for its slots.
+constexpr int kMaxQ = (kMaxSlots + kGroups - 1) / kGroups;
+__device__ __forceinline__ void dn_load_h(uint4 (&xv)[kMaxQ], const uint16_t* Hin, int S, int I, int gam, int p,
+                                          int lane) {
+    const __amdgpu_buffer_rsrc_t hr = buf_rsrc(Hin, (uint32_t)S * (uint32_t)I * 2u);
+#pragma unroll
+    for (int i = 0; i < kMaxQ; ++i) {
+        const int q = gam + kGroups * i;
+        xv[i] = buf_load16(hr, q < S ? (uint32_t)q * (uint32_t)I * 2u + (uint32_t)p * 1024u + 16u * (uint32_t)lane : kOOB);
+    }
+}
+__device__ __forceinline__ void dn_stage_h(const uint4 (&xv)[kMaxQ], uint8_t* s_stage, int S, int gam, int p, int lane) {
+#pragma unroll
+    for (int i = 0; i < kMaxQ; ++i) {
+        const int q = gam + kGroups * i;
+        if (q < S) stage_pair(xv[i], s_stage + (uint32_t)(4 * q + p) * kStgBytes, lane);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// x pair pr into registers: staged, then the diagonal operands and sums read back.
+__device__ __forceinline__ void x_operands(const uint4& xv, uint8_t* st, int lane, u32x4_t (&A)[8], float2& as) {
+    const int n = lane & 15, g = lane >> 4, h = n >> 3;
+    stage_pair(xv, st, lane);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) A[i] = u32x4_t{0u, 0u, 0u, 0u};
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    pair_operands(lds_addr(st), g, n, h, A, as);
+}
+
+// ------------------------------------------------------------------ gate/up
+template <int R, int NS, int Q, int CW, uint32_t POL>
+__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(const uint8_t* __restrict__ Gw,
+                                                            const uint8_t* __restrict__ Uw, int64_t ebytes,
+                                                            MoeRoute route, int E, int topk,
+                                                            const uint16_t* __restrict__ X, uint16_t* __restrict__ Hout,
+                                                            int I, int njobs) {
+    constexpr int RJ = 2 * R, np = 4 * R, nsb = 8 * R;
+    extern __shared__ __align__(16) uint8_t s_dyn[];   // ring | staged pairs
+    __shared__ float s_red[kMaxJobs * kRedJob];
+    __shared__ uint32_t s_cnt[kMaxJobs * kMaxRJ], s_read[kMaxJobs * kMaxRJ], s_done[kMaxJobs];
+    __shared__ __align__(16) uint32_t r_keys[kRouteMaxE];
+    __shared__ uint32_t r_win[kRouteMaxTopk];
+    __shared__ int32_t r_sel[kRouteMaxTopk];
+    __shared__ uint16_t r_selw[kRouteMaxTopk];
+    uint8_t* const s_stage = s_dyn + NS * kSlot;
+    const Ring rg{s_dyn, s_cnt, s_read, s_done, s_red};
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = blockIdx.x, G = gridDim.x;
+    const int T = (njobs - wg + G - 1) / G;   // <= kMaxJobs
+    const int it8 = I / kJR;
+    const int gam = w >> 2, p = w & 3, pr = 4 * gam + p;
+    for (int i = tid; i < kMaxJobs * kMaxRJ; i += blockDim.x) s_cnt[i] = s_read[i] = 0u;
+    if (tid < kMaxJobs) s_done[tid] = 0u;
+
+    // this wave's activation pair goes out before the routing
+    uint4 xv = make_uint4(0u, 0u, 0u, 0u);
+    if (w < kNCW && pr < np) xv = buf_load16(buf_rsrc(X, (uint32_t)nsb * 512u), (uint32_t)pr * 1024u + 16u * (uint32_t)lane);
+    // routing decision (its barriers also publish the zeroed counters)
+    route_workgroup(route.logits, E, topk, route.scale_bits, r_keys, r_win, r_sel, r_selw, wg == 0);
+    if (wg == 0 && tid < topk) {
+        route.sel_pub[tid] = r_sel[tid];
+        route.selw_pub[tid] = r_selw[tid];
+        if (route.sel_api) route.sel_api[tid] = r_sel[tid];
+        if (route.selw_api) route.selw_api[tid] = r_selw[tid];
+    }
+
+    if (w >= kNCW) {   // ---- copy wave c
+        const int c = w - kNCW;
+        const int ev = slot_experts(r_win, topk, E, lane);
+        GuCursor gc;
+        gc.start(c, wg, it8, RJ, G);
+        copy_ring<NS, Q, CW, kLoads, kReaders>(c, T * RJ, s_cnt, s_read, [&](int u) {
+            gu_issue<R, POL>(gc, ev, Gw, Uw, ebytes, s_dyn + (uint32_t)(u % NS) * kSlot, lane);
+            gc.advance(CW, it8, RJ, G);
+        });
+        return;
+    }
+    if (pr >= np) return;
+    // ---- compute wave (gam, p): pair pr of x, operands in registers
+    u32x4_t A[8];
+    float2 as;
+    x_operands(xv, s_stage + (uint32_t)pr * kStgBytes, lane, A, as);
+    int seen = -1;
+    gu_jobs<R, NS>(rg, T, 0, wg, G, it8, I, gam, p, A, as, hdr_sel(lane >> 4), code_k(), seen, Hout, lane);
+}
+
+// ------------------------------------------------------------------ down
+template <int NS, int Q, int CW, uint32_t POL>
+__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(const uint8_t* __restrict__ Dw, int64_t ebytes,
+                                                              const int32_t* __restrict__ sel,
+                                                              const uint16_t* __restrict__ selw, int E, int S,
+                                                              const uint16_t* __restrict__ Hin, int I, int64_t Hd,
+                                                              uint16_t* __restrict__ Y,
+                                                              const uint16_t* __restrict__ resid, int njobs) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];   // ring | staged pairs [slot][pair]
+    __shared__ float s_red[kMaxJobs * kRedJob];         // [job][slot][row][pair]
+    __shared__ uint32_t s_cnt[kMaxJobs * kMaxRJ], s_read[kMaxJobs * kMaxRJ], s_done[kMaxJobs];
+    uint8_t* const s_stage = s_dyn + NS * kSlot;
+    const Ring rg{s_dyn, s_cnt, s_read, s_done, s_red};
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = blockIdx.x, G = gridDim.x;
+    const int T = (njobs - wg + G - 1) / G;   // <= kMaxJobs
+    const int gam = w >> 2, p = w & 3;
+    for (int i = tid; i < kMaxJobs * kMaxRJ; i += blockDim.x) s_cnt[i] = s_read[i] = 0u;
+    if (tid < kMaxJobs) s_done[tid] = 0u;
+
+    // the activation pairs of this wave's slots go out first
+    uint4 xv[kMaxQ];
+    if (w < kNCW) dn_load_h(xv, Hin, S, I, gam, p, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
+
+    if (w >= kNCW) {   // ---- copy wave c: lane s holds slot s's expert
+        const int c = w - kNCW;
+        const int ev = lane < S ? (sel[lane] < 0 ? 0 : (sel[lane] >= E ? E - 1 : sel[lane])) : 0;
+        DnCursor dc;
+        dc.start(c, S, wg, G);
+        copy_ring<NS, Q, CW, kLoads, kReaders>(c, T * S, s_cnt, s_read, [&](int u) {
+            dn_issue<POL>(dc, ev, Dw, ebytes, Hd, s_dyn + (uint32_t)(u % NS) * kSlot, lane);
+            dc.advance(CW, S, G);
+        });
+        return;
+    }
+    // ---- compute wave (gam, p): pair p of slots gam, gam + 3, ...
+    dn_stage_h(xv, s_stage, S, gam, p, lane);
+    int seen = -1;
+    dn_jobs<NS>(rg, T, 0, S, wg, G, Hd, gam, p, lds_addr(s_stage), hdr_sel(lane >> 4), code_k(), seen, selw, Y, resid,
+                lane);
 }
 
 // Ring slots, rounds in flight per copy wave, copy waves (measured: 1 or 2 copy waves, 4 to 7

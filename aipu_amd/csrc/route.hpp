@@ -57,6 +57,49 @@ __device__ __forceinline__ void route_weights(const uint32_t* win, int topk, uin
     }
 }
 
+// bf16 router dot product of one row (the reference's logit linear, tools/glm_model_q4k_ref.py:663-668)
+// as the kRouterThreads threads of a router workgroup form it: thread t folds its 16-B chunks
+// c = 8t + 2048u (u = 0, 1, ...) into two fp32 partials (dwords 0, 2 into s0; 1, 3 into s1) in
+// increasing K and returns s0 + s1 summed over its wave (xor 32, 16, ..., 1); router_logit adds
+// the four waves' sums in wave order.  Every kernel that forms router logits uses this order.
+constexpr int kRouterThreads = 256;
+__device__ __forceinline__ float router_wave_dot(const uint16_t* row, const uint16_t* x, int64_t K, int t) {
+    float s0 = 0.f, s1 = 0.f;
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    // four chunks' loads are issued before any is used (K = 6144 is three chunks per thread)
+    constexpr int kU = 4;
+    for (int64_t c0 = (int64_t)t * 8; c0 < K; c0 += kU * kRouterThreads * 8) {
+        uint4 wv[kU], av[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t c = c0 + (int64_t)u * kRouterThreads * 8;
+            if (c < K) {
+                wv[u] = *(const uint4*)(row + c);
+                av[u] = *(const uint4*)(x + c);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t c = c0 + (int64_t)u * kRouterThreads * 8;
+            if (c >= K) break;
+            const uint4 w = wv[u], a = av[u];
+            s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.x), __builtin_bit_cast(bf2, w.x), s0, false);
+            s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.y), __builtin_bit_cast(bf2, w.y), s1, false);
+            s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.z), __builtin_bit_cast(bf2, w.z), s0, false);
+            s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w), __builtin_bit_cast(bf2, w.w), s1, false);
+        }
+    }
+    float v = s0 + s1;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float router_logit(const float* wsum) {
+    float tot = 0.f;
+    for (int w = 0; w < kRouterThreads / 64; ++w) tot += wsum[w];
+    return tot;
+}
+
 // The routing decision computed by one workgroup (all threads call it; E <= kRouteMaxE and
 // E rounded up to 8 <= the thread count, topk <= kRouteMaxTopk; keys holds >= that many).  An expert's rank is the number of larger
 // keys (all keys are distinct), so the top-k need no sort; with at least 2E threads two

@@ -101,50 +101,16 @@ __global__ __launch_bounds__(64) void k_router_tail_rows(const uint16_t* __restr
 
 // bf16 router GEMV: workgroup e computes logit e (256 threads split K; fixed-order
 // reduction) and writes it as bf16.
-constexpr int kRouterThreads = 256;
 
 __global__ __launch_bounds__(kRouterThreads) void k_router_logits(const uint16_t* __restrict__ W,
                                                                   const uint16_t* __restrict__ x, int64_t K,
                                                                   uint16_t* __restrict__ logits) {
     __shared__ float wsum[kRouterThreads / 64];
     const int t = threadIdx.x, e = blockIdx.x;
-    const uint16_t* row = W + (int64_t)e * K;
-    float s0 = 0.f, s1 = 0.f;
-    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-    // four chunks' loads are issued before any is used (K = 6144 is three chunks per thread);
-    // each thread still folds its chunks into s0 / s1 in increasing K
-    constexpr int kU = 4;
-    for (int64_t c0 = (int64_t)t * 8; c0 < K; c0 += kU * kRouterThreads * 8) {
-        uint4 wv[kU], av[kU];
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int64_t c = c0 + (int64_t)u * kRouterThreads * 8;
-            if (c < K) {
-                wv[u] = *(const uint4*)(row + c);
-                av[u] = *(const uint4*)(x + c);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int64_t c = c0 + (int64_t)u * kRouterThreads * 8;
-            if (c >= K) break;
-            const uint4 w = wv[u], a = av[u];
-            s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.x), __builtin_bit_cast(bf2, w.x), s0, false);
-            s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.y), __builtin_bit_cast(bf2, w.y), s1, false);
-            s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.z), __builtin_bit_cast(bf2, w.z), s0, false);
-            s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w), __builtin_bit_cast(bf2, w.w), s1, false);
-        }
-    }
-    float v = s0 + s1;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    const float v = router_wave_dot(W + (int64_t)e * K, x, K, t);
     if ((t & 63) == 0) wsum[t >> 6] = v;
     __syncthreads();
-    if (t == 0) {
-        float tot = 0.f;
-        for (int w = 0; w < kRouterThreads / 64; ++w) tot += wsum[w];
-        logits[e] = (uint16_t)bf16_rne(tot);
-    }
+    if (t == 0) logits[e] = (uint16_t)bf16_rne(router_logit(wsum));
 }
 
 // bf16 router GEMV for M <= 8 activation rows: workgroup e reads router row e once and forms
