@@ -227,6 +227,61 @@ def test_moe_c2_full_256_experts(mode):
         assert_bits_equal(h_bits(y), yref, "moe ref C2 E=256")
 
 
+def _moe_persistent_case(H, E, topk, seed):
+    I = 2048
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    ge = random_weights_gpu(Q4K, E * I, H, g)
+    ue = random_weights_gpu(Q4K, E * I, H, g)
+    de = random_weights_gpu(Q4K, E * H, I, g)
+    rng = np.random.default_rng(seed)
+    rw = qo.random_bf16(rng, (E, H), scale=0.05).view(np.uint8).reshape(-1)
+    x = qo.random_bf16(rng, H, scale=0.05)
+    return I, (ge, ue, de), rw, x
+
+
+@pytest.mark.parametrize("H,E,topk", [(2048, 16, 1), (4096, 64, 5), (6144, 32, 2), (2048, 300, 8)])
+def test_moe_fast_persistent_legs(H, E, topk):
+    """Shapes of the persistent expert legs (routed slots only, I = 2048, H = 2048 R): one to
+    eight slots (whole compute-wave groups idle at one and two slots, unequal groups at five),
+    R = 1, 2, 3, and an expert count whose routing keys need padding (300).  The routing equals
+    the reference tail of the fast logits and y is within the MoE bound."""
+    note(f"moe persistent legs H={H} E={E} topk={topk}")
+    I, (ge, ue, de), rw, x = _moe_persistent_case(H, E, topk, H + E + topk)
+    y, sel, sw = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, de, E, H, I, topk, d_bf16(x), mode="fast")
+    logits = h_bits(dev.gemv(BF16, d_u8(rw), E, H, d_bf16(x[None]), mode="fast"))[0]
+    es, ew, _ = go.router_tail(logits, topk)
+    assert np.array_equal(sel.cpu().numpy(), es)
+    assert_bits_equal(h_bits(sw), ew, "sel_w")
+    sub = tuple(_expert_rows(t, E, es) for t in (ge, ue, de))   # routed experts in slot order
+    _check_moe_output(h_bits(y), x, sub, None, np.arange(topk), ew, H, I)
+
+
+def test_moe_persistent_detects_corrupted_expert():
+    """Must-fail twin on the persistent legs: the d of every block in row 0 of the first routed
+    expert's down matrix raised to 4.0 moves y[0] past the MoE bound; the clean step passes."""
+    H, E, topk = 2048, 16, 2
+    note("moe persistent corruption twin")
+    I, (ge, ue, de), rw, x = _moe_persistent_case(H, E, topk, 5150)
+    logits = h_bits(dev.gemv(BF16, d_u8(rw), E, H, d_bf16(x[None]), mode="fast"))[0]
+    es, ew, _ = go.router_tail(logits, topk)
+    sub = tuple(_expert_rows(t, E, es) for t in (ge, ue, de))
+    bad = de.clone()
+    per = bad.numel() // E
+    row0 = bad[int(es[0]) * per:int(es[0]) * per + (I // 256) * 144].view(I // 256, 144)
+    row0[:, 0:2] = torch.tensor(np.asarray(qo.f32_to_f16_bits(np.array([4.0], np.float32)), np.uint16)
+                                .view(np.uint8), device=bad.device)
+    for down, expect_pass in ((bad, False), (de, True)):
+        y, sel, _ = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, down, E, H, I, topk, d_bf16(x), mode="fast")
+        assert np.array_equal(sel.cpu().numpy(), es)
+        try:
+            _check_moe_output(h_bits(y), x, sub, None, np.arange(topk), ew, H, I)
+            passed = True
+        except AssertionError:
+            passed = False
+        assert passed == expect_pass, f"check {'passed' if passed else 'failed'} on {'clean' if expect_pass else 'corrupted'} weights"
+
+
 @pytest.mark.parametrize("H,E", [(512, 300), (1280, 256), (1536, 512)])
 def test_moe_fast_router_wider_than_gateup_plan(H, E):
     """Expert counts that the gate/up plan cannot rank in-kernel (one key per thread and fewer

@@ -96,6 +96,30 @@ def test_moe_layer_fast_c2_shape():
     assert qo.bf16_ulp_distance(h_bits(nrm), h_bits(nr)).max() <= 1
 
 
+def test_moe_layer_fast_persistent_legs():
+    """A layer without a shared expert and with a bf16 router runs the persistent expert legs,
+    the residual added in the down leg's epilogue: the fused call equals rmsnorm -> MoE step ->
+    residual run as three separate calls (bitwise)."""
+    E, H, I, topk = 16, 2048, 2048, 4
+    note("moe layer fast persistent legs")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(16)
+    ge = random_weights_gpu(Q4K, E * I, H, gen)
+    ue = random_weights_gpu(Q4K, E * I, H, gen)
+    de = random_weights_gpu(Q4K, E * H, I, gen)
+    rng = np.random.default_rng(16)
+    rw = d_u8(qo.random_bf16(rng, (E, H), scale=0.05).view(np.uint8).reshape(-1))
+    h = d_bf16(qo.random_bf16(rng, H, scale=0.5))
+    g = d_bf16(qo.random_bf16(rng, H))
+    y, sel, sw = dev.moe_layer_decode(BF16, rw, Q4K, ge, ue, de, E, H, I, topk, h, g, mode="fast")
+    nrm = dev.rmsnorm(h, g, mode="fast")
+    f, sel2, sw2 = dev.moe_swiglu_decode(BF16, rw, Q4K, ge, ue, de, E, H, I, topk, nrm, mode="fast")
+    want = (h.float() + f.float()).to(torch.bfloat16)     # RNE of an exact fp32 sum of two bf16
+    assert torch.equal(sel, sel2)
+    assert_bits_equal(h_bits(sw), h_bits(sw2), "sel_w")
+    assert_bits_equal(h_bits(y), h_bits(want), "layer = pieces")
+
+
 def test_glm_mirror_rmsnorm_ffn_block_lm_head():
     """The reference-interface mirrors (aipu_amd/glm_model_q4k_ref.py): rmsnorm and ffn_block
     on the golden cases, matmul_bf16_dot on the 7-way order case, lm_head vs the oracle."""
