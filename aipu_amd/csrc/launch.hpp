@@ -95,14 +95,16 @@ hipError_t launch_moe_down_mfma(const uint8_t* D, const uint8_t* shD, const int3
                                 int passthrough, hipStream_t st, float* acc_scratch = nullptr,
                                 const uint16_t* resid = nullptr);
 
-// Persistent expert legs of the single-row step (routed slots only, topk <= 8,
-// H = 2048 R with R <= 3, I = 2048): gate/up routes from route.logits in every workgroup.
+// Persistent expert legs of the single-row step (topk <= 8 routed slots, nslots = topk or
+// topk + 1 with the shared expert last, H = 2048 R with R <= 3, I = 2048): gate/up routes from
+// route.logits in every workgroup.
 bool moe_persist_supported(int64_t E, int topk, int nslots, int64_t H, int64_t I);
-hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const MoeRoute& route, int topk, int64_t E,
-                                     int64_t H, int64_t I, const uint16_t* x, uint16_t* h, hipStream_t st);
-hipError_t launch_moe_down_persist(const uint8_t* D, const int32_t* sel, const uint16_t* selw, int topk, int64_t E,
-                                   int64_t H, int64_t I, const uint16_t* h, uint16_t* y, const uint16_t* resid,
-                                   hipStream_t st);
+hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
+                                     const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
+                                     const uint16_t* x, uint16_t* h, hipStream_t st);
+hipError_t launch_moe_down_persist(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
+                                   int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h,
+                                   uint16_t* y, const uint16_t* resid, hipStream_t st);
 
 // Batched MoE (M = 2..8 rows) over the union of the rows' experts, matrix-core GEMVs.
 // uidx/nslots come from the union pass; after_gateup enqueues h = bf16(silu(g) * u).

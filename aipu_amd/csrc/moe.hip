@@ -126,11 +126,13 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
 
     // 2-3. fast path: the gate/up kernel routes from the logits in every workgroup and
     // publishes the decision for the down kernel (no separate router-tail launch)
-    if (fast && !a.ascending && !has_shared && moe_persist_supported(a.E, a.topk, nslots, a.H, a.I)) {
-        // persistent legs: one workgroup per CU streams every expert row once
+    if (fast && !a.ascending && moe_persist_supported(a.E, a.topk, nslots, a.H, a.I)) {
+        // persistent legs: one workgroup per CU streams every expert row once (shared expert last)
         const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};
-        AIPU_TRY(launch_moe_gateup_persist(a.gate_exps, a.up_exps, route, a.topk, a.E, a.H, a.I, a.x, h, st));
-        return launch_moe_down_persist(a.down_exps, sel, selw, a.topk, a.E, a.H, a.I, h, a.y, a.resid, st);
+        AIPU_TRY(launch_moe_gateup_persist(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
+                                           a.I, a.x, h, st));
+        return launch_moe_down_persist(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y,
+                                       a.resid, st);
     }
     if (fast && !a.ascending && moe_mfma_supported(nslots, a.H, a.I) && moe_route_in_kernel(a.E, a.topk, a.H)) {
         const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};

@@ -1,5 +1,6 @@
 // Persistent matrix-core MoE expert legs for the single-row decode step (tolerance mode):
-// routed slots only (no shared expert), topk <= 8, H = 2048 R (R <= 3), I = 2048.
+// topk <= 8 routed slots and an optional shared expert as the last slot, H = 2048 R (R <= 3),
+// I = 2048.
 // Mirrors the expert half of decoder_block (tools/glm_model_q4k_ref.py:797-809) with
 // swiglu_expert (:702-708); the routing decision is route.hpp's (:663-699).
 //
@@ -13,7 +14,8 @@
 // the rounds of group gamma; the last set of a job reduces the job.
 //
 // Gate/up (k_moe_gu_p): job = (slot s, rows i0 .. i0+7 of I); round q = 0 .. 2R-1 holds K
-// segment k = q % R of the gate rows (q < R) or the up rows (q >= R) of expert sel[s].  Group
+// segment k = q % R of the gate rows (q < R) or the up rows (q >= R) of expert sel[s] (the
+// shared expert's for the last slot when there is one).  Group
 // gamma takes the rounds with k = gamma, so wave 4k + p always meets block pair 4k + p of x
 // and keeps that pair's operands in registers for the whole kernel.  Reduction per row: the
 // 4R pair sums in a fixed order, then h = bf16(silu(bf16(g)) * bf16(u)).  Every workgroup
@@ -21,11 +23,12 @@
 // the decision for the down leg and the caller.
 //
 // Down (k_moe_down_p): job = output rows d0 .. d0+7; round q = slot q (8 rows x 1152 B of
-// expert sel[q], all I = 2048 weights of the rows); group gamma takes the slots q = gamma
+// expert sel[q] or the shared expert, all I = 2048 weights of the rows); group gamma takes the slots q = gamma
 // mod 3 and stages those slots' activation pairs h[q] in LDS.  Reduction per row: per slot
 // y_s = (s0 + s1) + (s2 + s3) over its pair sums, then the slot-ordered combine
 //     facc = f32(facc + f32(w_s * bf16(y_s)))   (tools/glm_model_q4k_ref.py:799-809),
-// y = bf16(facc), or bf16(resid + bf16(facc)) with the decoder block's residual.
+// the shared slot last with w = 1; y = bf16(facc), or bf16(resid + bf16(facc)) with the
+// decoder block's residual.
 #include "common.hpp"
 #include "glm_act.hpp"
 #include "launch.hpp"
@@ -47,10 +50,11 @@ constexpr uint32_t kSlot = kJR * kRoundRow;   // bytes of a round
 constexpr int kReaders = 4;                   // sets that read a round
 constexpr int kNCW = 12;                      // compute waves
 constexpr int kGroups = 3;                    // compute wave groups of 4
-constexpr int kMaxJobs = 8;                   // jobs per workgroup
-constexpr int kMaxSlots = 8;                  // routed slots
-constexpr int kMaxRJ = 8;                     // rounds per job
-constexpr int kRedJob = 256;                  // pair sums per job (floats)
+constexpr int kMaxJobs = 9;                   // jobs per workgroup
+constexpr int kMaxRouted = 8;                 // routed slots
+constexpr int kMaxSlots = kMaxRouted + 1;     // and the shared expert
+constexpr int kMaxRJ = kMaxSlots;             // rounds per job (down: one per slot; gate/up: 2R <= 6)
+constexpr int kRedJob = kMaxSlots * kJR * 4;  // pair sums per job (floats; gate/up uses 16 x 12)
 constexpr int kGuNp = 12;                     // pair-sum stride of a gate/up row (4R <= 12)
 
 // Nine loads of round k of 8 rows (row stride rb) at `base` into the LDS slot `dst`.
@@ -175,13 +179,24 @@ struct GuCursor {
         }
     }
 };
+// Expert matrices of one leg: the routed stack (expert e at e * ebytes) and the shared expert
+// (slot topk, when there is one).
+struct Stack {
+    const uint8_t* base;
+    const uint8_t* shared;
+    int64_t ebytes;
+    __device__ const uint8_t* slot(int ev, int s, int topk) const {
+        return s < topk ? base + (int64_t)__builtin_amdgcn_readlane(ev, s) * ebytes : shared;
+    }
+};
+
 template <int R, uint32_t POL>
-__device__ __forceinline__ void gu_issue(const GuCursor& cu, int ev, const uint8_t* Gw, const uint8_t* Uw,
-                                         int64_t ebytes, uint8_t* dst, int lane) {
+__device__ __forceinline__ void gu_issue(const GuCursor& cu, int ev, const Stack& Gs, const Stack& Us, int topk,
+                                         uint8_t* dst, int lane) {
     constexpr uint32_t rb = R * kRoundRow;
-    const int64_t e = __builtin_amdgcn_readlane(ev, cu.js);
     const int half = cu.q >= R ? 1 : 0, k = cu.q - half * R;
-    issue_round<POL>((half ? Uw : Gw) + e * ebytes + (int64_t)cu.ji * kJR * rb, kJR, rb, (uint32_t)k, dst, lane);
+    issue_round<POL>((half ? Us : Gs).slot(ev, cu.js, topk) + (int64_t)cu.ji * kJR * rb, kJR, rb, (uint32_t)k, dst,
+                     lane);
 }
 
 // Copy-wave cursor over the down rounds: slot q of the job of output rows d0 .. d0 + 7.
@@ -201,11 +216,10 @@ struct DnCursor {
     }
 };
 template <uint32_t POL>
-__device__ __forceinline__ void dn_issue(const DnCursor& cu, int ev, const uint8_t* Dw, int64_t ebytes, int64_t Hd,
+__device__ __forceinline__ void dn_issue(const DnCursor& cu, int ev, const Stack& Ds, int topk, int64_t Hd,
                                          uint8_t* dst, int lane) {
     const int nvalid = (int)(Hd - cu.d0 < kJR ? Hd - cu.d0 : kJR);
-    const int64_t e = __builtin_amdgcn_readlane(ev, cu.q);
-    issue_round<POL>(Dw + e * ebytes + cu.d0 * (int64_t)kRoundRow, nvalid, kRoundRow, 0u, dst, lane);
+    issue_round<POL>(Ds.slot(ev, cu.q, topk) + cu.d0 * (int64_t)kRoundRow, nvalid, kRoundRow, 0u, dst, lane);
 }
 
 // Lane s < topk: slot s's expert from the winners' keys.
@@ -259,8 +273,8 @@ __device__ __forceinline__ void gu_jobs(const Ring& rg, int T, int u0, int wg, i
 // Down jobs of compute wave (gam, p): slots q = gam, gam + 3, ... of job t are rounds
 // u0 + S t + q, against staged pair 4q + p; the job's last set combines the slots.
 template <int NS>
-__device__ __forceinline__ void dn_jobs(const Ring& rg, int T, int u0, int S, int wg, int G, int64_t Hd, int gam, int p,
-                                        uint32_t stage, const HdrSel& hs, const CodeK& ck, int& seen,
+__device__ __forceinline__ void dn_jobs(const Ring& rg, int T, int u0, int S, int topk, int wg, int G, int64_t Hd,
+                                        int gam, int p, uint32_t stage, const HdrSel& hs, const CodeK& ck, int& seen,
                                         const uint16_t* selw, uint16_t* __restrict__ Y,
                                         const uint16_t* __restrict__ resid, int lane) {
     const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
@@ -287,16 +301,18 @@ __device__ __forceinline__ void dn_jobs(const Ring& rg, int T, int u0, int S, in
         uint32_t before = 0;
         for (int i = 0; i < mine; ++i) before = lds_add_rtn(&rg.done[t]);
         if (mine == 0 || before != (uint32_t)(4 * S) - 1u) continue;
-        // the job's last set: lane 8 * row + slot
+        // the job's last set: lane 8 * row + slot (slots 0..7; a ninth slot, the shared expert
+        // after eight routed ones, is formed by lane 8 * row itself); weight 1 for the shared slot
         const int row = lane >> 3, s = lane & 7;
-        float pw = 0.f;
-        if (s < S) {
-            const float* qp = rt + (s * kJR + row) * 4;
-            const float ys = (qp[0] + qp[1]) + (qp[2] + qp[3]);
-            pw = bf16_to_f32(selw[s]) * bf16_to_f32(bf16_rne(ys));
-        }
+        const auto slot_term = [&](int q) {
+            const float* qp = rt + (q * kJR + row) * 4;
+            const float yb = bf16_to_f32(bf16_rne((qp[0] + qp[1]) + (qp[2] + qp[3])));
+            return q < topk ? bf16_to_f32(selw[q]) * yb : yb;
+        };
+        const float pw = s < S ? slot_term(s) : 0.f;
         float facc = 0.f;
-        for (int s2 = 0; s2 < S; ++s2) facc = facc + __shfl(pw, (lane & ~7) + s2, 64);
+        for (int s2 = 0; s2 < S && s2 < kJR; ++s2) facc = facc + __shfl(pw, (lane & ~7) + s2, 64);
+        if (S > kJR) facc = facc + slot_term(kJR);
         const int64_t d = (int64_t)(wg + t * G) * kJR + row;
         if (s == 0 && d < Hd) {
             uint32_t yb = bf16_rne(facc);
@@ -338,9 +354,7 @@ __device__ __forceinline__ void x_operands(const uint4& xv, uint8_t* st, int lan
 
 // ------------------------------------------------------------------ gate/up
 template <int R, int NS, int Q, int CW, uint32_t POL>
-__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(const uint8_t* __restrict__ Gw,
-                                                            const uint8_t* __restrict__ Uw, int64_t ebytes,
-                                                            MoeRoute route, int E, int topk,
+__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack Us, MoeRoute route, int E, int topk,
                                                             const uint16_t* __restrict__ X, uint16_t* __restrict__ Hout,
                                                             int I, int njobs) {
     constexpr int RJ = 2 * R, np = 4 * R, nsb = 8 * R;
@@ -380,7 +394,7 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(const uint8_t* __
         GuCursor gc;
         gc.start(c, wg, it8, RJ, G);
         copy_ring<NS, Q, CW, kLoads, kReaders>(c, T * RJ, s_cnt, s_read, [&](int u) {
-            gu_issue<R, POL>(gc, ev, Gw, Uw, ebytes, s_dyn + (uint32_t)(u % NS) * kSlot, lane);
+            gu_issue<R, POL>(gc, ev, Gs, Us, topk, s_dyn + (uint32_t)(u % NS) * kSlot, lane);
             gc.advance(CW, it8, RJ, G);
         });
         return;
@@ -396,9 +410,8 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(const uint8_t* __
 
 // ------------------------------------------------------------------ down
 template <int NS, int Q, int CW, uint32_t POL>
-__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(const uint8_t* __restrict__ Dw, int64_t ebytes,
-                                                              const int32_t* __restrict__ sel,
-                                                              const uint16_t* __restrict__ selw, int E, int S,
+__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(Stack Ds, const int32_t* __restrict__ sel,
+                                                              const uint16_t* __restrict__ selw, int E, int topk, int S,
                                                               const uint16_t* __restrict__ Hin, int I, int64_t Hd,
                                                               uint16_t* __restrict__ Y,
                                                               const uint16_t* __restrict__ resid, int njobs) {
@@ -423,11 +436,11 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(const uint8_t* 
 
     if (w >= kNCW) {   // ---- copy wave c: lane s holds slot s's expert
         const int c = w - kNCW;
-        const int ev = lane < S ? (sel[lane] < 0 ? 0 : (sel[lane] >= E ? E - 1 : sel[lane])) : 0;
+        const int ev = lane < topk ? (sel[lane] < 0 ? 0 : (sel[lane] >= E ? E - 1 : sel[lane])) : 0;
         DnCursor dc;
         dc.start(c, S, wg, G);
         copy_ring<NS, Q, CW, kLoads, kReaders>(c, T * S, s_cnt, s_read, [&](int u) {
-            dn_issue<POL>(dc, ev, Dw, ebytes, Hd, s_dyn + (uint32_t)(u % NS) * kSlot, lane);
+            dn_issue<POL>(dc, ev, Ds, topk, Hd, s_dyn + (uint32_t)(u % NS) * kSlot, lane);
             dc.advance(CW, S, G);
         });
         return;
@@ -435,44 +448,49 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_down_p(const uint8_t* 
     // ---- compute wave (gam, p): pair p of slots gam, gam + 3, ...
     dn_stage_h(xv, s_stage, S, gam, p, lane);
     int seen = -1;
-    dn_jobs<NS>(rg, T, 0, S, wg, G, Hd, gam, p, lds_addr(s_stage), hdr_sel(lane >> 4), code_k(), seen, selw, Y, resid,
-                lane);
+    dn_jobs<NS>(rg, T, 0, S, topk, wg, G, Hd, gam, p, lds_addr(s_stage), hdr_sel(lane >> 4), code_k(), seen, selw, Y,
+                resid, lane);
 }
 
 // Ring slots, rounds in flight per copy wave, copy waves (measured: 1 or 2 copy waves, 4 to 7
 // rounds each, are within 1 us of each other; these were the fastest).  The ring takes more
 // than half the CU's LDS, so the workgroups spread one per CU.
+// With a ninth (shared) slot the down leg's staged pairs leave room for 11 slots.
 constexpr int kGuNS = 12, kGuQ = 5, kGuCW = 2;
-constexpr int kDnNS = 12, kDnQ = 7, kDnCW = 1;
+constexpr int kDnNS = 12, kDnNS9 = 11, kDnQ = 7, kDnCW = 1;
 
 size_t gu_lds(int R) { return (size_t)kGuNS * kSlot + (size_t)(4 * R) * kStgBytes; }
-size_t dn_lds(int S) { return (size_t)kDnNS * kSlot + (size_t)(4 * S) * kStgBytes; }
+size_t dn_lds(int ns, int S) { return (size_t)ns * kSlot + (size_t)(4 * S) * kStgBytes; }
 
 }  // namespace
 
 bool moe_persist_supported(int64_t E, int topk, int nslots, int64_t H, int64_t I) {
-    if (nslots != topk || topk < 1 || topk > kMaxSlots || E < 1 || E > kRouteMaxE || topk > E) return false;
+    if (topk < 1 || topk > kMaxRouted || (nslots != topk && nslots != topk + 1)) return false;
+    if (E < 1 || E > kRouteMaxE || topk > E) return false;
     if (H % 2048 != 0 || H < 2048 || H > 6144 || I != 2048) return false;
     if ((E + 7) / 8 * 8 > 64 * (kNCW + 1)) return false;   // in-kernel routing: one key per thread
     const int64_t cus = device_cu_count();
-    const int64_t gu_jobs = (int64_t)topk * (I / kJR), dn_jobs = (H + kJR - 1) / kJR;
+    const int64_t gu_jobs = (int64_t)nslots * (I / kJR), dn_jobs = (H + kJR - 1) / kJR;
     return gu_jobs <= kMaxJobs * cus && dn_jobs <= kMaxJobs * cus;
 }
 
-hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const MoeRoute& route, int topk, int64_t E,
-                                     int64_t H, int64_t I, const uint16_t* x, uint16_t* h, hipStream_t st) {
-    if (!moe_persist_supported(E, topk, topk, H, I) || !route.logits) return hipErrorInvalidValue;
+hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
+                                     const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
+                                     const uint16_t* x, uint16_t* h, hipStream_t st) {
+    if (!moe_persist_supported(E, topk, nslots, H, I) || !route.logits || (nslots > topk && (!shG || !shU)))
+        return hipErrorInvalidValue;
     const int R = (int)(H / 2048);
     const int64_t rb = row_bytes(T_Q4_K, H);
-    const int njobs = (int)(topk * (I / kJR));
+    const Stack Gs{G, shG, rb * I}, Us{U, shU, rb * I};
+    const int njobs = (int)(nslots * (I / kJR));
     const int cus = device_cu_count();
     const int tpw = (njobs + cus - 1) / cus;
     const int G2 = (njobs + tpw - 1) / tpw;
     const dim3 grid(G2), block(64 * (kNCW + kGuCW));
 #define AIPU_GU(RV)                                                                                              \
     if (R == RV) {                                                                                               \
-        hipLaunchKernelGGL((k_moe_gu_p<RV, kGuNS, kGuQ, kGuCW, kNT>), grid, block, gu_lds(RV), st, G, U, rb * I, route, (int)E, topk, \
-                           x, h, (int)I, njobs);                                                                 \
+        hipLaunchKernelGGL((k_moe_gu_p<RV, kGuNS, kGuQ, kGuCW, kNT>), grid, block, gu_lds(RV), st, Gs, Us, route, \
+                           (int)E, topk, x, h, (int)I, njobs);                                                   \
         return hipGetLastError();                                                                                \
     }
     AIPU_GU(1) AIPU_GU(2) AIPU_GU(3)
@@ -480,17 +498,23 @@ hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const M
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_moe_down_persist(const uint8_t* D, const int32_t* sel, const uint16_t* selw, int topk, int64_t E,
-                                   int64_t H, int64_t I, const uint16_t* h, uint16_t* y, const uint16_t* resid,
-                                   hipStream_t st) {
-    if (!moe_persist_supported(E, topk, topk, H, I)) return hipErrorInvalidValue;
+hipError_t launch_moe_down_persist(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
+                                   int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h,
+                                   uint16_t* y, const uint16_t* resid, hipStream_t st) {
+    if (!moe_persist_supported(E, topk, nslots, H, I) || (nslots > topk && !shD)) return hipErrorInvalidValue;
     const int64_t rb = row_bytes(T_Q4_K, I);
+    const Stack Ds{D, shD, rb * H};
     const int njobs = (int)((H + kJR - 1) / kJR);
     const int cus = device_cu_count();
     const int tpw = (njobs + cus - 1) / cus;
     const int G2 = (njobs + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_moe_down_p<kDnNS, kDnQ, kDnCW, 0>), dim3(G2), dim3(64 * (kNCW + kDnCW)), dn_lds(topk), st, D, rb * H, sel,
-                       selw, (int)E, topk, h, (int)I, H, y, resid, njobs);
+    const dim3 grid(G2), block(64 * (kNCW + kDnCW));
+    if (nslots <= kMaxRouted)
+        hipLaunchKernelGGL((k_moe_down_p<kDnNS, kDnQ, kDnCW, 0>), grid, block, dn_lds(kDnNS, nslots), st, Ds, sel, selw,
+                           (int)E, topk, nslots, h, (int)I, H, y, resid, njobs);
+    else
+        hipLaunchKernelGGL((k_moe_down_p<kDnNS9, kDnQ, kDnCW, 0>), grid, block, dn_lds(kDnNS9, nslots), st, Ds, sel,
+                           selw, (int)E, topk, nslots, h, (int)I, H, y, resid, njobs);
     return hipGetLastError();
 }
 

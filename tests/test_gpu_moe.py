@@ -240,21 +240,30 @@ def _moe_persistent_case(H, E, topk, seed):
     return I, (ge, ue, de), rw, x
 
 
-@pytest.mark.parametrize("H,E,topk", [(2048, 16, 1), (4096, 64, 5), (6144, 32, 2), (2048, 300, 8)])
-def test_moe_fast_persistent_legs(H, E, topk):
-    """Shapes of the persistent expert legs (routed slots only, I = 2048, H = 2048 R): one to
-    eight slots (whole compute-wave groups idle at one and two slots, unequal groups at five),
-    R = 1, 2, 3, and an expert count whose routing keys need padding (300).  The routing equals
-    the reference tail of the fast logits and y is within the MoE bound."""
-    note(f"moe persistent legs H={H} E={E} topk={topk}")
-    I, (ge, ue, de), rw, x = _moe_persistent_case(H, E, topk, H + E + topk)
-    y, sel, sw = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, de, E, H, I, topk, d_bf16(x), mode="fast")
+@pytest.mark.parametrize("H,E,topk,shared", [(2048, 16, 1, False), (4096, 64, 5, False), (6144, 32, 2, False),
+                                             (2048, 300, 8, False), (2048, 16, 4, True), (6144, 32, 8, True)])
+def test_moe_fast_persistent_legs(H, E, topk, shared):
+    """Shapes of the persistent expert legs (I = 2048, H = 2048 R): one to eight routed slots
+    (whole compute-wave groups idle at one and two slots, unequal groups at five), R = 1, 2, 3,
+    an expert count whose routing keys need padding (300), and the shared expert as the last
+    slot (five and nine slots).  The routing equals the reference tail of the fast logits and y
+    is within the MoE bound."""
+    note(f"moe persistent legs H={H} E={E} topk={topk} shared={shared}")
+    I, (ge, ue, de), rw, x = _moe_persistent_case(H, E, topk, H + E + topk + shared)
+    shd = sh = None
+    if shared:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(H + topk)
+        shd = (random_weights_gpu(Q4K, I, H, g), random_weights_gpu(Q4K, I, H, g), random_weights_gpu(Q4K, H, I, g))
+        sh = tuple(t.cpu().numpy() for t in shd)
+    y, sel, sw = dev.moe_swiglu_decode(BF16, d_u8(rw), Q4K, ge, ue, de, E, H, I, topk, d_bf16(x), mode="fast",
+                                       shared=shd)
     logits = h_bits(dev.gemv(BF16, d_u8(rw), E, H, d_bf16(x[None]), mode="fast"))[0]
     es, ew, _ = go.router_tail(logits, topk)
     assert np.array_equal(sel.cpu().numpy(), es)
     assert_bits_equal(h_bits(sw), ew, "sel_w")
     sub = tuple(_expert_rows(t, E, es) for t in (ge, ue, de))   # routed experts in slot order
-    _check_moe_output(h_bits(y), x, sub, None, np.arange(topk), ew, H, I)
+    _check_moe_output(h_bits(y), x, sub, sh, np.arange(topk), ew, H, I)
 
 
 def test_moe_persistent_detects_corrupted_expert():
