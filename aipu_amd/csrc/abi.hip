@@ -58,9 +58,10 @@ uintptr_t weight_align(int t, int mode = AIPU_MODE_FAST) {
 
 hipStream_t S(void* s) { return (hipStream_t)s; }
 
-// Shared checks for a GEMV-shaped call.
+// Shared checks for a GEMV-shaped call.  k256: K must be a whole number of 256-weight
+// super-blocks (every entry point but the plain GEMV, which serves any multiple of the block).
 int check_gemv(int type, const void* w, int64_t N, int64_t K, const void* x, int64_t M, const void* y,
-               const void* yf, int mode) {
+               const void* yf, int mode, bool k256 = true) {
     if (!known_type(type)) return fail(AIPU_ERR_TYPE, "unsupported ggml type %d", type);
     if (!w || !x || !y) return fail(AIPU_ERR_ARG, "null w/x/y pointer");
     if (mode != AIPU_MODE_FAST && mode != AIPU_MODE_REF) return fail(AIPU_ERR_ARG, "mode must be 0 (fast) or 1 (ref)");
@@ -69,7 +70,7 @@ int check_gemv(int type, const void* w, int64_t N, int64_t K, const void* x, int
     if (K % aipu::type_qk(type))
         return fail(AIPU_ERR_SHAPE, "K=%lld is not a multiple of the %s block size %d", (long long)K, type_name(type),
                     aipu::type_qk(type));
-    if (K % 256) return fail(AIPU_ERR_SHAPE, "K=%lld must be a multiple of 256", (long long)K);
+    if (k256 && K % 256) return fail(AIPU_ERR_SHAPE, "K=%lld must be a multiple of 256", (long long)K);
     if (N > (1LL << 31) || M > (1LL << 24)) return fail(AIPU_ERR_SHAPE, "N or M out of range");
     if (!aligned(w, weight_align(type, mode)))
         return fail(AIPU_ERR_ALIGN, "%s weights must be %d-byte aligned", type_name(type),
@@ -81,9 +82,11 @@ int check_gemv(int type, const void* w, int64_t N, int64_t K, const void* x, int
 }
 
 // Fast kernels exist for every type: Q4_K on the matrix cores, bf16 in the streaming
-// kernel, Q6_K / Q8_0 / F16 in the mixed-type kernel (K up to its staging limit; larger K
-// is served by the exact kernel, whose results trivially satisfy the fast-mode tolerance).
+// kernel, Q6_K / Q8_0 / F16 in the mixed-type kernel (K up to its staging limit).  Larger K,
+// and K that is not a whole number of 256-weight super-blocks, are served by the exact
+// kernel, whose results trivially satisfy the fast-mode tolerance.
 bool has_fast(int type, int64_t K) {
+    if (K % 256) return false;   // a partial super-block: the exact kernel
     if (type == aipu::T_Q4_K || type == aipu::T_BF16) return true;
     return aipu::gemv_mixed_supported(type, K);
 }
@@ -135,7 +138,7 @@ int aipu_gemv_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t 
 
 int aipu_gemv(int ggml_type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
               float* y_f32, int mode, void* stream) {
-    int rc = check_gemv(ggml_type, w, N, K, x, M, y, y_f32, mode);
+    int rc = check_gemv(ggml_type, w, N, K, x, M, y, y_f32, mode, false);
     if (rc) return rc;
     if (mode == AIPU_MODE_FAST && has_fast(ggml_type, K))
         return hip_status(aipu::launch_gemv_fast(ggml_type, w, N, K, x, M, y, y_f32, S(stream)), "aipu_gemv");

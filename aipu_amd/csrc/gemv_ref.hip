@@ -5,7 +5,8 @@
 //     acc = f32(acc + f32(x[m][k] * w[n][k]))     for k = 0 .. K-1, in order,
 // then y = bf16_RNE(acc).  One lane owns one output row and walks K sequentially; the
 // 64 rows of a workgroup are staged 256 weights at a time through LDS so the global
-// reads stay coalesced.  The library is compiled with -ffp-contract=off, so the multiply
+// reads stay coalesced.  A last stage of fewer weights serves K that is a multiple of the
+// type's block but not of 256 (Q8_0: 32; F16 / BF16: any K).  The library is compiled with -ffp-contract=off, so the multiply
 // and the add below are two separately rounded ops.
 #include "common.hpp"
 #include "launch.hpp"
@@ -28,7 +29,8 @@ struct Stage {
 // Dequantise weight k (0..255) of the row's current stage, reading the staged bytes.
 // Q4_K: tools/q4k_ref.py:45-60.  Computed per 32-weight sub-block by the caller.
 template <int TYPE>
-__device__ __forceinline__ void stage_mac(const uint8_t* rb, const float (*xs)[kStageW], int mcnt, float* acc) {
+__device__ __forceinline__ void stage_mac(const uint8_t* rb, const float (*xs)[kStageW], int mcnt, float* acc,
+                                          int kn) {
     if constexpr (TYPE == T_Q4_K) {
         const uint16_t* h = (const uint16_t*)rb;
         const float d = f16_to_f32(h[0]);
@@ -75,8 +77,8 @@ __device__ __forceinline__ void stage_mac(const uint8_t* rb, const float (*xs)[k
             }
         }
     } else if constexpr (TYPE == T_Q8_0) {
-        // 8 blocks of fp16 d | int8 qs[32]  (tools/q4k_ref.py:126-129)
-        for (int b = 0; b < 8; ++b) {
+        // up to 8 blocks of fp16 d | int8 qs[32]  (tools/q4k_ref.py:126-129)
+        for (int b = 0; b < kn / 32; ++b) {
             const uint8_t* p8 = rb + 34 * b;
             const float d = f16_to_f32((uint32_t)p8[0] | ((uint32_t)p8[1] << 8));
             for (int i = 0; i < 32; ++i) {
@@ -92,7 +94,7 @@ __device__ __forceinline__ void stage_mac(const uint8_t* rb, const float (*xs)[k
         }
     } else {  // F16 / BF16 passthrough
         const uint16_t* h = (const uint16_t*)rb;
-        for (int k = 0; k < 256; ++k) {
+        for (int k = 0; k < kn; ++k) {
             const float w = TYPE == T_F16 ? f16_to_f32(h[k]) : bf16_to_f32(h[k]);
             for (int mm = 0; mm < kMC; ++mm) {
                 if (mm < mcnt) {
@@ -143,26 +145,39 @@ __global__ __launch_bounds__(kRows) void k_gemv_ref(const uint8_t* __restrict__ 
     const int64_t m0 = (int64_t)blockIdx.y * kMC;
     const int mcnt = (int)((M - m0) < kMC ? (M - m0) : kMC);
     const int64_t rb = row_bytes(TYPE, K);
-    const int nstage = (int)(K / kStageW);
+    const int nfull = (int)(K / kStageW);
+    const int ktail = (int)(K - (int64_t)nfull * kStageW);   // a multiple of the type's block
     float acc[kMC];
 #pragma unroll
     for (int i = 0; i < kMC; ++i) acc[i] = 0.0f;
 
-    for (int st = 0; st < nstage; ++st) {
+    for (int st = 0; st < nfull + (ktail ? 1 : 0); ++st) {
+        const int kn = st < nfull ? kStageW : ktail;
         __syncthreads();
-        for (int idx = lane; idx < kRows * S::u16; idx += kRows) {
-            const int r = idx / S::u16, c = idx - r * S::u16;
-            const int64_t n = row0 + r;
-            uint16_t v = 0;
-            if (n < N) v = *(const uint16_t*)(W + n * rb + (int64_t)st * S::bytes + 2 * c);
-            rows[r * S::stride + c] = v;
+        if (kn == kStageW) {
+            for (int idx = lane; idx < kRows * S::u16; idx += kRows) {
+                const int r = idx / S::u16, c = idx - r * S::u16;
+                const int64_t n = row0 + r;
+                uint16_t v = 0;
+                if (n < N) v = *(const uint16_t*)(W + n * rb + (int64_t)st * S::bytes + 2 * c);
+                rows[r * S::stride + c] = v;
+            }
+        } else {
+            const int u16 = (int)(row_bytes(TYPE, kn) / 2);   // Q8_0: 17 words per block; F16 / BF16: kn
+            for (int idx = lane; idx < kRows * u16; idx += kRows) {
+                const int r = idx / u16, c = idx - r * u16;
+                const int64_t n = row0 + r;
+                uint16_t v = 0;
+                if (n < N) v = *(const uint16_t*)(W + n * rb + (int64_t)st * S::bytes + 2 * c);
+                rows[r * S::stride + c] = v;
+            }
         }
         for (int idx = lane; idx < kMC * kStageW; idx += kRows) {
             const int mm = idx / kStageW, k = idx - mm * kStageW;
-            xs[mm][k] = mm < mcnt ? bf16_to_f32(X[(m0 + mm) * K + (int64_t)st * kStageW + k]) : 0.0f;
+            xs[mm][k] = mm < mcnt && k < kn ? bf16_to_f32(X[(m0 + mm) * K + (int64_t)st * kStageW + k]) : 0.0f;
         }
         __syncthreads();
-        if (row0 + lane < N) stage_mac<TYPE>((const uint8_t*)(rows + lane * S::stride), xs, mcnt, acc);
+        if (row0 + lane < N) stage_mac<TYPE>((const uint8_t*)(rows + lane * S::stride), xs, mcnt, acc, kn);
     }
     const int64_t n = row0 + lane;
     if (n < N) {

@@ -79,8 +79,11 @@ int aipu_gemv_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t 
 /* The GEMM core: y[M][N] = bf16(x[M][K] . dequant(w)^T) straight from ggml blocks.
  * Replaces matmul_q4k(x, QW.dequant()) (tools/glm_model_q4k_ref.py:470-472 with
  * tools/q4k_matmul_gen.py:28-40) and the glm_matmul_q4k datapath (src/glm_matmul_q4k.v:50-288).
- * Types: Q4_K, Q6_K, Q8_0, F16, BF16.  K must be a multiple of 256 for every type: the
- * reference's datapath works in 256-weight super-blocks along K for all types (a Q8_0
+ * Types: Q4_K, Q6_K, Q8_0, F16, BF16.  K must be a multiple of the type's block: 256 for
+ * Q4_K and Q6_K, 32 for Q8_0 (tools/q4k_ref.py:126-129), 1 for F16 and BF16.  A K that is not
+ * a multiple of 256 runs the reference-order kernel in both modes (its results satisfy the
+ * fast-mode tolerance).  The other entry points below (tiles, SwiGLU, MoE, prefill) work in
+ * 256-weight super-blocks along K for every type, as the reference's datapath does (a Q8_0
  * super-block is 8 blocks of 32; src/glm_matmul_q4k.v:90-91, tools/q4k_mixed_gen.py:131,143,296).
  * y_f32 (nullable) receives the fp32 accumulators.  M >= 1 (M = K+1 <= 8 for speculative
  * verification batches; large M is served too, see aipu_gemm_prefill). */

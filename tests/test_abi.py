@@ -58,7 +58,7 @@ def test_gemv_validation():
     assert f(12, FAKE_ODD, 64, 256, FAKE, 1, FAKE, NULL, 0, S) == ALIGN
     assert f(12, FAKE, 64, 256, ctypes.c_void_p(0x100008), 1, FAKE, NULL, 0, S) == ALIGN  # fast mode wants 16 B
     assert f(12, FAKE, 64, 256, FAKE, 1, FAKE, NULL, 7, S) == ARG
-    assert f(8, FAKE, 64, 48, FAKE, 1, FAKE, NULL, 1, S) == SHAPE     # Q8_0: K%32 ok, K%256 not
+    assert f(8, FAKE, 64, 48, FAKE, 1, FAKE, NULL, 1, S) == SHAPE     # Q8_0: K = 48 is not a whole number of blocks
 
 
 def test_dequant_and_elementwise_validation():

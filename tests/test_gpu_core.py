@@ -123,6 +123,31 @@ def test_gemv_ref_bitexact(t, N, K, M):
     assert_bits_equal(h_bits(y), ye, "y")
 
 
+PARTIAL_CASES = [
+    (qo.GGML_Q8_0, 70, 288, 1), (qo.GGML_Q8_0, 64, 4128, 3), (qo.GGML_F16, 65, 100, 2), (qo.GGML_F16, 33, 513, 1),
+    (30, 64, 264, 4), (30, 17, 7, 1),
+]
+
+
+@pytest.mark.parametrize("mode", ["ref", "fast"])
+@pytest.mark.parametrize("t,N,K,M", PARTIAL_CASES)
+def test_gemv_k_not_multiple_of_256(t, N, K, M, mode):
+    """K a multiple of the type's block but not of 256 (Q8_0: 32; F16 / BF16: any K, odd
+    ones included): the last 256-weight stage is partial; both modes run the reference order
+    and are bit-exact against the oracle."""
+    note(f"gemv partial super-block type={t} N={N} K={K} M={M} {mode}")
+    rng = np.random.default_rng(N * K + M + 7)
+    raw = qo.random_bf16(rng, N * K).view(np.uint8) if t == 30 else qo.random_weights(rng, t, N, K)
+    x = qo.random_bf16(rng, (M, K))
+    y, yf = dev.gemv(t, d_u8(raw), N, K, d_bf16(x), mode=mode, out_f32=True)
+    if t == 30:
+        acc, ye = qo.gemv_ref(qo.bf16_bits_to_f32(raw.view(np.uint16)).reshape(N, K), qo.bf16_bits_to_f32(x))
+    else:
+        acc, ye = co.gemv_ref(t, raw, N, K, x)
+    assert_bits_equal(u32(h_f32(yf)), u32(acc), "acc")
+    assert_bits_equal(h_bits(y), ye, "y")
+
+
 def test_gemv_ref_full_north_star_shape():
     """K = N = 6144, M = 1: every output bit-exact against the C oracle."""
     note("gemv ref 6144x6144")
