@@ -4,8 +4,8 @@
 // tools/q4k_mixed_gen.py:382-440.  A single-tile call serves the plain GEMV of the types
 // other than Q4_K.
 //
-// Workgroup.  Four waves own one 16-row group of one tile; wave w takes the w-th quarter of
-// the row's 256-weight blocks.  Each wave stages its own activations, then streams its 16
+// Workgroup.  Four waves own one 16-row group of one tile (8 rows for F16 / BF16); wave w
+// takes the w-th quarter of the row's 256-weight blocks.  Each wave stages its own activations, then streams its 16
 // rows group by group (GS blocks per group) into its own LDS slice with direct-to-LDS buffer
 // loads (16 consecutive bytes per lane, so one instruction covers ~1 KB of row bytes), and
 // copies a group into registers before the next group's loads are issued into the slice.
@@ -17,6 +17,10 @@
 // Lane layout: lane 16g + n works on row n of the group and on weights 64g..64g+63 of every
 // block (a Q6_K lane instead takes half g>>1, positions l = 16(g&1)..+15 of the four
 // 32-position runs, which are the same 64 weights in the order the Q6_K bytes store them).
+// F16 / BF16 groups are 8 rows x 2 blocks (the same 8 KB as 16 rows x 1 block, in half the
+// groups, so a wave waits for half as many copies): lane 16g + n takes row n & 7 and block
+// n >> 3 of the group.  (Q6_K and Q8_0 groups of 8 rows x 4 blocks, two blocks per lane,
+// measured slower: their decode is VALU-bound.)
 //
 // Arithmetic.  Q4_K runs on the matrix cores (mfma_gemv.hpp).  The other types decode in
 // VALU registers against fp32 activations staged in LDS, with partial sums per scale group
@@ -50,24 +54,26 @@ template <int TYPE>
 struct Geom;
 template <>
 struct Geom<T_Q4_K> {
-    static constexpr int kBlk = 144, kPitch = 144, GS = 3;
+    static constexpr int kBlk = 144, kPitch = 144, GS = 3, kRows = kTR;
 };
 template <>
 struct Geom<T_Q6_K> {
-    static constexpr int kBlk = 210, kPitch = 224, GS = 2;
+    static constexpr int kBlk = 210, kPitch = 224, GS = 2, kRows = kTR;
 };
 template <>
 struct Geom<T_Q8_0> {
-    static constexpr int kBlk = 272, kPitch = 272, GS = 2;
+    static constexpr int kBlk = 272, kPitch = 272, GS = 2, kRows = kTR;
 };
 template <>
 struct Geom<T_F16> {
-    static constexpr int kBlk = 512, kPitch = 512, GS = 1;
+    static constexpr int kBlk = 512, kPitch = 512, GS = 2, kRows = kTR / 2;
 };
 template <>
 struct Geom<T_BF16> {
-    static constexpr int kBlk = 512, kPitch = 512, GS = 1;
+    static constexpr int kBlk = 512, kPitch = 512, GS = 2, kRows = kTR / 2;
 };
+// Output rows per workgroup of a tile of type t.
+int mix_tile_rows(int t) { return t == T_F16 || t == T_BF16 ? kTR / 2 : kTR; }
 
 // Direct-to-LDS copy of one group: piece j (16 B) of the slice is piece p of block b of row
 // r, j = (r * GS + b) * kPitch / 16 + p.  Lanes past the last piece, and blocks past the
@@ -77,7 +83,7 @@ struct MixDma {
     typedef Geom<TYPE> G;
     static constexpr int kP16 = G::kPitch / 16;
     static constexpr int kRowPieces = G::GS * kP16;
-    static constexpr int kPieces = 16 * kRowPieces;
+    static constexpr int kPieces = G::kRows * kRowPieces;
     static constexpr int kInsts = (kPieces + 63) / 64;
     static_assert(kInsts * 1024 <= kSliceBytes, "slice too small");
     uint32_t off[kInsts];
@@ -276,8 +282,8 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
     const int bpk = kb1 - kb0;
     const int NG = (bpk + G::GS - 1) / G::GS;
     const int64_t rb = (int64_t)nsb * G::kBlk;
-    const int r0 = grp * kTR;
-    const int nvalid = T.nrows - r0 < kTR ? T.nrows - r0 : kTR;
+    const int r0 = grp * G::kRows;
+    const int nvalid = T.nrows - r0 < G::kRows ? T.nrows - r0 : G::kRows;
 
     // 1. this wave's activations of every row (pieces past its blocks, and rows past M, read
     // as zero), 2. its first group
@@ -423,36 +429,37 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
                     }
                 }
             } else {
-                Raw128 R[G::GS];
+                // 8 rows x 2 blocks: this lane's row n & 7, block n >> 3 of the group (a block
+                // past the wave's range reads zeros, against zero-staged activations)
+                const int bb = n >> 3;
+                const uint8_t* q = wW + (uint32_t)(n & 7) * (uint32_t)(G::kPitch * G::GS) + G::kPitch * bb + 128 * g;
+                Raw128 R[1];
 #pragma unroll
-                for (int bb = 0; bb < G::GS; ++bb)
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) R[bb].v[i] = *(const uint4*)(p + G::kPitch * bb + 128 * g + 16 * i);
+                for (int i = 0; i < 8; ++i) R[0].v[i] = *(const uint4*)(q + 16 * i);
                 if (gi + 1 < NG) {
                     regs_consumed(R);   // the slice has been read: refill it
                     const int nxt = (gi + 1) * G::GS;
                     dma.issue(wr, wW, kb0 + nxt, bpk - nxt);
                 }
+                const int b = gi * G::GS + bb;
 #pragma unroll
-                for (int bb = 0; bb < G::GS; ++bb) {
-                    const int b = gi * G::GS + bb;
-#pragma unroll
-                    for (int m = 0; m < MR; ++m)
-                        acc[m] = f16_block<TYPE>(R[bb], (const float*)(wA + m * AR::kBytes) + 256 * b, g, acc[m]);
-                }
+                for (int m = 0; m < MR; ++m)
+                    acc[m] = f16_block<TYPE>(R[0], (const float*)(wA + m * AR::kBytes) + 256 * b, g, acc[m]);
             }
         }
     }
     // a wave with no blocks still has its (all-zero) first group in flight
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
-    // 5. per row: reduce over the four K-groups, then across the four parts in order
+    // 5. per row: reduce over the four K-groups (and an 8-row group's two blocks), then
+    // across the four parts in order
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         float a = acc[m];
         a += __shfl_xor(a, 16, 64);
         a += __shfl_xor(a, 32, 64);
-        if (lane < kTR) red[(m * kMixW + w) * kTR + lane] = a;
+        if constexpr (G::kRows < kTR) a += __shfl_xor(a, 8, 64);
+        if (lane < G::kRows) red[(m * kMixW + w) * kTR + lane] = a;
     }
     __syncthreads();
     const int m = tid / kTR, rr = tid - m * kTR;
@@ -525,7 +532,7 @@ hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K
         const aipu_tile_desc& d = tiles[i];
         if (!gemv_mixed_supported(d.ggml_type, K) || d.nrows < 1 || d.nrows > (1LL << 30)) return hipErrorInvalidValue;
         a.t[i] = MixTile{(const uint8_t*)d.w, d.row0, (int32_t)d.nrows, d.ggml_type, (int32_t)nwg, 0};
-        nwg += (d.nrows + kTR - 1) / kTR;
+        nwg += (d.nrows + mix_tile_rows(d.ggml_type) - 1) / mix_tile_rows(d.ggml_type);
         if (nwg > (1LL << 30)) return hipErrorInvalidValue;
     }
     a.n = n_tiles;
