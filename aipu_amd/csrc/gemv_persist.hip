@@ -19,7 +19,7 @@
 // sub-block sum of column n for h = n >> 3.  Codes, seeds and epilogue are those of
 // mfma_gemv.hpp, and the reduction follows its fast-mode order: block terms (block_sum),
 // pair sums (a row shift by 8), then the balanced tree over the pairs with three cross-lane
-// adds -- bit-identical to the M = 2..8 kernels' canon_sum.
+// adds -- bit-identical to the canon_sum of the small-batch kernels (k_gemvs, k_gemvm).
 #include "common.hpp"
 #include "launch.hpp"
 #include "mfma_gemv.hpp"

@@ -60,8 +60,8 @@ hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uin
                                hipStream_t st);
 
 // gemv_persist_m.hip -- persistent Q4_K GEMV for 2 .. 8 activation rows (tolerance mode,
-// K = 2048, 4096, 6144, at most three 8-row tiles per CU), row m bit-identical to the
-// single-row kernels
+// K = 2048, 4096, 6144, at most three 8-row tiles per CU); a row's result does not depend on
+// the other rows of the batch, and agrees with the single-row kernels within the tolerance
 bool gemv_persist_m_supported(int64_t N, int64_t K, int64_t M);
 hipError_t launch_gemv_persist_m(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
                                  float* yf, int64_t ys, hipStream_t st);

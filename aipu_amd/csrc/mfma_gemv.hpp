@@ -278,8 +278,9 @@ struct ActLayout {
 };
 
 // ------------------------------------------------------------- fast-mode reduction order
-// Every plain Q4_K GEMV kernel of the tolerance mode (M = 1 and the M = 2..8 batches) forms
-// an output the same way, so a row of a batch equals the single-row result bit for bit:
+// The single-row kernels and the small-batch kernels (k_gemvs, k_gemvm) of the tolerance mode
+// form an output the same way, so a row of a batch they serve equals the single-row result bit
+// for bit (the persistent multi-row kernel uses its own, dense form):
 //   1. per block b and K-group g (lane 16g + n): S_lo, S_hi from the MFMA chain (seeded with
 //      -128 * the sub-block activation sums), then
 //         term_g = fma(-dmin, fma(m1, A_hi, m0 * A_lo), d * fma(sc1, S_hi, sc0 * S_lo));

@@ -86,7 +86,11 @@ int aipu_gemv_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t 
  * 256-weight super-blocks along K for every type, as the reference's datapath does (a Q8_0
  * super-block is 8 blocks of 32; src/glm_matmul_q4k.v:90-91, tools/q4k_mixed_gen.py:131,143,296).
  * y_f32 (nullable) receives the fp32 accumulators.  M >= 1 (M = K+1 <= 8 for speculative
- * verification batches; large M is served too, see aipu_gemm_prefill). */
+ * verification batches; large M is served too, see aipu_gemm_prefill).  In AIPU_MODE_FAST the
+ * rows of a Q4_K batch may differ from their one-row results within the fast-mode tolerance
+ * (the multi-row kernel sums in its own order; within batches of 2..8 rows a row's bits do not
+ * depend on the other rows or on its position); use AIPU_MODE_REF where a verify batch must
+ * reproduce one-row decoding bit for bit. */
 int aipu_gemv(int ggml_type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
               uint16_t* y, float* y_f32, int mode, void* stream);
 

@@ -213,18 +213,31 @@ def test_gemv_fast_tolerance(N, K, M):
     assert np.array_equal(u32(h_f32(yf2)), u32(h_f32(yf)))
 
 
-# Fast-mode batch invariance: row r of an M-row call is bit-identical to the one-row call on
-# that row, fp32 accumulators included, so a speculative-verify batch computes exactly what
-# greedy decoding computes (the reference gates PE_M rows against per-row PE_M = 1 runs,
-# Makefile:1500-1506).  Covers every row count of a verify batch at the BASELINE shape and the
-# other matrix-core shapes (ragged N, passes of 8 + remainder).  It holds while the rows of a
-# batch are served by the matrix-core kernels, i.e. K <= 7168 (every BASELINE shape); above
-# that, batches of 2+ rows fall back to the streaming kernel's different summation order.
+# Fast-mode batch invariance (the reference gates PE_M rows against per-row PE_M = 1 runs,
+# Makefile:1500-1506).  Two kinds of batch kernel serve the rows:
+# - the small-batch kernels (k_gemvs, k_gemvm) form every output in the single-row order, so
+#   row r of an M-row call is bit-identical to the one-row call on that row, fp32 included;
+# - the persistent multi-row kernel (passes of 2..8 rows, K = 2048/4096/6144, at most three
+#   8-row tiles per CU) forms its rows in its own order: a row agrees with its one-row call
+#   within the fast-mode tolerance (fp32 gate, bf16 within 1 ulp where well conditioned), and
+#   its bits depend neither on the other rows of the batch nor on its position -- reversing
+#   the batch, or sending the row in another batch, gives the same bits.  Exact
+#   speculative-verify == greedy therefore needs AIPU_MODE_REF (bit-exact in every shape).
+# Covers every row count of a verify batch at the BASELINE shape and the other matrix-core
+# shapes (ragged N, passes of 8 + remainder); above K = 7168 batches of 2+ rows fall back to
+# the streaming kernel's different summation order.
 INVARIANCE_CASES = [(6144, 6144, m) for m in (2, 3, 4, 5, 6, 7, 8)] + [
-    (4096, 4096, 4), (1001, 2048, 8), (300, 2304, 3), (512, 4096, 12), (64, 7168, 8),
+    (4096, 4096, 4), (1001, 2048, 8), (300, 2304, 3), (512, 4096, 12), (64, 7168, 8), (300, 4096, 9),
     # persistent multi-row kernel: three tiles per CU with a ragged last tile, two tiles per
-    # CU, a single tile, and one tile too many for it (the per-tile kernels take over)
+    # CU, a single tile, and one tile too many for it (the small-batch kernels take over)
     (6100, 6144, 3), (2050, 4096, 6), (8, 2048, 2), (6144 + 24, 6144, 8)]
+
+
+def _persistent_row(N, K, M, r):
+    """Whether row r of an M-row fast GEMV is served by the persistent multi-row kernel
+    (passes of 8 rows; a pass of one row goes to the single-row kernel)."""
+    left = min(M - (r // 8) * 8, 8)
+    return left >= 2 and K % 2048 == 0 and 2048 <= K <= 6144 and (N + 7) // 8 <= 3 * 256
 
 
 @pytest.mark.parametrize("N,K,M", INVARIANCE_CASES)
@@ -234,12 +247,38 @@ def test_gemv_fast_batch_invariance(N, K, M):
     raw = qo.random_q4k_blocks(rng, N * K // 256)
     x = qo.random_bf16(rng, (M, K))
     wd = d_u8(raw)
-    y, yf = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(x), mode="fast", out_f32=True)
-    yb, yfb = h_bits(y), u32(h_f32(yf))
+
+    def fast(rows):
+        y, yf = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(np.ascontiguousarray(rows)), mode="fast", out_f32=True)
+        return h_bits(y), u32(h_f32(yf))
+
+    yb, yfb = fast(x)
+    w = xf = None
+    pers = [r for r in range(M) if _persistent_row(N, K, M, r)]
+    if pers:
+        w = qo.dequant_q4k(raw).reshape(N, K)
+        xf = qo.bf16_bits_to_f32(x)
     for r in range(M):
-        y1, yf1 = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(x[r:r + 1]), mode="fast", out_f32=True)
-        assert_bits_equal(u32(h_f32(yf1))[0], yfb[r], f"row {r} of M={M}: fp32 accumulators")
-        assert_bits_equal(h_bits(y1)[0], yb[r], f"row {r} of M={M}: bf16 outputs")
+        y1, yf1 = fast(x[r:r + 1])
+        if r in pers:
+            f = yfb[r].view(np.float32)
+            ok, worst = qo.tolerance_gate(w, xf[r:r + 1], f[None, :], rel=1e-5)
+            assert ok, f"row {r} of M={M}: fp32 accumulators {worst:.3f} of the tolerance"
+            ok, max_ulp, _ = qo.bf16_parity(yb[r][None, :], yf1[0].view(np.float32)[None, :], w, xf[r:r + 1])
+            assert ok, f"row {r} of M={M}: bf16 {max_ulp} ulp from the one-row call"
+        else:
+            assert_bits_equal(yf1[0], yfb[r], f"row {r} of M={M}: fp32 accumulators")
+            assert_bits_equal(y1[0], yb[r], f"row {r} of M={M}: bf16 outputs")
+    if len(pers) == M and M <= 8:
+        # the same rows in reverse order, and each row again beside row 0 in a two-row batch
+        yr, yfr = fast(x[::-1])
+        for r in range(M):
+            assert_bits_equal(yfr[M - 1 - r], yfb[r], f"row {r} of M={M}, batch reversed: fp32 accumulators")
+            assert_bits_equal(yr[M - 1 - r], yb[r], f"row {r} of M={M}, batch reversed: bf16 outputs")
+        for r in range(1, M):
+            y2, yf2 = fast(np.stack([x[r], x[0]]))
+            assert_bits_equal(yf2[0], yfb[r], f"row {r} of M={M} in a two-row batch: fp32 accumulators")
+            assert_bits_equal(yf2[1], yfb[0], f"row 0 of M={M} in a two-row batch: fp32 accumulators")
 
 
 # Q6_K / Q8_0 / F16 through the mixed-type kernel: shapes where some waves own no blocks
