@@ -15,7 +15,7 @@
 //     against the 6-bit mins (exact in bf16).
 //   * Per super-block: acc += d * D1 - dmin * D2 (two fp32 FMAs per output).
 //
-// Pre-pass (k_prefill_rowexp, k_prefill_pack) writes the scaled activations into a caller
+// Pre-pass (k_prefill_stage; k_prefill_rowexp + k_prefill_pack for K > 32768) writes the scaled activations into a caller
 // workspace in the order the GEMM reads them: for each 128-row tile and super-block one
 // 72 KB chunk, [t][i][lane] 16-B MFMA operands (t = MFMA 0..7, i = 16-row subtile 0..7)
 // then [i][lane] 16-B sum operands, so the GEMM stages a chunk into LDS with straight
@@ -83,6 +83,17 @@ __device__ __forceinline__ void split3(float v, uint32_t& hi, uint32_t& mid, uin
     lo = __float_as_uint(r2) >> 16;
 }
 
+// The row exponent from the largest |x| bits of a row.
+__device__ __forceinline__ int row_exponent(uint32_t mx) {
+    int e = 0;
+    if (mx != 0 && mx < 0x7F80u) {
+        int ex;
+        (void)frexpf(bf16_to_f32(mx), &ex);   // max = f * 2^ex, f in [0.5, 1)
+        e = ex - 15;
+    }
+    return e;
+}
+
 // Row exponent e_m: the largest |x| of row m scaled by 2^-e_m lies in [2^14, 2^15).  Rows
 // that are all zero, hold inf/nan, or lie past M get e = 0.  One workgroup per row.
 __global__ __launch_bounds__(256) void k_prefill_rowexp(const uint16_t* __restrict__ X, int64_t K, int M,
@@ -108,46 +119,23 @@ __global__ __launch_bounds__(256) void k_prefill_rowexp(const uint16_t* __restri
     for (int s = 32; s >= 1; s >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, s, 64));
     if (lane == 0) part[tid >> 6] = mx;
     __syncthreads();
-    if (tid == 0) {
-        mx = max(max(part[0], part[1]), max(part[2], part[3]));
-        int e = 0;
-        if (mx != 0 && mx < 0x7F80u) {
-            int ex;
-            (void)frexpf(bf16_to_f32(mx), &ex);   // max = f * 2^ex, f in [0.5, 1)
-            e = ex - 15;
-        }
-        rexp[row] = e;
-    }
+    if (tid == 0) rexp[row] = row_exponent(max(max(part[0], part[1]), max(part[2], part[3])));
 }
 
-// Chunk (mt, b) of the workspace.  One thread per (row, sub-block s): it converts the 32
-// activations of the sub-block, writes them into the 8-byte halves of the eight operand
-// entries that carry them (sub-block s = 2c + hh sits in half hh of entries (t, g) with
-// (t < 4 ? 0 : 2) + (g >> 1) = c), and writes its exactly split sum into half s >> 2 of the
-// sum entry of lane group s & 3.  Rows past M get zeros.
-__global__ __launch_bounds__(256) void k_prefill_pack(const uint16_t* __restrict__ X, int64_t K, int M,
-                                                      const int32_t* __restrict__ rexp, uint8_t* __restrict__ ws,
-                                                      int nsb) {
-    const int b = blockIdx.x, mt = blockIdx.y;
-    const int item = blockIdx.z * 256 + threadIdx.x;   // 0 .. kBM * 8 - 1
-    const int ml = item >> 3, s = item & 7;
-    const int i = ml >> 4, r = ml & 15;
-    const int m = mt * kBM + ml;
-    uint8_t* chunk = ws + ((int64_t)mt * nsb + b) * kChunk;
+// One (row, sub-block) item of chunk (mt, b): the 32 activations w (bf16 pairs, in K order)
+// scaled by 2^-e into fp16, written into the 8-byte halves of the eight operand entries that
+// carry them (sub-block s = 2c + hh sits in half hh of entries (t, g) with
+// (t < 4 ? 0 : 2) + (g >> 1) = c), and their exactly split sum into half s >> 2 of the sum
+// entry of lane group s & 3.  valid = false (rows past M) writes zeros.
+__device__ __forceinline__ void pack_item(uint8_t* chunk, int i, int r, int s, const uint32_t (&w)[16], int e,
+                                          bool valid) {
     uint32_t v[32];
     float sum = 0.f;
-    if (m < M) {
-        const int e = rexp[m];
-        const uint4* src = (const uint4*)(X + (int64_t)m * K + (int64_t)b * QK_K + 32 * s);
+    if (valid) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint4 x = src[q];
-            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                v[8 * q + 2 * k] = f16_scaled(w[k], e);
-                v[8 * q + 2 * k + 1] = f16_scaled(w[k] >> 16, e);
-            }
+        for (int k = 0; k < 16; ++k) {
+            v[2 * k] = f16_scaled(w[k], e);
+            v[2 * k + 1] = f16_scaled(w[k] >> 16, e);
         }
 #pragma unroll
         for (int k = 0; k < 32; ++k) sum += __half2float(__ushort_as_half((unsigned short)v[k]));
@@ -168,8 +156,69 @@ __global__ __launch_bounds__(256) void k_prefill_pack(const uint16_t* __restrict
         }
     }
     uint32_t h = 0, md = 0, l = 0;
-    if (m < M) split3(sum, h, md, l);
+    if (valid) split3(sum, h, md, l);
     *(uint2*)(chunk + kChunkA + ((int64_t)i * 64 + 16 * (s & 3) + r) * 16 + 8 * (s >> 2)) = make_uint2(h | md << 16, l);
+}
+
+__device__ __forceinline__ void load_item(const uint16_t* X, int64_t K, int m, int item, uint32_t (&w)[16]) {
+    const uint4* src = (const uint4*)(X + (int64_t)m * K + 32 * (int64_t)item);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 x = src[q];
+        w[4 * q] = x.x;
+        w[4 * q + 1] = x.y;
+        w[4 * q + 2] = x.z;
+        w[4 * q + 3] = x.w;
+    }
+}
+
+// Chunk (mt, b) of the workspace, one thread per (row, sub-block s), with the row exponents
+// of k_prefill_rowexp (any K).
+__global__ __launch_bounds__(256) void k_prefill_pack(const uint16_t* __restrict__ X, int64_t K, int M,
+                                                      const int32_t* __restrict__ rexp, uint8_t* __restrict__ ws,
+                                                      int nsb) {
+    const int b = blockIdx.x, mt = blockIdx.y;
+    const int item = blockIdx.z * 256 + threadIdx.x;   // 0 .. kBM * 8 - 1
+    const int ml = item >> 3, s = item & 7;
+    const int m = mt * kBM + ml;
+    uint32_t w[16];
+    const bool valid = m < M;
+    if (valid) load_item(X, K, m, 8 * b + s, w);
+    pack_item(ws + ((int64_t)mt * nsb + b) * kChunk, ml >> 4, ml & 15, s, w, valid ? rexp[m] : 0, valid);
+}
+
+// Both staging steps in one pass (K <= kStageMaxK): one workgroup per padded row m, one
+// thread per sub-block of the row.  Each thread loads its 32 activations once, the
+// workgroup takes the row maximum of their |x| bits (the same maximum, so the same exponent,
+// as k_prefill_rowexp), and each thread packs its item as k_prefill_pack does.
+constexpr int64_t kStageMaxK = 1024 / 8 * QK_K;
+__global__ __launch_bounds__(1024) void k_prefill_stage(const uint16_t* __restrict__ X, int64_t K, int M,
+                                                        int32_t* __restrict__ rexp, uint8_t* __restrict__ ws,
+                                                        int nsb) {
+    __shared__ uint32_t part[16];
+    const int m = blockIdx.x, item = threadIdx.x, lane = item & 63;
+    const bool on = item < nsb * 8, valid = on && m < M;
+    uint32_t w[16];
+    uint32_t mx = 0;
+    if (valid) {
+        load_item(X, K, m, item, w);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            mx = max(mx, w[k] & 0x7FFFu);
+            mx = max(mx, (w[k] >> 16) & 0x7FFFu);
+        }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, d, 64));
+    if (lane == 0) part[item >> 6] = mx;
+    __syncthreads();
+    mx = 0;
+    for (int k = 0; k < (int)(blockDim.x >> 6); ++k) mx = max(mx, part[k]);
+    const int e = row_exponent(mx);
+    if (item == 0) rexp[m] = e;
+    if (!on) return;
+    const int mt = m / kBM, ml = m % kBM, b = item >> 3;
+    pack_item(ws + ((int64_t)mt * nsb + b) * kChunk, ml >> 4, ml & 15, item & 7, w, e, valid);
 }
 
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t off) {
@@ -461,9 +510,14 @@ hipError_t launch_gemm_prefill(int type, const void* w, int64_t N, int64_t K, co
     if ((int64_t)mtiles * ntiles > 0x7FFFFFFF || (int64_t)64 * nsb * 144 >= (1LL << 32)) return hipErrorInvalidValue;
     uint8_t* chunks = (uint8_t*)ws;
     int32_t* rexp = (int32_t*)(chunks + (int64_t)mtiles * nsb * kChunk);
-    hipLaunchKernelGGL(k_prefill_rowexp, dim3((unsigned)Mp), dim3(256), 0, st, x, K, (int)M, rexp);
-    hipLaunchKernelGGL(k_prefill_pack, dim3((unsigned)nsb, (unsigned)mtiles, kBM * 8 / 256), dim3(256), 0, st, x, K,
-                       (int)M, rexp, chunks, nsb);
+    if (K <= kStageMaxK) {
+        hipLaunchKernelGGL(k_prefill_stage, dim3((unsigned)Mp), dim3((unsigned)((nsb * 8 + 63) / 64 * 64)), 0, st, x, K,
+                           (int)M, rexp, chunks, nsb);
+    } else {
+        hipLaunchKernelGGL(k_prefill_rowexp, dim3((unsigned)Mp), dim3(256), 0, st, x, K, (int)M, rexp);
+        hipLaunchKernelGGL(k_prefill_pack, dim3((unsigned)nsb, (unsigned)mtiles, kBM * 8 / 256), dim3(256), 0, st, x, K,
+                           (int)M, rexp, chunks, nsb);
+    }
     hipLaunchKernelGGL(k_prefill_gemm, dim3((unsigned)(mtiles * ntiles)), dim3(kWaves * 64), 0, st,
                        (const uint8_t*)w, N, nsb, chunks, rexp, (int)M, y, y_f32, mtiles, (int)ntiles);
     return hipGetLastError();

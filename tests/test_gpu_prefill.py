@@ -40,7 +40,10 @@ def _check(raw, N, K, x_bits, y, yf, what):
 
 
 @pytest.mark.parametrize("M,N,K", [(130, 300, 512), (128, 256, 256), (1, 17, 768), (257, 520, 1024),
-                                   (64, 64, 2048), (200, 1000, 1536)])
+                                   (64, 64, 2048), (200, 1000, 1536),
+                                   # the largest K of the one-pass staging kernel, and past it the
+                                   # two-kernel staging (row exponents, then packing)
+                                   (5, 24, 32768), (3, 40, 33024)])
 def test_prefill_tolerance_shapes(M, N, K):
     note(f"prefill M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 7 + N * 3 + K)
