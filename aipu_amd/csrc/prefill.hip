@@ -187,38 +187,56 @@ __global__ __launch_bounds__(256) void k_prefill_pack(const uint16_t* __restrict
     pack_item(ws + ((int64_t)mt * nsb + b) * kChunk, ml >> 4, ml & 15, s, w, valid ? rexp[m] : 0, valid);
 }
 
-// Both staging steps in one pass (K <= kStageMaxK): one workgroup per padded row m, one
-// thread per sub-block of the row.  Each thread loads its 32 activations once, the
-// workgroup takes the row maximum of their |x| bits (the same maximum, so the same exponent,
-// as k_prefill_rowexp), and each thread packs its item as k_prefill_pack does.
-constexpr int64_t kStageMaxK = 1024 / 8 * QK_K;
+// Both staging steps in one pass (K <= kStageMaxK): one workgroup per kStageRows padded rows,
+// IPT items per thread.  Item j is (row j % kStageRows, sub-block j / kStageRows of the row),
+// so the 64 items of a wave write kStageRows neighbouring rows of each operand entry.  Each
+// thread loads its items' activations once, the workgroup takes each row's maximum of |x|
+// bits (the same maximum, so the same exponent, as k_prefill_rowexp), and each thread packs
+// its items as k_prefill_pack does.
+constexpr int kStageRows = 4;
+constexpr int kStageMaxIpt = 4;
+constexpr int64_t kStageMaxK = 1024 * kStageMaxIpt / (8 * kStageRows) * QK_K;
+template <int IPT>
 __global__ __launch_bounds__(1024) void k_prefill_stage(const uint16_t* __restrict__ X, int64_t K, int M,
                                                         int32_t* __restrict__ rexp, uint8_t* __restrict__ ws,
                                                         int nsb) {
-    __shared__ uint32_t part[16];
-    const int m = blockIdx.x, item = threadIdx.x, lane = item & 63;
-    const bool on = item < nsb * 8, valid = on && m < M;
-    uint32_t w[16];
+    constexpr int RW = kStageRows;
+    __shared__ uint32_t part[16][RW];
+    const int t = threadIdx.x, lane = t & 63, T = (int)blockDim.x;   // T: a multiple of 64
+    const int m = blockIdx.x * RW + t % RW;                            // the row of every item of t
+    const int nitems = RW * 8 * nsb;
+    const bool valid = m < M;
+    uint32_t w[IPT][16];
     uint32_t mx = 0;
-    if (valid) {
-        load_item(X, K, m, item, w);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            mx = max(mx, w[k] & 0x7FFFu);
-            mx = max(mx, (w[k] >> 16) & 0x7FFFu);
+    for (int k = 0; k < IPT; ++k) {
+        const int j = t + k * T;
+        if (j < nitems && valid) {
+            load_item(X, K, m, j / RW, w[k]);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                mx = max(mx, w[k][q] & 0x7FFFu);
+                mx = max(mx, (w[k][q] >> 16) & 0x7FFFu);
+            }
         }
     }
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, d, 64));
-    if (lane == 0) part[item >> 6] = mx;
+    for (int d = RW; d < 64; d <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, d, 64));
+    if (lane < RW) part[t >> 6][lane] = mx;
     __syncthreads();
     mx = 0;
-    for (int k = 0; k < (int)(blockDim.x >> 6); ++k) mx = max(mx, part[k]);
+    for (int v = 0; v < T / 64; ++v) mx = max(mx, part[v][t % RW]);
     const int e = row_exponent(mx);
-    if (item == 0) rexp[m] = e;
-    if (!on) return;
-    const int mt = m / kBM, ml = m % kBM, b = item >> 3;
-    pack_item(ws + ((int64_t)mt * nsb + b) * kChunk, ml >> 4, ml & 15, item & 7, w, e, valid);
+    if (t < RW) rexp[m] = e;
+    const int mt = m / kBM, ml = m % kBM;
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+        const int j = t + k * T;
+        if (j < nitems) {
+            const int g = j / RW;   // sub-block of the row
+            pack_item(ws + ((int64_t)mt * nsb + g / 8) * kChunk, ml >> 4, ml & 15, g & 7, w[k], e, valid);
+        }
+    }
 }
 
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t off) {
@@ -511,8 +529,16 @@ hipError_t launch_gemm_prefill(int type, const void* w, int64_t N, int64_t K, co
     uint8_t* chunks = (uint8_t*)ws;
     int32_t* rexp = (int32_t*)(chunks + (int64_t)mtiles * nsb * kChunk);
     if (K <= kStageMaxK) {
-        hipLaunchKernelGGL(k_prefill_stage, dim3((unsigned)Mp), dim3((unsigned)((nsb * 8 + 63) / 64 * 64)), 0, st, x, K,
-                           (int)M, rexp, chunks, nsb);
+        const int items = kStageRows * 8 * nsb;
+        const dim3 grid((unsigned)(Mp / kStageRows));
+        const auto threads = [&](int ipt) { return dim3((unsigned)((items + 64 * ipt - 1) / (64 * ipt) * 64)); };
+        if (items <= 1024)
+            hipLaunchKernelGGL(k_prefill_stage<1>, grid, threads(1), 0, st, x, K, (int)M, rexp, chunks, nsb);
+        else if (items <= 2048)
+            hipLaunchKernelGGL(k_prefill_stage<2>, grid, threads(2), 0, st, x, K, (int)M, rexp, chunks, nsb);
+        else
+            hipLaunchKernelGGL(k_prefill_stage<kStageMaxIpt>, grid, threads(kStageMaxIpt), 0, st, x, K, (int)M, rexp,
+                               chunks, nsb);
     } else {
         hipLaunchKernelGGL(k_prefill_rowexp, dim3((unsigned)Mp), dim3(256), 0, st, x, K, (int)M, rexp);
         hipLaunchKernelGGL(k_prefill_pack, dim3((unsigned)nsb, (unsigned)mtiles, kBM * 8 / 256), dim3(256), 0, st, x, K,
