@@ -46,7 +46,10 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
                                                              const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
                                                              float* __restrict__ Yf, int ntiles) {
     constexpr int NB = TT < 3 ? TT : 3;                        // tile buffers
-    constexpr int Q = 4 < (NB - 1) * R + 1 ? 4 : (NB - 1) * R + 1;   // rounds in flight (see the reuse wait)
+    // rounds in flight: up to 4; with buffer reuse (TT > NB) at most (NB - 1) R + 1 (see the
+    // reuse wait), without it at most the TT R rounds there are
+    constexpr int QL = TT <= NB ? TT * R : (NB - 1) * R + 1;
+    constexpr int Q = 4 < QL ? 4 : QL;
     static_assert(Q >= 1 && 8 * Q <= 63, "rounds in flight within vmcnt");
     extern __shared__ __align__(16) uint8_t s_tile[];          // NB * 8 * pitch (direct-to-LDS targets only)
     __shared__ __align__(16) uint8_t s_stage[kPMaxPairs * kPStage];
