@@ -21,6 +21,7 @@ TYPE_Q6_K = 14
 TYPE_BF16 = 30
 MODE_FAST = 0
 MODE_REF = 1
+MODE_FAST_DENSE = 2
 PREFILL_CODES = 0
 MAX_TILES = 64
 

@@ -95,7 +95,7 @@ bool has_fast(int type, int64_t K) {
 
 extern "C" {
 
-int aipu_version(void) { return 100; }
+int aipu_version(void) { return 200; }
 
 const char* aipu_last_error(void) { return g_err.c_str(); }
 
@@ -138,10 +138,14 @@ int aipu_gemv_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t 
 
 int aipu_gemv(int ggml_type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
               float* y_f32, int mode, void* stream) {
+    if (mode != AIPU_MODE_FAST && mode != AIPU_MODE_REF && mode != AIPU_MODE_FAST_DENSE)
+        return fail(AIPU_ERR_ARG, "mode must be 0 (fast), 1 (ref) or 2 (fast, dense batches)");
+    const bool dense = mode == AIPU_MODE_FAST_DENSE;
+    if (dense) mode = AIPU_MODE_FAST;   // the same arguments, alignment and kernels but for Q4_K batches
     int rc = check_gemv(ggml_type, w, N, K, x, M, y, y_f32, mode, false);
     if (rc) return rc;
     if (mode == AIPU_MODE_FAST && has_fast(ggml_type, K))
-        return hip_status(aipu::launch_gemv_fast(ggml_type, w, N, K, x, M, y, y_f32, S(stream)), "aipu_gemv");
+        return hip_status(aipu::launch_gemv_fast(ggml_type, w, N, K, x, M, y, y_f32, S(stream), dense), "aipu_gemv");
     return hip_status(aipu::launch_gemv_ref(ggml_type, w, N, K, x, M, y, y_f32, S(stream)), "aipu_gemv");
 }
 

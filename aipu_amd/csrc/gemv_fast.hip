@@ -707,10 +707,12 @@ hipError_t gemv_stream_mc(const uint8_t* W, int64_t N, int64_t K, const uint16_t
 }  // namespace
 
 hipError_t launch_gemv_fast(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
-                            float* y_f32, hipStream_t st) {
+                            float* y_f32, hipStream_t st, bool dense) {
     switch (type) {
         case T_Q4_K:
-            if (gemv_mfma_supported(N, K, M)) return launch_gemv_mfma(w, N, K, x, M, y, y_f32, N, st);
+            // the matrix-core dispatch serves every M wherever it serves one row (rows without a
+            // multi-row kernel in the one-row order run one launch each)
+            if (gemv_mfma_supported(N, K, 1)) return launch_gemv_mfma(w, N, K, x, M, y, y_f32, N, st, dense);
             return gemv_stream_mc<T_Q4_K, 4>((const uint8_t*)w, N, K, x, M, y, y_f32, st);
         case T_BF16: return gemv_stream_mc<T_BF16, 2>((const uint8_t*)w, N, K, x, M, y, y_f32, st);
         case T_Q6_K:

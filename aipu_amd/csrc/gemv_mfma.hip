@@ -1084,48 +1084,51 @@ bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M) {
 }
 
 // y[M][N] (row stride ystride) = x[M][K] . W^T, in passes of at most 8 activation rows.
+// A pass goes to a multi-row kernel only if that kernel forms each row exactly as the one-row
+// launch does (the persistent row-pair kernel, k_gemvm, k_gemvs: the order of mfma_gemv.hpp,
+// which the single-row kernels k_gemv1p and k_gemv1 follow); every other row runs as its own
+// one-row launch, so each row of the result is bit-identical to the one-row call on that row
+// at every shape.  `dense` swaps the persistent row-pair kernel for the dense one (rows within
+// the tolerance of their one-row results); nothing else changes.
 hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
-                            float* y_f32, int64_t ystride, hipStream_t st) {
+                            float* y_f32, int64_t ystride, hipStream_t st, bool dense) {
     const uint8_t* W = (const uint8_t*)w;
     const int nsb = (int)(K / QK_K);
     PlanS ps;
     const bool small = make_plans(nsb, ps);
+    Plan1 p1;
+    const bool canon1 = gemv_persist_supported(N, K) || make_plan1(nsb, 1, kMaxW, p1);   // one-row launch in that order
     for (int64_t m0 = 0; m0 < M;) {
         const int left = (int)(M - m0 < 8 ? M - m0 : 8);
-        if (left >= 2 && gemv_persist_m_supported(N, K, left)) {   // two to eight rows, one persistent pass
-            const hipError_t e = launch_gemv_persist_m(W, N, K, x + m0 * K, left, y + m0 * ystride,
-                                                       y_f32 ? y_f32 + m0 * ystride : nullptr, ystride, st);
-            if (e != hipSuccess) return e;
-            m0 += left;
-            continue;
-        }
-        if (left >= 5 && gemvm_supported(nsb, 8)) {   // five to eight rows in one pass
-            const ProbPlain<8> pb{W, N, row_bytes(T_Q4_K, K), y + m0 * ystride, y_f32 ? y_f32 + m0 * ystride : nullptr,
-                                  ystride, left};
-            const hipError_t e = run_gemvm<8>(pb, nsb, (unsigned)((N + kTR - 1) / kTR), x + m0 * K, (int)K, st);
-            if (e != hipSuccess) return e;
-            m0 += left;
-            continue;
-        }
-        if (small && left >= 2) {   // two to four rows, the weights read once
-            const int mr = left < kSmallMaxRows ? left : kSmallMaxRows;
-            const ProbPlain<4> pb{W, N, row_bytes(T_Q4_K, K), y + m0 * ystride, y_f32 ? y_f32 + m0 * ystride : nullptr,
-                                  ystride, mr};
-            const hipError_t e = runs(pb, ps, (unsigned)((N + kTR - 1) / kTR), x + m0 * K, (int)K, st);
-            if (e != hipSuccess) return e;
-            m0 += mr;
-            continue;
-        }
-        const int mr = (int)(M - m0 < 4 ? M - m0 : 4);
         const uint16_t* xm = x + m0 * K;
         uint16_t* ym = y + m0 * ystride;
         float* yfm = y_f32 ? y_f32 + m0 * ystride : nullptr;
-        hipError_t e;
-        if (mr == 1) e = plain_pass<1>(W, N, K, xm, 1, ym, yfm, ystride, st);
-        else if (mr == 2) e = plain_pass<2>(W, N, K, xm, 2, ym, yfm, ystride, st);
-        else e = plain_pass<4>(W, N, K, xm, mr, ym, yfm, ystride, st);
+        if (left >= 2 && canon1) {
+            if (gemv_persist_m_supported(N, K, left, dense)) {   // two to eight rows, one persistent pass
+                const hipError_t e = launch_gemv_persist_m(W, N, K, xm, left, ym, yfm, ystride, dense, st);
+                if (e != hipSuccess) return e;
+                m0 += left;
+                continue;
+            }
+            if (left >= 5 && gemvm_supported(nsb, 8)) {   // five to eight rows in one pass
+                const ProbPlain<8> pb{W, N, row_bytes(T_Q4_K, K), ym, yfm, ystride, left};
+                const hipError_t e = run_gemvm<8>(pb, nsb, (unsigned)((N + kTR - 1) / kTR), xm, (int)K, st);
+                if (e != hipSuccess) return e;
+                m0 += left;
+                continue;
+            }
+            if (small) {   // two to four rows, the weights read once
+                const int mr = left < kSmallMaxRows ? left : kSmallMaxRows;
+                const ProbPlain<4> pb{W, N, row_bytes(T_Q4_K, K), ym, yfm, ystride, mr};
+                const hipError_t e = runs(pb, ps, (unsigned)((N + kTR - 1) / kTR), xm, (int)K, st);
+                if (e != hipSuccess) return e;
+                m0 += mr;
+                continue;
+            }
+        }
+        const hipError_t e = plain_pass<1>(W, N, K, xm, 1, ym, yfm, ystride, st);
         if (e != hipSuccess) return e;
-        m0 += mr;
+        ++m0;
     }
     return hipSuccess;
 }

@@ -44,7 +44,7 @@ hipError_t launch_gemv_ref_f32(const float* w, int64_t N, int64_t K, const float
 
 // gemv_fast.hip -- tolerance-mode streaming GEMV
 hipError_t launch_gemv_fast(int type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
-                            uint16_t* y, float* y_f32, hipStream_t st);
+                            uint16_t* y, float* y_f32, hipStream_t st, bool dense = false);
 hipError_t launch_gemv_tiles(const aipu_tile_desc* tiles, int n_tiles, int64_t N, int64_t K, const uint16_t* x,
                              int64_t M, uint16_t* y, float* y_f32, int mode, hipStream_t st);
 
@@ -60,16 +60,19 @@ hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uin
                                hipStream_t st);
 
 // gemv_persist_m.hip -- persistent Q4_K GEMV for 2 .. 8 activation rows (tolerance mode,
-// K = 2048, 4096, 6144, at most three 8-row tiles per CU); a row's result does not depend on
-// the other rows of the batch, and agrees with the single-row kernels within the tolerance
-bool gemv_persist_m_supported(int64_t N, int64_t K, int64_t M);
+// K = 2048, 4096, 6144, at most three 8-row tiles per CU).  dense = false: row m is
+// bit-identical to the single-row kernels; dense = true: a row agrees with them within the
+// tolerance (and does not depend on the other rows of the batch)
+bool gemv_persist_m_supported(int64_t N, int64_t K, int64_t M, bool dense);
 hipError_t launch_gemv_persist_m(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
-                                 float* yf, int64_t ys, hipStream_t st);
+                                 float* yf, int64_t ys, bool dense, hipStream_t st);
 
-// gemv_mfma.hip -- matrix-core Q4_K GEMV (tolerance mode)
+// gemv_mfma.hip -- matrix-core Q4_K GEMV (tolerance mode).  dense = false: every row of a
+// batch is bit-identical to the one-row launch on that row; dense = true allows the dense
+// multi-row kernel (rows within the tolerance of their one-row results)
 bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M);
 hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
-                            float* y_f32, int64_t ystride, hipStream_t st);
+                            float* y_f32, int64_t ystride, hipStream_t st, bool dense = false);
 bool moe_mfma_supported(int nslots, int64_t H, int64_t I);
 // Routing source of the gate/up leg: either `sel` (expert ids already decided) or, when
 // `logits` is set, the kernel routes from the logits itself and workgroup 0 publishes the

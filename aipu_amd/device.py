@@ -12,7 +12,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import (MODE_FAST, MODE_REF, TYPE_BF16, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, TileDesc, call)
+from ._lib import (MODE_FAST, MODE_FAST_DENSE, MODE_REF, TYPE_BF16, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, TileDesc, call)
 
 QK = {TYPE_Q4_K: 256, TYPE_Q6_K: 256, TYPE_Q8_0: 32, TYPE_F16: 1, TYPE_BF16: 1}
 BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_F16: 2, TYPE_BF16: 2}
@@ -29,6 +29,13 @@ def _mode(mode):
     if mode in (MODE_REF, "ref"):
         return MODE_REF
     raise ValueError(f"mode must be 'fast' or 'ref', got {mode!r}")
+
+
+def _gemv_mode(mode):
+    """aipu_gemv also takes 'fast_dense' (dense multi-row Q4_K batches, rows within tolerance)."""
+    if mode in (MODE_FAST_DENSE, "fast_dense"):
+        return MODE_FAST_DENSE
+    return _mode(mode)
 
 
 def _stream(t):
@@ -96,7 +103,10 @@ def gemv_f32(w, x, out_f32=False):
 
 
 def gemv(ggml_type, w, N, K, x, mode="fast", out=None, out_f32=False):
-    """y[M,N] = bf16(x[M,K] . dequant(w)^T).  Returns y (and the fp32 accumulators)."""
+    """y[M,N] = bf16(x[M,K] . dequant(w)^T).  Returns y (and the fp32 accumulators).
+
+    mode: "fast", "ref" or "fast_dense" (Q4_K batches of 2..8 rows on the dense multi-row
+    kernel, rows within the tolerance of their one-row results)."""
     _need_cuda(w, x)
     x = _bf16(x)
     if x.dim() == 1:
@@ -104,7 +114,7 @@ def gemv(ggml_type, w, N, K, x, mode="fast", out=None, out_f32=False):
     M = x.shape[0]
     y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     yf = torch.empty((M, N), dtype=torch.float32, device=x.device) if out_f32 else None
-    call("aipu_gemv", ggml_type, _ptr(w), N, K, _ptr(x), M, _ptr(y), _ptr(yf), _mode(mode), _stream(x))
+    call("aipu_gemv", ggml_type, _ptr(w), N, K, _ptr(x), M, _ptr(y), _ptr(yf), _gemv_mode(mode), _stream(x))
     return (y, yf) if out_f32 else y
 
 

@@ -20,7 +20,9 @@
  *       sequential fp32 MAC in K order, bf16 RNE; tools/q4k_ref.py:67-92).
  *       AIPU_MODE_FAST is the bandwidth-optimised path: dequantised weights are exact, fp32
  *       accumulators are within 1e-5 * sum|a*w| of exact, bf16 outputs within 1 ulp of
- *       AIPU_MODE_REF.  Both are deterministic (run-to-run bitwise identical).
+ *       AIPU_MODE_REF.  Both are deterministic (run-to-run bitwise identical).  In both, row m
+ *       of a multi-row GEMV is bit-identical to the one-row call on that row (a speculative-
+ *       verify batch reproduces greedy decoding, the reference's PE_M gate, Makefile:1488-1508).
  */
 #ifndef AIPU_Q4K_H
 #define AIPU_Q4K_H
@@ -39,8 +41,9 @@ extern "C" {
 #define AIPU_TYPE_Q6_K 14
 #define AIPU_TYPE_BF16 30
 
-#define AIPU_MODE_FAST 0
-#define AIPU_MODE_REF  1
+#define AIPU_MODE_FAST       0
+#define AIPU_MODE_REF        1
+#define AIPU_MODE_FAST_DENSE 2   /* aipu_gemv only: see there */
 
 #define AIPU_OK             0
 #define AIPU_ERR_ARG       -1   /* null pointer or bad enum */
@@ -86,11 +89,13 @@ int aipu_gemv_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t 
  * 256-weight super-blocks along K for every type, as the reference's datapath does (a Q8_0
  * super-block is 8 blocks of 32; src/glm_matmul_q4k.v:90-91, tools/q4k_mixed_gen.py:131,143,296).
  * y_f32 (nullable) receives the fp32 accumulators.  M >= 1 (M = K+1 <= 8 for speculative
- * verification batches; large M is served too, see aipu_gemm_prefill).  In AIPU_MODE_FAST the
- * rows of a Q4_K batch may differ from their one-row results within the fast-mode tolerance
- * (the multi-row kernel sums in its own order; within batches of 2..8 rows a row's bits do not
- * depend on the other rows or on its position); use AIPU_MODE_REF where a verify batch must
- * reproduce one-row decoding bit for bit. */
+ * verification batches; large M is served too, see aipu_gemm_prefill).  In AIPU_MODE_FAST and
+ * AIPU_MODE_REF each row of the result is bit-identical to the one-row call on that row, for
+ * every type and shape.  AIPU_MODE_FAST_DENSE is AIPU_MODE_FAST except for Q4_K batches of
+ * 2..8 rows at K = 2048, 4096, 6144: those run the dense multi-row kernel, whose rows agree with
+ * their one-row results within the fast-mode tolerance only (a row's bits still depend neither
+ * on the other rows nor on its position in the batch); for callers that batch independent rows
+ * and do not need batch == one-row bits (it is faster from four rows on). */
 int aipu_gemv(int ggml_type, const void* w, int64_t N, int64_t K, const uint16_t* x, int64_t M,
               uint16_t* y, float* y_f32, int mode, void* stream);
 

@@ -326,6 +326,54 @@ def router_logits(router_type, router_w, E, H, x_bits):
 BF16_TYPE = 30
 
 
+def router_logits_fast_order(rw_bits, E, H, x_bits, dot2="fused"):
+    """bf16 router GEMV in the order of the fast-mode router kernel -- a MODEL of this
+    repository's kernel (aipu_amd/csrc/route.hpp: router_wave_dot, router_logit), not of the
+    reference, used to measure how often fast-mode routing departs from the reference order.
+
+    256 threads per logit; thread t folds the 16-byte chunks c = 8t + 2048u (u = 0, 1, ...)
+    in increasing K into two fp32 partials: element pairs (c, c+1) and (c+4, c+5) into s0,
+    (c+2, c+3) and (c+6, c+7) into s1, one two-element dot product per pair; then s0 + s1; the
+    64 lanes of a wave are summed by a butterfly (xor 32, 16, ..., 1); the four wave sums are
+    added in wave order starting from +0; bf16 RNE.  ``dot2`` models the two-element dot
+    product: "fused" rounds s + a0*w0 + a1*w1 once, "chain" rounds after each product.
+    ``x_bits`` is bf16[H] or bf16[B, H]; returns bf16 logits [E] or [B, E].
+    """
+    w = qo.bf16_bits_to_f32(np.asarray(rw_bits, np.uint16).reshape(E, H)).astype(np.float64)
+    xb = np.asarray(x_bits, np.uint16)
+    single = xb.ndim == 1
+    x = qo.bf16_bits_to_f32(np.atleast_2d(xb)).astype(np.float64)
+    B = x.shape[0]
+    T = 256
+    s = [np.zeros((B, E, T), np.float32), np.zeros((B, E, T), np.float32)]
+    t8 = 8 * np.arange(T)
+    with np.errstate(over="ignore", invalid="ignore"):
+        for c0 in range(0, H, 2048):
+            for pair in range(4):
+                idx = c0 + t8 + 2 * pair
+                ok = idx < H
+                i0, i1 = np.where(ok, idx, 0), np.where(ok, idx + 1, 0)
+                p0 = x[:, None, i0] * w[None, :, i0]          # exact: bf16 x bf16
+                p1 = x[:, None, i1] * w[None, :, i1]
+                p0 = np.where(ok, p0, 0.0)
+                p1 = np.where(ok, p1, 0.0)
+                acc = s[pair & 1]
+                if dot2 == "fused":
+                    acc[...] = (acc.astype(np.float64) + (p0 + p1)).astype(np.float32)
+                else:
+                    acc[...] = (acc + p0.astype(np.float32)).astype(np.float32)
+                    acc[...] = (acc + p1.astype(np.float32)).astype(np.float32)
+        v = (s[0] + s[1]).astype(np.float32).reshape(B, E, 4, 64)
+        lane = np.arange(64)
+        for off in (32, 16, 8, 4, 2, 1):
+            v = (v + v[..., lane ^ off]).astype(np.float32)
+        tot = np.zeros((B, E), np.float32)
+        for wv in range(4):
+            tot = (tot + v[:, :, wv, 0]).astype(np.float32)
+    out = qo.bf16_round_bits(tot)
+    return out[0] if single else out
+
+
 def moe_decode_ref(x_bits, router_type, router_w, experts, ggml_type, E, H, I, topk,
                    scale_bits=0x40200000, shared=None):
     """Whole MoE FFN decode step in reference order.

@@ -58,6 +58,10 @@ def test_gemv_validation():
     assert f(12, FAKE_ODD, 64, 256, FAKE, 1, FAKE, NULL, 0, S) == ALIGN
     assert f(12, FAKE, 64, 256, ctypes.c_void_p(0x100008), 1, FAKE, NULL, 0, S) == ALIGN  # fast mode wants 16 B
     assert f(12, FAKE, 64, 256, FAKE, 1, FAKE, NULL, 7, S) == ARG
+    # AIPU_MODE_FAST_DENSE: the fast mode's checks (16-B activations); other entry points refuse it
+    assert f(12, FAKE, 64, 256, ctypes.c_void_p(0x100008), 1, FAKE, NULL, 2, S) == ALIGN
+    assert f(12, FAKE, 64, 100, FAKE, 1, FAKE, NULL, 2, S) == SHAPE
+    assert L().aipu_swiglu_expert(12, FAKE, FAKE, FAKE, 256, 256, FAKE, FAKE, NULL, 2, FAKE, 1 << 20, S) == ARG
     assert f(8, FAKE, 64, 48, FAKE, 1, FAKE, NULL, 1, S) == SHAPE     # Q8_0: K = 48 is not a whole number of blocks
 
 

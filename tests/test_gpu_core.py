@@ -189,6 +189,9 @@ FAST_CASES = [
     (64, 9216, 1), (40, 12288, 1),
     # N / #CUs rows per workgroup (two tiles, the second partly or barely filled)
     (4100, 2048, 1), (7000, 6144, 1),
+    # the persistent single-row kernel at its largest K (five copy rounds per tile, two pairs
+    # per compute wave): 32 and 29 blocks, and a shape with N > 6144 that reuses tile buffers
+    (300, 8192, 1), (64, 7424, 1), (7000, 8192, 1),
 ]
 
 
@@ -213,31 +216,31 @@ def test_gemv_fast_tolerance(N, K, M):
     assert np.array_equal(u32(h_f32(yf2)), u32(h_f32(yf)))
 
 
-# Fast-mode batch invariance (the reference gates PE_M rows against per-row PE_M = 1 runs,
-# Makefile:1500-1506).  Two kinds of batch kernel serve the rows:
-# - the small-batch kernels (k_gemvs, k_gemvm) form every output in the single-row order, so
-#   row r of an M-row call is bit-identical to the one-row call on that row, fp32 included;
-# - the persistent multi-row kernel (passes of 2..8 rows, K = 2048/4096/6144, at most three
-#   8-row tiles per CU) forms its rows in its own order: a row agrees with its one-row call
-#   within the fast-mode tolerance (fp32 gate, bf16 within 1 ulp where well conditioned), and
-#   its bits depend neither on the other rows of the batch nor on its position -- reversing
-#   the batch, or sending the row in another batch, gives the same bits.  Exact
-#   speculative-verify == greedy therefore needs AIPU_MODE_REF (bit-exact in every shape).
-# Covers every row count of a verify batch at the BASELINE shape and the other matrix-core
-# shapes (ragged N, passes of 8 + remainder); above K = 7168 batches of 2+ rows fall back to
-# the streaming kernel's different summation order.
+# Fast-mode batch invariance: the reference gates PE_M = 2 rows bit-exact against per-row
+# PE_M = 1 runs (Makefile:1488-1508), and speculative decoding "changes speed, never output"
+# (PROJECT_BRIEFING.md:50).  In fast mode every row of an M-row call is bit-identical to the
+# one-row call on that row, fp32 accumulators included: the persistent row-pair kernel
+# (M = 2..8 at K = 2048/4096/6144), k_gemvs / k_gemvm elsewhere, and a launch per row where no
+# multi-row kernel forms rows in the one-row order (K / 256 not split into at most 8 parts of
+# at most 4 blocks: 2816, 5632; M = 1 off the persistent kernel: K > 8192), and the streaming
+# kernel beyond the matrix-core staging limit.
+# Covers every row count of a verify batch at the BASELINE shape, the other matrix-core shapes
+# (ragged N, passes of 8 + remainder), the shapes without a multi-row kernel, and K > 8192.
 INVARIANCE_CASES = [(6144, 6144, m) for m in (2, 3, 4, 5, 6, 7, 8)] + [
     (4096, 4096, 4), (1001, 2048, 8), (300, 2304, 3), (512, 4096, 12), (64, 7168, 8), (300, 4096, 9),
-    # persistent multi-row kernel: three tiles per CU with a ragged last tile, two tiles per
+    # persistent row-pair kernel: three tiles per CU with a ragged last tile, two tiles per
     # CU, a single tile, and one tile too many for it (the small-batch kernels take over)
-    (6100, 6144, 3), (2050, 4096, 6), (8, 2048, 2), (6144 + 24, 6144, 8)]
+    (6100, 6144, 3), (2050, 4096, 6), (8, 2048, 2), (6144 + 24, 6144, 8),
+    # no multi-row kernel in the one-row order: one launch per row
+    (300, 2816, 5), (64, 5632, 2),
+    # K > 8192: the one-row kernel is k_gemv1 (several weight-copy rounds); beyond the
+    # matrix-core staging limit (K > 30464) every M runs the streaming kernel
+    (64, 9216, 3), (40, 12288, 5), (64, 18432, 8), (16, 32768, 3)]
 
 
-def _persistent_row(N, K, M, r):
-    """Whether row r of an M-row fast GEMV is served by the persistent multi-row kernel
-    (passes of 8 rows; a pass of one row goes to the single-row kernel)."""
-    left = min(M - (r // 8) * 8, 8)
-    return left >= 2 and K % 2048 == 0 and 2048 <= K <= 6144 and (N + 7) // 8 <= 3 * 256
+def _fast_rows(t, wd, N, K, rows, mode):
+    y, yf = dev.gemv(t, wd, N, K, d_bf16(np.ascontiguousarray(rows)), mode=mode, out_f32=True)
+    return h_bits(y), u32(h_f32(yf))
 
 
 @pytest.mark.parametrize("N,K,M", INVARIANCE_CASES)
@@ -247,20 +250,62 @@ def test_gemv_fast_batch_invariance(N, K, M):
     raw = qo.random_q4k_blocks(rng, N * K // 256)
     x = qo.random_bf16(rng, (M, K))
     wd = d_u8(raw)
-
-    def fast(rows):
-        y, yf = dev.gemv(qo.GGML_Q4_K, wd, N, K, d_bf16(np.ascontiguousarray(rows)), mode="fast", out_f32=True)
-        return h_bits(y), u32(h_f32(yf))
-
-    yb, yfb = fast(x)
-    w = xf = None
-    pers = [r for r in range(M) if _persistent_row(N, K, M, r)]
-    if pers:
-        w = qo.dequant_q4k(raw).reshape(N, K)
-        xf = qo.bf16_bits_to_f32(x)
+    yb, yfb = _fast_rows(qo.GGML_Q4_K, wd, N, K, x, "fast")
     for r in range(M):
-        y1, yf1 = fast(x[r:r + 1])
-        if r in pers:
+        y1, yf1 = _fast_rows(qo.GGML_Q4_K, wd, N, K, x[r:r + 1], "fast")
+        assert_bits_equal(yf1[0], yfb[r], f"row {r} of M={M}: fp32 accumulators")
+        assert_bits_equal(y1[0], yb[r], f"row {r} of M={M}: bf16 outputs")
+    # and the batch itself meets the tolerance gate (the one-row kernel's contract)
+    w = qo.dequant_q4k(raw).reshape(N, K)
+    ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), yfb.view(np.float32), rel=1e-5)
+    assert ok, f"batch of M={M}: fp32 accumulators {worst:.3f} of the tolerance"
+
+
+@pytest.mark.parametrize("N,K,M", [(300, 4096, 2), (513, 6144, 3), (4100, 4096, 4)])
+def test_gemv_fast_batch_invariance_bf16(N, K, M):
+    """bf16 weights (the router's type) in the streaming kernel: batch rows == one-row calls."""
+    note(f"gemv fast bf16 batch invariance N={N} K={K} M={M}")
+    rng = np.random.default_rng(11 * N + K + M)
+    wb = qo.random_bf16(rng, (N, K), scale=0.05)
+    x = qo.random_bf16(rng, (M, K))
+    wd = d_u8(wb.view(np.uint8).reshape(-1))
+    yb, yfb = _fast_rows(go.BF16_TYPE, wd, N, K, x, "fast")
+    for r in range(M):
+        y1, yf1 = _fast_rows(go.BF16_TYPE, wd, N, K, x[r:r + 1], "fast")
+        assert_bits_equal(yf1[0], yfb[r], f"bf16 row {r} of M={M}: fp32 accumulators")
+        assert_bits_equal(y1[0], yb[r], f"bf16 row {r} of M={M}: bf16 outputs")
+
+
+# AIPU_MODE_FAST_DENSE: Q4_K batches of 2..8 rows at K = 2048/4096/6144 run the dense
+# multi-row kernel.  A row agrees with its one-row call within the fast-mode tolerance (fp32
+# gate, bf16 within 1 ulp where well conditioned), and its bits depend neither on the other
+# rows of the batch nor on its position -- reversing the batch, or sending the row in another
+# batch, gives the same bits.  Shapes it does not serve behave as AIPU_MODE_FAST.
+DENSE_CASES = [(6144, 6144, m) for m in (2, 4, 7, 8)] + [
+    (6100, 6144, 3), (2050, 4096, 6), (8, 2048, 2), (1001, 2048, 8), (6144 + 24, 6144, 8), (300, 2816, 5)]
+
+
+def _dense_row(N, K, M, r):
+    """Whether row r of an M-row dense-mode GEMV is served by the dense multi-row kernel
+    (passes of 8 rows; a pass of one row goes to the single-row kernel)."""
+    left = min(M - (r // 8) * 8, 8)
+    return left >= 2 and K % 2048 == 0 and 2048 <= K <= 6144 and (N + 7) // 8 <= 3 * 256
+
+
+@pytest.mark.parametrize("N,K,M", DENSE_CASES)
+def test_gemv_fast_dense_batch(N, K, M):
+    note(f"gemv fast_dense batch N={N} K={K} M={M}")
+    rng = np.random.default_rng(7 * N + K + M)
+    raw = qo.random_q4k_blocks(rng, N * K // 256)
+    x = qo.random_bf16(rng, (M, K))
+    wd = d_u8(raw)
+    yb, yfb = _fast_rows(qo.GGML_Q4_K, wd, N, K, x, "fast_dense")
+    w = qo.dequant_q4k(raw).reshape(N, K)
+    xf = qo.bf16_bits_to_f32(x)
+    dense = [r for r in range(M) if _dense_row(N, K, M, r)]
+    for r in range(M):
+        y1, yf1 = _fast_rows(qo.GGML_Q4_K, wd, N, K, x[r:r + 1], "fast_dense")
+        if r in dense:
             f = yfb[r].view(np.float32)
             ok, worst = qo.tolerance_gate(w, xf[r:r + 1], f[None, :], rel=1e-5)
             assert ok, f"row {r} of M={M}: fp32 accumulators {worst:.3f} of the tolerance"
@@ -269,14 +314,14 @@ def test_gemv_fast_batch_invariance(N, K, M):
         else:
             assert_bits_equal(yf1[0], yfb[r], f"row {r} of M={M}: fp32 accumulators")
             assert_bits_equal(y1[0], yb[r], f"row {r} of M={M}: bf16 outputs")
-    if len(pers) == M and M <= 8:
+    if len(dense) == M and M <= 8:
         # the same rows in reverse order, and each row again beside row 0 in a two-row batch
-        yr, yfr = fast(x[::-1])
+        yr, yfr = _fast_rows(qo.GGML_Q4_K, wd, N, K, x[::-1], "fast_dense")
         for r in range(M):
             assert_bits_equal(yfr[M - 1 - r], yfb[r], f"row {r} of M={M}, batch reversed: fp32 accumulators")
             assert_bits_equal(yr[M - 1 - r], yb[r], f"row {r} of M={M}, batch reversed: bf16 outputs")
         for r in range(1, M):
-            y2, yf2 = fast(np.stack([x[r], x[0]]))
+            y2, yf2 = _fast_rows(qo.GGML_Q4_K, wd, N, K, np.stack([x[r], x[0]]), "fast_dense")
             assert_bits_equal(yf2[0], yfb[r], f"row {r} of M={M} in a two-row batch: fp32 accumulators")
             assert_bits_equal(yf2[1], yfb[0], f"row 0 of M={M} in a two-row batch: fp32 accumulators")
 
