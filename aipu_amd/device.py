@@ -179,6 +179,16 @@ def moe_workspace(E, H, I, topk, device):
     return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
+def moe_workspace_views(ws, E, I, nslots):
+    """The step's router logits (E bf16) and per-slot h (nslots x I bf16) inside a MoE
+    workspace after aipu_moe_swiglu_decode / aipu_moe_layer_decode (include/aipu_q4k.h
+    documents the offsets)."""
+    h0 = 256 * ((E + 127) // 128) + 512
+    logits = ws[:2 * E].view(torch.bfloat16)
+    h = ws[h0:h0 + 2 * nslots * I].view(torch.bfloat16).view(nslots, I)
+    return logits, h
+
+
 def swiglu_expert(ggml_type, wg, wu, wd, H, I, x, mode="fast", workspace=None, return_h=False):
     """One SwiGLU expert (tools/glm_model_q4k_ref.py:702-708) on device tensors."""
     _need_cuda(wg, wu, wd, x)

@@ -138,7 +138,10 @@ int aipu_router_topk(const uint16_t* logits, int64_t E, int topk, uint32_t scale
 /* Workspace bytes for aipu_swiglu_expert / aipu_moe_swiglu_decode.  The workspace holds the
  * router logits, the routing decision, h and per-slot scratch; every call writes what it
  * reads, so its contents on entry do not matter.  It must not be shared by calls that can
- * run concurrently. */
+ * run concurrently.  Once an aipu_moe_swiglu_decode or aipu_moe_layer_decode call has run on
+ * its stream, the workspace can be inspected: bytes [0, 2E) hold the step's router logits
+ * (E bf16, the ones it routed from), and from byte 256 * ceil(E / 128) + 512 the SwiGLU
+ * activations h of every slot (I bf16 per slot, in slot order, the shared expert last). */
 int64_t aipu_moe_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
 
 /* One SwiGLU expert: gate/up GEMVs (bf16), h = bf16(f32(silu(gate)) * f32(up)),
