@@ -358,13 +358,17 @@ int aipu_moe_swiglu_decode_noalloc(int router_type, const void* router_w, int gg
         return fail(AIPU_ERR_WORKSPACE, "aipu_moe_swiglu_decode_noalloc: E=%lld H=%lld I=%lld topk=%d needs %lld "
                                         "bytes of scratch, more than the %lld-byte per-GPU array",
                     (long long)E, (long long)H, (long long)I, topk, (long long)need, (long long)kScratchBytes);
-    void* ws = nullptr;
-    int rc = scratch_for(S(stream), &ws);
-    if (rc) return rc;
+    // every argument is checked (with a stand-in for the scratch address, which moe_args only
+    // tests for presence and alignment) before anything touches the GPU
     aipu::MoeArgs a;
-    rc = moe_args(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, shared_gate, shared_up, shared_down,
-                  E, H, I, topk, scale_bits, x, y, sel_idx, sel_w, mode, ws, kScratchBytes, need, a);
+    int rc = moe_args(router_type, router_w, ggml_type, gate_exps, up_exps, down_exps, shared_gate, shared_up,
+                      shared_down, E, H, I, topk, scale_bits, x, y, sel_idx, sel_w, mode, (void*)(uintptr_t)256,
+                      kScratchBytes, need, a);
     if (rc) return rc;
+    void* ws = nullptr;
+    rc = scratch_for(S(stream), &ws);
+    if (rc) return rc;
+    a.ws = ws;
     return hip_status(aipu::launch_moe_decode(a, S(stream)), "aipu_moe_swiglu_decode_noalloc");
 }
 
@@ -407,6 +411,18 @@ int aipu_moe_layer_decode(int router_type, const void* router_w, int ggml_type, 
                             E >= 1 && topk >= 1 ? aipu::moe_layer_workspace_bytes(E, H, I, topk) : 0, a);
     if (rc) return rc;
     return hip_status(aipu::launch_moe_layer_decode(a, gamma, S(stream)), "aipu_moe_layer_decode");
+}
+
+int aipu_wait_timeouts(uint32_t* gave_up) {
+    if (!gave_up) return fail(AIPU_ERR_ARG, "null pointer");
+    uint32_t a = 0, b = 0, c = 0;
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = aipu::wait_gave_up_gemv_persist(&a);
+    if (e == hipSuccess) e = aipu::wait_gave_up_gemv_persist_m(&b);
+    if (e == hipSuccess) e = aipu::wait_gave_up_moe_persist(&c);
+    if (e != hipSuccess) return fail(AIPU_ERR_HIP, "aipu_wait_timeouts: %s", hipGetErrorString(e));
+    *gave_up = (a | b | c) ? 1u : 0u;
+    return ok();
 }
 
 int aipu_rmsnorm(const uint16_t* x, const uint16_t* gamma, int64_t n, uint16_t* y, int mode, void* stream) {

@@ -501,17 +501,19 @@ __global__ __launch_bounds__(kMixW * 64) void k_mixed(MixArgs args, const uint16
 }
 
 // Blocks per wave the activation region of k_mixed<XI> holds (every type's groups rounded
-// up to whole groups must fit): 2 XI blocks.
+// up to whole groups must fit): 2 XI blocks.  A wave's bpk blocks round up to
+// max(3 ceil(bpk / 3), 2 ceil(bpk / 2)) = 3, 3, 4, 6, 6, 6, 9, 9, ... blocks, so 1-3 blocks per
+// wave take XI = 2, 4-6 take XI = 3 and 7-16 take XI = 8.
 int mix_xi(int64_t K) {
     const int nsb = (int)(K / QK_K);
     const int bpk = (nsb + kMixW - 1) / kMixW;
     const int need = (bpk + 2) / 3 * 3 > (bpk + 1) / 2 * 2 ? (bpk + 2) / 3 * 3 : (bpk + 1) / 2 * 2;
-    return need <= 4 ? 2 : need <= 6 ? 3 : need <= 8 ? 4 : need <= 16 ? 8 : 0;
+    return need <= 4 ? 2 : need <= 6 ? 3 : need <= 16 ? 8 : 0;
 }
 
 // Activation rows per launch that the LDS holds beside the weight slices (160 KB): four up
-// to 6 blocks per wave (K <= 6144), two up to 8 (K <= 8192), one beyond.
-int mix_rows(int xi) { return xi <= 3 ? 4 : xi == 4 ? 2 : 1; }
+// to 6 blocks per wave (K <= 6144), one beyond (K <= 16384).
+int mix_rows(int xi) { return xi <= 3 ? 4 : 1; }
 
 bool mix_type(int t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0 || t == T_F16 || t == T_BF16; }
 
@@ -549,7 +551,6 @@ hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K
     if (xi == XV && mr == MV) hipLaunchKernelGGL((k_mixed<XV, MV>), grid, block, lds, st, a, xm, (int)K, rows, ym, yfm, ys);
         AIPU_MIX(2, 1) AIPU_MIX(2, 2) AIPU_MIX(2, 4)
         AIPU_MIX(3, 1) AIPU_MIX(3, 2) AIPU_MIX(3, 4)
-        AIPU_MIX(4, 1) AIPU_MIX(4, 2)
         AIPU_MIX(8, 1)
 #undef AIPU_MIX
         const hipError_t e = hipGetLastError();

@@ -305,4 +305,7 @@ hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uin
     }
 }
 
+// Whether a bounded wait in this file's kernels gave up since the last call (then cleared).
+hipError_t wait_gave_up_gemv_persist(uint32_t* flag) { return take_wait_gave_up(flag); }
+
 }  // namespace aipu

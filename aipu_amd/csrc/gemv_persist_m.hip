@@ -503,4 +503,7 @@ hipError_t launch_gemv_persist_m(const uint8_t* W, int64_t N, int64_t K, const u
     return hipErrorInvalidValue;
 }
 
+// Whether a bounded wait in this file's kernels gave up since the last call (then cleared).
+hipError_t wait_gave_up_gemv_persist_m(uint32_t* flag) { return take_wait_gave_up(flag); }
+
 }  // namespace aipu

@@ -67,6 +67,12 @@ bool gemv_persist_m_supported(int64_t N, int64_t K, int64_t M, bool dense);
 hipError_t launch_gemv_persist_m(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
                                  float* yf, int64_t ys, bool dense, hipStream_t st);
 
+// Persistent kernels (gemv_persist.hip, gemv_persist_m.hip, moe_persist.hip): whether one of
+// their bounded waits gave up since the last call (the word is then cleared).
+hipError_t wait_gave_up_gemv_persist(uint32_t* flag);
+hipError_t wait_gave_up_gemv_persist_m(uint32_t* flag);
+hipError_t wait_gave_up_moe_persist(uint32_t* flag);
+
 // gemv_mfma.hip -- matrix-core Q4_K GEMV (tolerance mode).  dense = false: every row of a
 // batch is bit-identical to the one-row launch on that row; dense = true allows the dense
 // multi-row kernel (rows within the tolerance of their one-row results)

@@ -87,10 +87,14 @@ __device__ __forceinline__ void set_weights(uint32_t sl, uint32_t cnt, int pp, i
         : "v"(ah), "v"(aq), "v"(cnt)
         : "memory");
     if (!known && __builtin_amdgcn_readfirstlane(cv) < 1u) {
-        for (uint32_t it = 0; it < (1u << 22); ++it) {
+        for (uint32_t it = 0;; ++it) {
             uint32_t c;
             asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(c) : "v"(cnt) : "memory");
             if (__builtin_amdgcn_readfirstlane(c) >= 1u) break;
+            if (it == (1u << 22)) {   // give up (recorded), as spin_ge does
+                wait_gave_up();
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
         asm volatile(
@@ -517,5 +521,8 @@ hipError_t launch_moe_down_persist(const uint8_t* D, const uint8_t* shD, const i
                            selw, (int)E, topk, nslots, h, (int)I, H, y, resid, njobs);
     return hipGetLastError();
 }
+
+// Whether a bounded wait in this file's kernels gave up since the last call (then cleared).
+hipError_t wait_gave_up_moe_persist(uint32_t* flag) { return take_wait_gave_up(flag); }
 
 }  // namespace aipu

@@ -78,10 +78,35 @@ __device__ __forceinline__ uint32_t lds_poll(const uint32_t* c) {
     asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(c)) : "memory");
     return __builtin_amdgcn_readfirstlane(v);
 }
+// A wait that gives up (below) sets this word, one per translation unit that includes this
+// header, with one vector atomic; the library reads and clears it through
+// aipu_wait_timeouts(), so the wrong result such a launch leaves is reported, not silent.
+[[maybe_unused]] static __device__ uint32_t g_wait_gave_up;
+
+__device__ __forceinline__ void wait_gave_up() {
+    __hip_atomic_fetch_or(&g_wait_gave_up, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Host side: this translation unit's word (nonzero = some wait gave up), then cleared.
+[[maybe_unused]] static hipError_t take_wait_gave_up(uint32_t* flag) {
+    hipError_t e = hipMemcpyFromSymbol(flag, HIP_SYMBOL(g_wait_gave_up), sizeof(uint32_t));
+    if (e == hipSuccess && *flag) {
+        const uint32_t zero = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_wait_gave_up), &zero, sizeof(uint32_t));
+    }
+    return e;
+}
+
 // Bounded wait for a counter: every wave reaches the end of the kernel even if a post were
-// lost (the result would then be wrong, never a hang).
+// lost.  The result would then be wrong, never a hang, and the give-up is recorded.
 __device__ __forceinline__ void spin_ge(const uint32_t* c, uint32_t v) {
-    for (uint32_t it = 0; lds_poll(c) < v && it < (1u << 22); ++it) __builtin_amdgcn_s_sleep(1);
+    for (uint32_t it = 0; lds_poll(c) < v; ++it) {
+        if (it == (1u << 22)) {
+            wait_gave_up();
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
 }
 
 // Copy wave c of CW: rounds u = c, c + CW, ... < U (LOADS loads each) into slots u % NS, at

@@ -366,3 +366,11 @@ def stream_read(buf, sink):
     """Read-bandwidth probe over a uint8 device buffer (bytes multiple of 16)."""
     _need_cuda(buf, sink)
     call("aipu_stream_read", _ptr(buf), buf.numel(), _ptr(sink), _stream(buf))
+
+
+def wait_timeouts():
+    """Whether a bounded wait of a persistent kernel gave up since the last call (its launch's
+    result is then wrong); synchronises the current device and clears the flag."""
+    flag = ctypes.c_uint32(0)
+    call("aipu_wait_timeouts", ctypes.byref(flag))
+    return bool(flag.value)

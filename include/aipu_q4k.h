@@ -253,6 +253,14 @@ int64_t aipu_lm_head_workspace_bytes(int64_t V);
 int aipu_lm_head(const uint16_t* w, int64_t V, int64_t K, const uint16_t* x, uint16_t* logits,
                  int32_t* argmax, void* workspace, int64_t ws_bytes, void* stream);
 
+/* Health check with no counterpart in the reference.  The persistent kernels (the M = 1 and
+ * multi-row GEMVs, the MoE expert legs) coordinate their waves through bounded waits: a wave
+ * that waited about 2^22 polls for a post that never came stops waiting rather than hang, and
+ * its launch's result is then wrong.  Such a give-up sets a per-device word; this call
+ * synchronises the current device, stores 1 in *gave_up if any wait gave up since the last
+ * call (0 otherwise) and clears the word. */
+int aipu_wait_timeouts(uint32_t* gave_up);
+
 /* Measurement utility with no counterpart in the reference: streams `bytes` (a multiple of
  * 16) from `p` with the same 16-B global loads the GEMV kernels use and folds them into
  * sink[0..255]; used to measure the achievable HBM read ceiling beside the 8 TB/s peak. */

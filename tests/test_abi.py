@@ -120,6 +120,22 @@ def test_moe_validation():
     assert call(I=300) == SHAPE
     assert call(rt=5) == TYPE
     assert call(g=NULL) == ARG
+    # the allocation-free step checks every argument before it looks up its scratch on the GPU
+    # (this container has none: any HIP call would fail with AIPU_ERR_HIP)
+    f3 = L().aipu_moe_swiglu_decode_noalloc
+
+    def call3(**kw):
+        a = dict(args, **kw)
+        return f3(a["rt"], a["rw"], a["t"], a["g"], a["u"], a["d"], a["sg"], a["su"], a["sd"], a["E"], a["H"],
+                  a["I"], a["k"], a["sc"], a["x"], a["y"], a["si"], a["sw"], a["mode"], S)
+
+    assert call3(g=NULL) == ARG
+    assert call3(sg=FAKE) == ARG
+    assert call3(rt=5) == TYPE
+    assert call3(k=17) == SHAPE
+    assert call3(x=ctypes.c_void_p(0x100008), mode=0) == ALIGN
+    assert call3(mode=2) == ARG
+    assert call3(E=256, H=6144, I=2048 * 128) == WS    # beyond the per-GPU scratch array
     f2 = L().aipu_swiglu_expert
     assert f2(12, FAKE, FAKE, FAKE, 512, 256, FAKE, FAKE, NULL, 1, FAKE, 10, S) == WS
     assert f2(12, FAKE, FAKE, FAKE, 500, 256, FAKE, FAKE, NULL, 1, FAKE, 10, S) == SHAPE

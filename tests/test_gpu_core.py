@@ -12,7 +12,7 @@ from oracle import c_oracle as co
 from oracle import glm_oracle as go
 from oracle import q4k_oracle as qo
 
-from .gpu_util import assert_bits_equal, d_bf16, d_u8, h_bits, h_f32, note, u32
+from .gpu_util import assert_bits_equal, d_bf16, d_u8, h_bits, h_f32, note, random_weights_gpu, u32
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
@@ -405,3 +405,26 @@ def test_gemv_fast_detects_corrupted_weights():
     _, yf = dev.gemv(qo.GGML_Q4_K, d_u8(bad), N, K, d_bf16(x), mode="fast", out_f32=True)
     ok, _ = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
     assert not ok
+
+
+def test_persistent_waits_complete():
+    """No bounded wait of the persistent kernels gives up in normal runs: the give-up flag
+    (aipu_wait_timeouts) stays clear across the single-row, row-pair, dense multi-row and MoE
+    expert-leg kernels."""
+    note("persistent kernels: wait give-up flag")
+    dev.wait_timeouts()   # clear whatever earlier tests left
+    g = torch.Generator(device="cuda")
+    g.manual_seed(17)
+    N = K = 6144
+    w = random_weights_gpu(qo.GGML_Q4_K, N, K, g)
+    x = (torch.randn((8, K), device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+    for m, mode in ((1, "fast"), (2, "fast"), (8, "fast"), (8, "fast_dense")):
+        dev.gemv(qo.GGML_Q4_K, w, N, K, x[:m], mode=mode)
+    E, H, I, topk = 16, 2048, 2048, 8
+    ex = [random_weights_gpu(qo.GGML_Q4_K, E * I, H, g), random_weights_gpu(qo.GGML_Q4_K, E * I, H, g),
+          random_weights_gpu(qo.GGML_Q4_K, E * H, I, g)]
+    rw = (torch.randn((E, H), device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    xm = (torch.randn(H, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    dev.moe_swiglu_decode(go.BF16_TYPE, rw.view(torch.uint8).reshape(-1), qo.GGML_Q4_K, *ex, E, H, I, topk, xm,
+                          mode="fast")
+    assert not dev.wait_timeouts()

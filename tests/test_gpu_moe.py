@@ -402,10 +402,11 @@ def test_mixed_tiles_c3_full_shape():
     assert qo.bf16_parity(h_bits(y), acc, w, qo.bf16_bits_to_f32(x))[0]
 
 
-# Mixed-type batches share each weight pass: K = 6144 and 2048 run four (or three) rows in one
-# launch, K = 8192 two passes of two rows.  Every row must equal its single-row launch bit for
-# bit (the rows are formed independently from the same decoded weights) and pass the gate.
-@pytest.mark.parametrize("K,M", [(6144, 4), (2048, 3), (8192, 4)])
+# Mixed-type batches share each weight pass: K <= 6144 runs up to four rows per launch (K = 6144
+# and 2048: one pass of four or three rows; K = 5120 with six rows: a pass of four, then one of
+# two), larger K one row per launch (K = 8192).  Every row must equal its single-row launch bit
+# for bit (the rows are formed independently from the same decoded weights) and pass the gate.
+@pytest.mark.parametrize("K,M", [(6144, 4), (2048, 3), (5120, 6), (8192, 2)])
 def test_mixed_tiles_batch(K, M):
     note(f"tiles fast batch K={K} M={M}")
     rng = np.random.default_rng(K + M)
