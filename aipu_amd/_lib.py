@@ -96,6 +96,7 @@ SIGNATURES = {
     "aipu_lm_head": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "aipu_stream_read": (_I, [_P, _I64, _P, _P]),
     "aipu_wait_timeouts": (_I, [_P]),
+    "aipu_measure_gemv": (_I, [_I, _P, _I64, _I64, _P, _P]),
 }
 
 _lib = None

@@ -413,6 +413,18 @@ int aipu_moe_layer_decode(int router_type, const void* router_w, int ggml_type, 
     return hip_status(aipu::launch_moe_layer_decode(a, gamma, S(stream)), "aipu_moe_layer_decode");
 }
 
+int aipu_measure_gemv(int what, const void* w, int64_t N, int64_t K, const uint16_t* x, void* stream) {
+    if (what != AIPU_MEASURE_EMPTY && what != AIPU_MEASURE_COPY) return fail(AIPU_ERR_ARG, "unknown measurement %d", what);
+    if (!w || !x) return fail(AIPU_ERR_ARG, "null pointer");
+    if (N < 1 || K < 256 || K % 256 || !aipu::gemv_persist_supported(N, K))
+        return fail(AIPU_ERR_SHAPE, "N=%lld K=%lld: the M = 1 persistent kernel serves K = 256 .. 8192 (multiples of 256)",
+                    (long long)N, (long long)K);
+    if (!aligned(w, 16) || !aligned(x, 16)) return fail(AIPU_ERR_ALIGN, "weights and activations must be 16-byte aligned");
+    return hip_status(aipu::launch_gemv_persist((const uint8_t*)w, N, K, x, nullptr, nullptr, S(stream),
+                                                what == AIPU_MEASURE_COPY ? 1 : 2),
+                      "aipu_measure_gemv");
+}
+
 int aipu_wait_timeouts(uint32_t* gave_up) {
     if (!gave_up) return fail(AIPU_ERR_ARG, "null pointer");
     uint32_t a = 0, b = 0, c = 0;

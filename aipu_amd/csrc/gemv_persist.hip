@@ -40,8 +40,10 @@ constexpr int kPMaxPairs = kPMaxNsb / 2;
 constexpr int kPStage = kStgBytes; // per pair: operand entries + 16 sub-block sums
 
 // R rounds per tile (ceil(row bytes / 1 KB)), TT tiles per workgroup, XPW pairs per compute
-// wave.  nsb = K / 256 is a runtime value with ceil(144 * nsb / 1024) == R.
-template <int R, int TT, int XPW>
+// wave.  nsb = K / 256 is a runtime value with ceil(144 * nsb / 1024) == R.  COPY_ONLY = true
+// is a measurement variant (aipu_measure_gemv): the copy wave runs the same copy schedule and
+// the compute waves leave after the first barrier, so nothing is computed or written.
+template <int R, int TT, int XPW, bool COPY_ONLY = false>
 __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __restrict__ W, int64_t N, int nsb,
                                                              const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
                                                              float* __restrict__ Yf, int ntiles) {
@@ -85,6 +87,12 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     __builtin_amdgcn_sched_barrier(0);
     // the copy wave joins the barrier after issuing its first Q rounds (before its first post)
     if (w != NCW) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // counters initialised
+    if constexpr (COPY_ONLY) {
+        if (w != NCW) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no load still in flight when the wave ends
+            return;
+        }
+    }
 
     if (w == NCW) {
         // ---- copy wave: round u = t * R + k, posted in order once landed
@@ -98,7 +106,7 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
                 constexpr int t = step / R, k = step - t * R;
                 // A buffer is reused once its previous tile is reduced.  That tile's last
                 // round is posted by now: Q <= (NB - 1) * R + 1 keeps it at least Q rounds back.
-                if constexpr (k == 0 && t >= NB) spin_ge(&s_freed[t - NB], 1u);
+                if constexpr (k == 0 && t >= NB && !COPY_ONLY) spin_ge(&s_freed[t - NB], 1u);
                 const int64_t r0 = (int64_t)(wg + t * G) * kPR;
                 const int nvalid = t < T ? (int)(N - r0 < kPR ? N - r0 : kPR) : 0;
                 const __amdgpu_buffer_rsrc_t wr =
@@ -239,6 +247,9 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     }
 }
 
+// Measurement: an empty kernel with k_gemv1p's launch shape (grid, block and LDS).
+__global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p_empty() {}
+
 int cu_count() {
     static int n = 0;
     if (n == 0) {
@@ -251,13 +262,13 @@ int cu_count() {
     return n;
 }
 
-template <int R, int XPW>
+template <int R, int XPW, bool COPY_ONLY = false>
 hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16_t* y, float* yf, int TT, int G,
                  int ntiles, int ncw, size_t lds, hipStream_t st) {
     const dim3 grid(G), block(64 * (ncw + 1));
     switch (TT) {
 #define AIPU_P(TV) \
-    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, XPW>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles); break;
+    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, XPW, COPY_ONLY>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles); break;
         AIPU_P(1)
         AIPU_P(2)
         AIPU_P(3)
@@ -278,9 +289,10 @@ bool gemv_persist_supported(int64_t N, int64_t K) {
     return N >= 1 && K >= QK_K && K % QK_K == 0 && K / QK_K <= kPMaxNsb && N <= ((int64_t)1 << 31);
 }
 
-// y[0 .. N) = x . W^T for one activation row (Q4_K, K <= 8192).
+// y[0 .. N) = x . W^T for one activation row (Q4_K, K <= 8192).  variant 1: the copy schedule
+// alone; variant 2: an empty kernel of the same launch shape (measurement only).
 hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
-                               hipStream_t st) {
+                               hipStream_t st, int variant) {
     if (!gemv_persist_supported(N, K)) return hipErrorInvalidValue;
     const int nsb = (int)(K / QK_K);
     const int ntiles = (int)((N + kPR - 1) / kPR);
@@ -294,6 +306,23 @@ hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uin
     const int ncw = (np + xpw - 1) / xpw;
     const int nb = TT < 3 ? TT : 3;
     const size_t lds = (size_t)nb * kPR * tile_pitch((uint32_t)nsb * 144u);
+    if (variant == 2) {
+        // the same dynamic LDS plus the kernel's static arrays
+        const size_t stat = (size_t)kPMaxPairs * kPStage + (size_t)nb * kPR * kPMaxPairs * 4 + (size_t)TT * (R + 2) * 4;
+        hipLaunchKernelGGL(k_gemv1p_empty, dim3(G), dim3(64 * (ncw + 1)), lds + stat, st);
+        return hipGetLastError();
+    }
+    if (variant == 1) {
+        switch (R * 4 + xpw) {
+            case 1 * 4 + 1: return run_p<1, 1, true>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+            case 2 * 4 + 1: return run_p<2, 1, true>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+            case 3 * 4 + 1: return run_p<3, 1, true>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+            case 4 * 4 + 1: return run_p<4, 1, true>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+            case 4 * 4 + 2: return run_p<4, 2, true>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+            case 5 * 4 + 2: return run_p<5, 2, true>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (R * 4 + xpw) {
         case 1 * 4 + 1: return run_p<1, 1>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
         case 2 * 4 + 1: return run_p<2, 1>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);

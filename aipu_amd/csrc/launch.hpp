@@ -57,7 +57,7 @@ hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K
 // gemv_persist.hip -- persistent single-row Q4_K GEMV (tolerance mode, K <= 8192)
 bool gemv_persist_supported(int64_t N, int64_t K);
 hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
-                               hipStream_t st);
+                               hipStream_t st, int variant = 0);
 
 // gemv_persist_m.hip -- persistent Q4_K GEMV for 2 .. 8 activation rows (tolerance mode,
 // K = 2048, 4096, 6144, at most three 8-row tiles per CU).  dense = false: row m is

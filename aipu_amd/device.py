@@ -368,6 +368,13 @@ def stream_read(buf, sink):
     call("aipu_stream_read", _ptr(buf), buf.numel(), _ptr(sink), _stream(buf))
 
 
+def measure_gemv(what, w, N, K, x):
+    """Launch floors of the M = 1 Q4_K GEMV at (N, K): what = "empty" (an empty kernel of the
+    same launch shape) or "copy" (its weight-copy schedule alone)."""
+    _need_cuda(w, x)
+    call("aipu_measure_gemv", {"empty": 0, "copy": 1}[what], _ptr(w), N, K, _ptr(x), _stream(x))
+
+
 def wait_timeouts():
     """Whether a bounded wait of a persistent kernel gave up since the last call (its launch's
     result is then wrong); synchronises the current device and clears the flag."""

@@ -102,8 +102,26 @@ def time_eager(fn_list):
     return e0.elapsed_time(e1)
 
 
-def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label="", eager=False):
-    """Rotating-buffer GEMV timing.  Returns dict with us/launch, GB/s, percentiles, hot number."""
+def time_isolated(fn_list):
+    """Each launch alone: HIP events on the launch stream around it, then a host sync before the
+    next one, so no launch queues behind another (what a kernel tracer then sees per dispatch is
+    the kernel's own duration).  Returns us per launch (list)."""
+    import torch
+    out = []
+    for f in fn_list:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        f()
+        e1.record()
+        e1.synchronize()
+        out.append(1000.0 * e0.elapsed_time(e1))
+    return out
+
+
+def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label="", eager=False, isolated=False):
+    """Rotating-buffer GEMV timing.  Returns dict with us/launch, GB/s, percentiles, hot number.
+    isolated: every launch alone (time_isolated), for kernel traces."""
     device = "cuda"
     wb = q4k_bytes(N, K)
     nbuf = max(2, math.ceil(rot_bytes / wb))
@@ -120,6 +138,15 @@ def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label
     for i in range(warmup):
         launcher(i)()
     torch.cuda.synchronize()
+    if isolated:
+        t = time_isolated([launcher(i) for i in range(steps)])
+        alg = wb + 2 * K * M + 2 * N * M
+        us = pct(t, 50)
+        log(f"{label} isolated N={N} K={K} M={M} {mode}: median {us:.2f} us per launch alone (p10 {pct(t, 10):.2f}, "
+            f"p90 {pct(t, 90):.2f}), {alg / (us * 1e-6) / 1e9:.0f} GB/s")
+        return dict(N=N, K=K, M=M, mode=mode, us_per_launch=us, p10_us=pct(t, 10), p90_us=pct(t, 90),
+                    gbs=alg / (us * 1e-6) / 1e9, alg_bytes=alg, weight_rotation_bytes=nbuf * wb,
+                    timing="each launch alone: HIP events around it, host sync before the next")
     if eager:
         fns = [launcher(i) for i in range(steps)]
         total_ms = time_eager(fns)
@@ -135,22 +162,66 @@ def bench_gemv(dev, torch, N, K, M, steps, warmup, rot_bytes, mode="fast", label
     nlaunch = max(steps, nbuf)
     ms, _ = time_graph([launcher(i) for i in range(nlaunch)], reps=REPS)
     per_launch_us = [1000.0 * t / nlaunch for t in ms]
-    # cache-hot (labelled): the same buffer every launch
-    hot_ms, _ = time_graph([(lambda: dev.gemv(Q4K, W[0], N, K, X[0], mode=mode, out=Y[0])) for _ in range(200)], reps=3)
     alg = wb + 2 * K * M + 2 * N * M
     us = pct(per_launch_us, 50)
     res = dict(N=N, K=K, M=M, mode=mode, us_per_launch=us, gbs=alg / (us * 1e-6) / 1e9,
                alg_bytes=alg, weight_rotation_bytes=nbuf * wb, rotation_buffers=nbuf, launches_per_replay=nlaunch,
                timed_replays=REPS, p10_us=pct(per_launch_us, 10), p50_us=us, p90_us=pct(per_launch_us, 90),
-               min_us=min(per_launch_us), hot_us=1000.0 * pct(hot_ms, 50) / 200)
+               min_us=min(per_launch_us))
     res["pct_peak"] = 100.0 * res["gbs"] / PEAK_GBS
     res["gemv_per_s"] = 1e6 / us
     res["tflops"] = 2.0 * M * N * K / (us * 1e-6) / 1e12
-    res["hot_gbs_cache_resident"] = alg / (res["hot_us"] * 1e-6) / 1e9
+    hot = ""
+    if mode != "ref":
+        # cache-hot (labelled): the same buffer every launch
+        hot_ms, _ = time_graph([(lambda: dev.gemv(Q4K, W[0], N, K, X[0], mode=mode, out=Y[0])) for _ in range(200)],
+                               reps=3)
+        res["hot_us"] = 1000.0 * pct(hot_ms, 50) / 200
+        res["hot_gbs_cache_resident"] = alg / (res["hot_us"] * 1e-6) / 1e9
+        hot = f"; hot {res['hot_us']:.2f} us"
     log(f"{label} N={N} K={K} M={M} {mode}: {us:.2f} us/launch, {res['gbs']:.0f} GB/s "
-        f"({res['pct_peak']:.1f}% of 8 TB/s); hot {res['hot_us']:.2f} us")
+        f"({res['pct_peak']:.1f}% of 8 TB/s){hot}")
     del W, X, Y
     torch.cuda.empty_cache()
+    return res
+
+
+def bench_exact(dev, torch, rot_bytes):
+    """The price of the reference's exact order (AIPU_MODE_REF: exact dequant, sequential fp32
+    MAC in K order, bit-identical to tools/q4k_ref.py): the north-star GEMV and the verify
+    batches of config 1, timed like the fast legs over one rotation of the weights."""
+    out = {}
+    for M in (1, 2, 4, 8):
+        out[f"m{M}"] = bench_gemv(dev, torch, 6144, 6144, M, 1, 0, rot_bytes, mode="ref", label="exact order")
+    return out
+
+
+def bench_floor(dev, torch, N, K, rot_bytes, steps=1000):
+    """What bounds the M = 1 GEMV at (N, K), each timed like the headline (one HIP graph of
+    launches over rotating weights, median replay): an empty kernel with the GEMV kernel's
+    launch shape, the kernel's weight-copy schedule alone (aipu_measure_gemv), and a plain
+    streaming read of the same bytes per launch (aipu_stream_read)."""
+    device = "cuda"
+    wb = q4k_bytes(N, K)
+    nbuf = max(2, math.ceil(rot_bytes / wb))
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4321 + N + K)
+    W = gen_q4k(nbuf * N, K, gen, device).view(nbuf, wb)
+    X = (torch.randn((nbuf, 1, K), device=device, generator=gen)).to(torch.bfloat16)
+    nlaunch = max(steps, nbuf)
+    res = dict(N=N, K=K, alg_bytes=wb + 2 * K + 2 * N, launches_per_replay=nlaunch, timed_replays=REPS)
+    for what in ("empty", "copy"):
+        ms, _ = time_graph([(lambda j=i % nbuf: dev.measure_gemv(what, W[j], N, K, X[j])) for i in range(nlaunch)],
+                           reps=REPS)
+        res[f"{what}_us"] = 1000.0 * pct(ms, 50) / nlaunch
+    res["copy_gbs"] = wb / (res["copy_us"] * 1e-6) / 1e9
+    del W, X
+    torch.cuda.empty_cache()
+    rd = bench_stream_read_sized(dev, torch, res["alg_bytes"], rot_bytes)
+    res["stream_read_us"] = rd["us_per_launch"]
+    res["stream_read_gbs"] = rd["gbs"]
+    log(f"floors N={N} K={K}: empty launch {res['empty_us']:.2f} us, copy schedule {res['copy_us']:.2f} us "
+        f"({res['copy_gbs']:.0f} GB/s), stream read {res['stream_read_us']:.2f} us")
     return res
 
 
@@ -545,7 +616,10 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=200)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of one HIP graph")
-    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1", "lmhead", "layer", "batched"], default=None,
+    ap.add_argument("--isolated", action="store_true",
+                    help="with --only gemv / c0 / c1: every launch alone (host sync between launches), for kernel traces")
+    ap.add_argument("--only", choices=["gemv", "moe", "stream", "copy", "tiles", "prefill", "c1", "lmhead", "layer", "batched",
+                                       "floor", "c0", "exact"], default=None,
                     help="run one measurement only (for kernel tracing / counter runs)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
                     help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into "
@@ -595,14 +669,27 @@ def main():
         print(json.dumps(bench_lmhead(dev, torch)))
         return
     if args.only == "c1":
-        print(json.dumps({f"m{M}": bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, label="C1") for M in (2, 4, 8)}))
+        print(json.dumps({f"{mode}_m{M}": bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, mode=mode, label="C1",
+                                                     isolated=args.isolated)
+                          for mode in ("fast", "fast_dense") for M in (2, 4, 8)}))
+        return
+    if args.only == "c0":
+        print(json.dumps(bench_gemv(dev, torch, 4096, 4096, 1, 1000, 50, rot, label="C0", eager=args.eager,
+                                    isolated=args.isolated)))
+        return
+    if args.only == "floor":
+        print(json.dumps({"ns": bench_floor(dev, torch, 6144, 6144, rot), "c0": bench_floor(dev, torch, 4096, 4096, rot)}))
+        return
+    if args.only == "exact":
+        print(json.dumps(bench_exact(dev, torch, rot)))
         return
     if args.only == "stream":
         r = bench_stream_read(dev, torch)
         r["gemv_size"] = bench_stream_read_sized(dev, torch, q4k_bytes(6144, 6144) + 4 * 6144, rot)
         print(json.dumps(r))
         return
-    head = bench_gemv(dev, torch, 6144, 6144, 1, args.steps, args.warmup, rot, label="north star", eager=args.eager)
+    head = bench_gemv(dev, torch, 6144, 6144, 1, args.steps, args.warmup, rot, label="north star", eager=args.eager,
+                      isolated=args.isolated and args.only == "gemv")
     if args.only == "gemv":
         print(json.dumps(head))
         return
@@ -615,8 +702,14 @@ def main():
             f"{extra['stream_read_gemv_size']['gbs']:.0f} GB/s")
         extra["moe_decode_c2"] = bench_moe(dev, torch, args.moe_steps)
         extra["gemv_c0_4096"] = bench_gemv(dev, torch, 4096, 4096, 1, 1000, 50, rot, label="C0")
-        for M in (2, 4, 8):
+        extra["floor_ns"] = bench_floor(dev, torch, 6144, 6144, rot)
+        extra["floor_c0"] = bench_floor(dev, torch, 4096, 4096, rot)
+        for M in (2, 4, 8):   # verify batches: rows bit-identical to the one-row launch
             extra[f"gemv_c1_m{M}"] = bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, label="C1")
+        for M in (2, 4, 8):   # opt-in dense batches: rows within the tolerance of the one-row launch
+            extra[f"gemv_c1_dense_m{M}"] = bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, mode="fast_dense",
+                                                      label="C1 dense")
+        extra["exact_order"] = bench_exact(dev, torch, rot)
         extra["mixed_tiles_c3"] = bench_tiles(dev, torch)
         extra["mixed_tiles_c3_m4"] = bench_tiles(dev, torch, M=4)
         extra["prefill_c4"] = bench_prefill(dev, torch)

@@ -266,6 +266,16 @@ int aipu_wait_timeouts(uint32_t* gave_up);
  * sink[0..255]; used to measure the achievable HBM read ceiling beside the 8 TB/s peak. */
 int aipu_stream_read(const void* p, int64_t bytes, uint32_t* sink, void* stream);
 
+/* Measurement utility with no counterpart in the reference: the floors of the M = 1 Q4_K GEMV
+ * kernel at one shape (Q4_K weights w[N][K/256], K a multiple of 256 up to 8192, x as for
+ * aipu_gemv).  what = AIPU_MEASURE_EMPTY launches an empty kernel with the launch shape (grid,
+ * block, LDS) that aipu_gemv uses for this shape at M = 1 and touches no memory;
+ * what = AIPU_MEASURE_COPY runs that kernel's weight-copy schedule alone (every weight byte
+ * streamed into LDS as the GEMV streams it, nothing computed, nothing written). */
+#define AIPU_MEASURE_EMPTY 0
+#define AIPU_MEASURE_COPY  1
+int aipu_measure_gemv(int what, const void* w, int64_t N, int64_t K, const uint16_t* x, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -428,3 +428,19 @@ def test_persistent_waits_complete():
     dev.moe_swiglu_decode(go.BF16_TYPE, rw.view(torch.uint8).reshape(-1), qo.GGML_Q4_K, *ex, E, H, I, topk, xm,
                           mode="fast")
     assert not dev.wait_timeouts()
+
+
+@pytest.mark.parametrize("N,K", [(6144, 6144), (4096, 4096), (2048, 8192)])
+def test_measure_gemv_variants(N, K):
+    """The measurement launches (an empty kernel of the M = 1 GEMV's launch shape, its copy
+    schedule alone) run to completion, write nothing, and leave no wait given up."""
+    note(f"measure_gemv N={N} K={K}")
+    dev.wait_timeouts()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(N + K)
+    w = random_weights_gpu(qo.GGML_Q4_K, N, K, g)
+    x = torch.zeros((1, K), dtype=torch.bfloat16, device="cuda")
+    for what in ("empty", "copy"):
+        dev.measure_gemv(what, w, N, K, x)
+    torch.cuda.synchronize()
+    assert not dev.wait_timeouts()
