@@ -18,6 +18,8 @@
 // stream.  The block loop is software pipelined PD deep; loads that fall past the wave's
 // blocks or past the tile's valid rows use an out-of-range buffer offset, which reads zero
 // without a memory access, so every load is unconditional and the waits are static.
+#include <type_traits>
+
 #include "common.hpp"
 #include "glm_act.hpp"
 #include "launch.hpp"
@@ -29,6 +31,16 @@ namespace aipu {
 using namespace mg;
 
 namespace {
+
+// Problems that declare kCanon = true sum their outputs in the fast-mode order (k_gemv1).
+template <class P, class = void>
+struct CanonOrder {
+    static constexpr bool value = false;
+};
+template <class P>
+struct CanonOrder<P, std::void_t<decltype(P::kCanon)>> {
+    static constexpr bool value = P::kCanon;
+};
 
 constexpr int kXL = 8;          // activation pieces (16 B) staged per thread, at most
 constexpr int kMaxW = 8;        // waves per workgroup
@@ -44,6 +56,9 @@ struct TileRef {
 // Plain GEMV: tile = 16 consecutive rows of W, activation rows x[M][K].
 template <int MR>
 struct ProbPlain {
+    // k_gemv1 forms the output in the fast-mode order of mfma_gemv.hpp (block terms, pair sums,
+    // the balanced tree), the order of every other single-row and batch kernel
+    static constexpr bool kCanon = true;
     const uint8_t* W;
     int64_t N, rb;
     uint16_t* Y;
@@ -420,6 +435,9 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
     constexpr int kSlots = Prob::kShareAct ? kMaxW / 2 : kMaxW;   // activation staging slots
     __shared__ __align__(16) uint8_t s_act[kSlots * kActWave];
     __shared__ float red[(kLoop ? 2 : 1) * kMaxW * kTR];   // double-buffered across a workgroup's tiles
+    // fast-mode order: every block term of the tile, [row][block] (one tile per workgroup)
+    constexpr bool kCanon = CanonOrder<Prob>::value;
+    __shared__ float bterm[kCanon ? kTR * kMaxW * kBpkMax : 1];
     extern __shared__ __align__(16) uint8_t s_w[];
     const int BPK = GS * NG;
     const int XP = BPK * 32;
@@ -522,8 +540,26 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
                 const int b = gi * GS + bb;   // block index within this wave's part
                 a_reads(A, lds_addr(wA + 512u * (uint32_t)b + 16u * (uint32_t)g), diag_mask(1));
                 const float2 as = sums_read(wS + (b * 4 + g) * 2);   // no wait on the refill in flight
-                acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
+                if constexpr (kCanon) {
+                    // block term: the four K-groups' terms (q4k_block1 from zero is block_term)
+                    const float bt = block_sum(q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, 0.0f));
+                    if (lane < kTR) bterm[lane * nsb + kb0 + b] = bt;
+                } else {
+                    acc = q4k_block1(R[bb], A, as, hs, ck, dlo, dhi, acc);
+                }
             }
+        }
+        if constexpr (kCanon) {
+            // pair sums and the balanced tree over every block term of the row, on eight lanes
+            // per row (canon_sum8)
+            __syncthreads();
+            for (int i = tid; i < kTR * 8; i += (int)blockDim.x) {
+                const int rn = i >> 3, k = i & 7;
+                const float y = canon_sum8(nsb, k, [&](int b) { return bterm[rn * nsb + b]; });
+                if (k == 0) pb.store(t, rn, 0, y);
+            }
+            if constexpr (kLoop) __syncthreads();   // read before a next tile writes its terms
+            continue;
         }
 
         // 5. reduce over the four K-groups, then across the K parts (an LDS-only barrier: the
@@ -963,7 +999,8 @@ int64_t static_lds1(int xi, bool share) {
     return (int64_t)(share ? kMaxW / 2 : kMaxW) * 2 * xi * 544 + kMaxW * kTR * 4;
 }
 
-bool make_plan1(int nsb, int T, int kp_max, Plan1& p, bool share = false) {
+// canon: the plain GEMV's block-term buffer (16 rows x 8 waves x 2 XI blocks) is static LDS too
+bool make_plan1(int nsb, int T, int kp_max, Plan1& p, bool share = false, bool canon = false) {
     for (int kp = (kp_max < kMaxW / T ? kp_max : kMaxW / T); kp >= 1; --kp) {
         if (nsb % kp) continue;
         const int bpk = nsb / kp;
@@ -974,7 +1011,8 @@ bool make_plan1(int nsb, int T, int kp_max, Plan1& p, bool share = false) {
             if (bpk % gs) continue;
             const int W = T * kp;
             const int64_t lds = (int64_t)W * dma_bytes(gs);
-            if (lds + static_lds1(xi, share) > kMaxLds1) continue;
+            const int64_t bterm = canon ? (int64_t)kTR * kMaxW * 2 * xi * 4 : 0;
+            if (lds + static_lds1(xi, share) + bterm > kMaxLds1) continue;
             p = Plan1{kp, gs, bpk / gs, xi, W, lds};
             return true;
         }
@@ -1054,6 +1092,20 @@ bool gemvm_supported(int nsb, int mr) {
     return false;
 }
 
+// One-row shapes where the 16-row-tile kernel (k_gemv1) measured faster than the persistent one
+// (MI355X, a HIP graph of launches over weights rotated through 0.6 GB, N = 2048..16384 against
+// K = 2048..8192): every CU gets one or two 16-row tiles and K <= 4096 (C0, 4096 x 4096: 4.41
+// against 4.68 us); or at least one tile per CU and K = 2048 (the persistent kernel's second copy
+// round is 128 B per row; 16384 x 2048: 6.83 against 9.21 us) or K > 6144 (two block pairs per
+// persistent compute wave; 4096 x 8192: 5.97 against 7.94 us).  Both kernels form a row in the
+// same order, so the choice never changes a result bit.
+bool prefer_gemv1(int64_t N, int64_t K) {
+    const int64_t t16 = (N + kTR - 1) / kTR, cus = device_cu_count();
+    if (t16 < cus) return false;
+    if (K == 2048 || K > 6144) return true;
+    return K <= 4096 && t16 <= 2 * cus;
+}
+
 template <int MR>
 hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int M, uint16_t* y, float* yf,
                       int64_t ystride, hipStream_t st) {
@@ -1061,9 +1113,10 @@ hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x,
     const ProbPlain<MR> pb{W, N, row_bytes(T_Q4_K, K), y, yf, ystride, M};
     const unsigned nwg = (unsigned)((N + kTR - 1) / kTR);
     if constexpr (MR == 1) {
-        if (gemv_persist_supported(N, K)) return launch_gemv_persist(W, N, K, x, y, yf, st);
         Plan1 p1;
-        if (make_plan1(nsb, 1, kMaxW, p1)) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
+        const bool k1 = make_plan1(nsb, 1, kMaxW, p1, false, true);
+        if (gemv_persist_supported(N, K) && !(k1 && prefer_gemv1(N, K))) return launch_gemv_persist(W, N, K, x, y, yf, st);
+        if (k1) return run1(pb, p1, nwg, x, 0, (int64_t)K * 2, (int)K, st);
     } else {
         if (gemvm_supported(nsb, MR)) return run_gemvm<MR>(pb, nsb, nwg, x, (int)K, st);
     }
@@ -1097,7 +1150,7 @@ hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t*
     PlanS ps;
     const bool small = make_plans(nsb, ps);
     Plan1 p1;
-    const bool canon1 = gemv_persist_supported(N, K) || make_plan1(nsb, 1, kMaxW, p1);   // one-row launch in that order
+    const bool canon1 = gemv_persist_supported(N, K) || make_plan1(nsb, 1, kMaxW, p1, false, true);   // one-row launch in that order
     for (int64_t m0 = 0; m0 < M;) {
         const int left = (int)(M - m0 < 8 ? M - m0 : 8);
         const uint16_t* xm = x + m0 * K;

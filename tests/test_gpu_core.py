@@ -231,6 +231,9 @@ INVARIANCE_CASES = [(6144, 6144, m) for m in (2, 3, 4, 5, 6, 7, 8)] + [
     # persistent row-pair kernel: three tiles per CU with a ragged last tile, two tiles per
     # CU, a single tile, and one tile too many for it (the small-batch kernels take over)
     (6100, 6144, 3), (2050, 4096, 6), (8, 2048, 2), (6144 + 24, 6144, 8),
+    # one-row calls on the 16-row-tile kernel (k_gemv1) against batches on the row-pair and
+    # small-batch kernels
+    (4096, 2048, 3), (8192, 4096, 2), (4096, 8192, 2),
     # no multi-row kernel in the one-row order: one launch per row
     (300, 2816, 5), (64, 5632, 2),
     # K > 8192: the one-row kernel is k_gemv1 (several weight-copy rounds); beyond the
