@@ -9,8 +9,9 @@
 // (XPW of them), stages those pairs' activations itself and keeps their block-diagonal MFMA
 // operands in registers for the whole kernel; for every tile it computes its pairs (8 rows x
 // 2 blocks, one MFMA set) as soon as the round holding them has landed.  Compute wave 0
-// reduces each tile once all its pairs are in and stores the 8 outputs; the copy wave reuses
-// a tile buffer once that tile is reduced (NB buffers).  The copy wave issues its first Q
+// reduces each tile once all its pairs are in and stores the 8 outputs (the workgroup's last
+// tile: the wave whose set completes it); the copy wave reuses a tile buffer once that tile is
+// reduced (NB buffers).  The copy wave issues its first Q
 // rounds before it joins the workgroup barrier.
 //
 // MFMA set (v_mfma_f32_16x16x32_bf16, lane 16g + n): column n = row n & 7 of the tile, block
@@ -167,6 +168,7 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     const HdrSel hs = hdr_sel(g);
     const CodeK ck = code_k();
     int seen = -1;   // highest round known to have landed
+    bool last_done = false;
     for (int t = 0; t < T; ++t) {
 #pragma unroll
         for (int i = 0; i < XPW; ++i) {
@@ -219,13 +221,15 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
             float* rt = s_red + (t % NB) * (kPR * kPMaxPairs);
             if (lane < kPR) rt[lane * kPMaxPairs + p] = ps;
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
-            lds_post(&s_done[t]);
+            if (t == T - 1) last_done = lds_add_rtn(&s_done[t]) == (uint32_t)np - 1u;
+            else lds_post(&s_done[t]);
         }
-        // Wave 0 reduces the tile once every pair is in.  Its own pairs sit in the tile's first
+        // Wave 0 reduces a tile once every pair is in.  Its own pairs sit in the tile's first
         // round, so it has time to spare; the waves of the last round, whose sets finish a tile,
-        // go straight on to the next tile.
-        if (w == 0) {
-            spin_ge(&s_done[t], (uint32_t)np);
+        // go straight on to the next tile.  The workgroup's last tile has no next tile: the wave
+        // whose post completes it reduces it, with no wait.
+        if (t == T - 1 ? last_done : w == 0) {
+            if (t < T - 1) spin_ge(&s_done[t], (uint32_t)np);
             const float* rt = s_red + (t % NB) * (kPR * kPMaxPairs);
             {
                 // v_k on lane 8 * row + k, then the tree (xor 1, xor 2, mirror)
