@@ -458,6 +458,49 @@ def test_mixed_tiles_ragged_fast():
 
 
 
+def _tile_weights(rng, t, rows, K):
+    """(raw bytes, dequantised float32[rows, K]) of a tile; BF16 tiles hold N(0, 0.05^2) bf16."""
+    if t == BF16:
+        bits = qo.random_bf16(rng, (rows, K), scale=0.05)
+        return bits.view(np.uint8).reshape(-1), qo.bf16_bits_to_f32(bits)
+    raw = qo.random_weights(rng, t, rows, K)
+    return raw, qo.dequant_matrix(t, raw, rows, K)
+
+
+# The fp16-operand types (Q8_0, F16) scale each activation row's part by a power of two that
+# puts its largest magnitude in [2^14, 2^15); the bf16-operand types take the activations as
+# they are.  Rows far below and above 1, a row whose elements span 2^-40..2^40, and an all-zero
+# row, at K = 2048 (four rows per launch) and K = 12288 (two rows per launch, two launches).
+@pytest.mark.parametrize("K", [2048, 12288])
+def test_mixed_tiles_activation_range(K):
+    note(f"tiles fast activation range K={K}")
+    rng = np.random.default_rng(37 + K)
+    rows = 32
+    types = [Q4K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16, BF16]
+    tw = [_tile_weights(rng, t, rows, K) for t in types]
+    tiles = [(t, d_u8(r), i * rows, rows) for i, (t, (r, _)) in enumerate(zip(types, tw))]
+    N = rows * len(types)
+    xf = rng.standard_normal((4, K)).astype(np.float32)
+    xf[0] *= np.float32(2.0 ** -60)
+    xf[1] *= np.float32(2.0 ** 60)
+    xf[2] *= np.exp2(rng.integers(-40, 41, K)).astype(np.float32)
+    xf[3] = 0.0
+    x = qo.bf16_round_bits(xf)
+    y, yf = dev.gemv_tiles(tiles, N, K, d_bf16(x), mode="fast", out_f32=True)
+    yb, yfb = h_bits(y), u32(h_f32(yf))
+    for r in range(4):
+        y1, yf1 = dev.gemv_tiles(tiles, N, K, d_bf16(x[r:r + 1]), mode="fast", out_f32=True)
+        assert_bits_equal(u32(h_f32(yf1))[0], yfb[r], f"row {r}: fp32 accumulators vs its one-row launch")
+        assert_bits_equal(h_bits(y1)[0], yb[r], f"row {r}: bf16 outputs vs its one-row launch")
+    assert np.all(h_f32(yf)[3] == 0.0)
+    acc = np.concatenate([co.gemv_ref(t, r, rows, K, x)[0] for t, (r, _) in zip(types, tw)], axis=1)
+    w = np.concatenate([wd for _, wd in tw])
+    ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), h_f32(yf))
+    note(f"  worst |delta| = {worst:.4f} of the 1e-5*sum|a*w| bound")
+    assert ok, worst
+    assert qo.bf16_parity(h_bits(y), acc, w, qo.bf16_bits_to_f32(x))[0]
+
+
 def test_mixed_tiles_detect_corruption():
     """Must-fail twin for the tile path: one Q6_K weight of tile 1 changed (its qh bits) moves
     that output past the gate; the clean tiles pass it."""
