@@ -1336,6 +1336,37 @@ struct ProbUDown {
     }
 };
 
+// The down leg of a two-row pass: workgroup (u * htiles2 + it) computes tiles 2it and 2it + 1
+// of slot u (the second copied while the first computes), each exactly as ProbUDown<2> would.
+struct ProbUDown2 {
+    const uint8_t *D, *shD;
+    const int32_t* uidx;
+    const int32_t* nslots;
+    int htiles2, M;
+    int64_t rb, ebytes, I, H;
+    const uint16_t* h;
+    uint16_t* y;
+    static constexpr uint32_t kPolicy = kNT;
+    static constexpr bool kTwoTiles = true;
+    __device__ bool active(int wg) const { return wg / htiles2 < *nslots; }
+    __device__ const uint16_t* act(int wg, const uint16_t*) const { return h + (int64_t)(wg / htiles2) * M * I; }
+    __device__ TileRef tile(int wg, int part) const {
+        const int u = wg / htiles2, it = 2 * (wg % htiles2) + part;
+        const int e = __builtin_amdgcn_readfirstlane(uidx[u]);
+        const uint8_t* base = e < 0 ? shD : D + (int64_t)e * ebytes;
+        const int64_t nv = H - (int64_t)it * kTR;   // a second tile past H reads as zero
+        return TileRef{base + (nv > 0 ? (int64_t)it * kTR * rb : 0), (int)(nv <= 0 ? 0 : nv < kTR ? nv : kTR), 0};
+    }
+    __device__ void store2(int wg, int n, int r, float v0, float v1) const {
+        if (r >= M) return;
+        const int u = wg / htiles2, it = 2 * (wg % htiles2);
+        const int64_t d = (int64_t)it * kTR + n;
+        uint16_t* yr = y + ((int64_t)u * M + r) * H;
+        if (d < H) yr[d] = (uint16_t)bf16_rne(v0);
+        if (d + kTR < H) yr[d + kTR] = (uint16_t)bf16_rne(v1);
+    }
+};
+
 // Gate/up with the SwiGLU fused, for the small-batch kernel: workgroup (u * itiles + it)
 // computes rows it*16.. of both the gate and the up projection of slot u (two tiles, the
 // second copied while the first computes) and writes h[u][m][i] = bf16(silu(g) * u) -- the
@@ -1399,6 +1430,12 @@ static hipError_t union_gemvs(const MoeUnionArgs& a, hipStream_t st) {
         if (e == hipSuccess) e = a.after_gateup(st);
     }
     if (e != hipSuccess) return e;
+    if (MR == 2 && make_plans((int)(a.I / QK_K), psI)) {
+        // two rows: two tiles of the slot per workgroup
+        const int htiles2 = (htiles + 1) / 2;
+        const ProbUDown2 pd{a.D, a.shD, a.uidx, a.nslots, htiles2, a.M, rbI, rbI * a.H, a.I, a.H, a.h, a.y};
+        return runs_mr<2>(pd, psI, (unsigned)(a.max_slots * htiles2), a.h, (int)a.I, st);
+    }
     const ProbUDown<MR> pd{a.D, a.shD, a.uidx, a.nslots, htiles, a.M, rbI, rbI * a.H, a.I, a.H, a.h, a.y};
     return union_leg<MR>(pd, (int)(a.I / QK_K), (unsigned)(a.max_slots * htiles), a.h, (int)a.I, st);
 }

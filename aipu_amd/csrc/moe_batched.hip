@@ -16,6 +16,7 @@
 #include "common.hpp"
 #include "glm_act.hpp"
 #include "launch.hpp"
+#include "route.hpp"
 
 namespace aipu {
 namespace {
@@ -90,6 +91,91 @@ __global__ __launch_bounds__(64) void k_union(const int32_t* __restrict__ sel, c
         uint32_t g = kInactive;
         for (int t = 0; t < topk; ++t)
             if (sel[r * topk + t] == ulist[u]) g = (uint32_t)selw[r * topk + t] << 16;
+        ugate[r * ms + u] = g;
+    }
+}
+
+// The routing of every row of a pass and their union in one workgroup, for E <= kRouteMaxE:
+// the decision of route_workgroup (k_router_rank_rows) for all rows at once -- the keys of
+// as many rows as give two threads per key, every key's rank counted by two threads over
+// half the keys each, the slot weights of each row on a lane of its own -- then the union of
+// k_union over the decisions held in LDS.  One launch instead of two.
+constexpr int kRUThreads = 2 * kRouteMaxE;
+__global__ __launch_bounds__(kRUThreads) void k_route_union(const uint16_t* __restrict__ logits, int M, int E,
+                                                            int topk, uint32_t scale_bits, int32_t* __restrict__ sel,
+                                                            uint16_t* __restrict__ selw, int32_t* sel2, uint16_t* selw2,
+                                                            int shared, int ms, int32_t* __restrict__ uidx,
+                                                            int32_t* __restrict__ nslots, uint32_t* __restrict__ ugate) {
+    __shared__ __align__(16) uint32_t keys[kRUThreads / 2];
+    __shared__ uint32_t win[kRowsPerPass * kRouteMaxTopk];
+    __shared__ int32_t s_sel[kRowsPerPass * kRouteMaxTopk];
+    __shared__ uint16_t s_selw[kRowsPerPass * kRouteMaxTopk];
+    __shared__ uint8_t flag[kRouteMaxE];
+    __shared__ int32_t ulist[kRowsPerPass * kRouteMaxTopk];
+    __shared__ int s_count;
+    const int t = threadIdx.x, nthr = blockDim.x;
+    const int e8 = (E + 7) & ~7;   // keys padded with zeros (below every key) to whole 16-B reads
+    const int rpi = (nthr / 2) / e8;   // rows ranked together (>= 1 for E <= kRouteMaxE)
+    for (int r0 = 0; r0 < M; r0 += rpi) {
+        const int nr = M - r0 < rpi ? M - r0 : rpi;
+        for (int i = t; i < nr * e8; i += nthr) {
+            const int rr = i / e8, e = i - rr * e8;
+            keys[i] = e < E ? route_key(logits[(int64_t)(r0 + rr) * E + e], e) : 0u;
+        }
+        __syncthreads();
+        const int rr = t / (2 * e8), k = (t >> 1) - rr * e8, half = t & 1;
+        if (rr < nr && k < E) {
+            const uint32_t my = keys[rr * e8 + k];
+            const uint4* kp = (const uint4*)(keys + rr * e8 + half * (e8 / 2));
+            int rank = 0;
+#pragma unroll 8
+            for (int j = 0; j < e8 / 8; ++j) {
+                const uint4 k4 = kp[j];
+                rank += (k4.x > my) + (k4.y > my) + (k4.z > my) + (k4.w > my);
+            }
+            rank += __shfl_xor(rank, 1, 64);
+            if (rank < topk && half == 0) win[(r0 + rr) * kRouteMaxTopk + rank] = my;
+        }
+        __syncthreads();
+    }
+    if (t < M) route_weights(win + t * kRouteMaxTopk, topk, scale_bits, s_sel + t * topk, s_selw + t * topk);
+    for (int e = t; e < E; e += nthr) flag[e] = 0;
+    __syncthreads();
+    for (int i = t; i < M * topk; i += nthr) {
+        const int e = s_sel[i];
+        sel[i] = e;
+        selw[i] = s_selw[i];
+        if (sel2) sel2[i] = e;
+        if (selw2) selw2[i] = s_selw[i];
+        if (e >= 0 && e < E) flag[e] = 1;
+    }
+    __syncthreads();
+    if (t < 64) {   // one wave lists the flagged experts in ascending index
+        int count = 0;
+        for (int c = 0; c < E; c += 64) {
+            const int e = c + t;
+            const bool f = e < E && flag[e];
+            const uint64_t b = __ballot(f);
+            const int pos = count + __popcll(b & ((1ull << t) - 1ull));
+            if (f) {
+                uidx[pos] = e;
+                ulist[pos] = e;
+            }
+            count += __popcll(b);
+        }
+        if (t == 0) {
+            if (shared) uidx[count] = -1;
+            *nslots = count + (shared ? 1 : 0);
+            s_count = count;
+        }
+    }
+    __syncthreads();
+    const int count = s_count;
+    for (int i = t; i < M * count; i += nthr) {
+        const int r = i / count, u = i - r * count;
+        uint32_t g = kInactive;
+        for (int k = 0; k < topk; ++k)
+            if (s_sel[r * topk + k] == ulist[u]) g = (uint32_t)s_selw[r * topk + k] << 16;
         ugate[r * ms + u] = g;
     }
 }
@@ -174,11 +260,16 @@ hipError_t fast_pass(const MoeArgs& a, int64_t r0, int M, const BLayout& L, hipS
     } else {   // past the mixed-type kernel's staging limit: the exact kernel (within any tolerance)
         AIPU_TRY(launch_gemv_ref(a.router_type, a.router_w, a.E, a.H, x, M, logits, nullptr, st));
     }
-    AIPU_TRY(launch_router_tail_rows(logits, M, (int)a.E, a.topk, a.scale_bits, sel, selw,
-                                     a.sel_idx_out ? a.sel_idx_out + r0 * a.topk : nullptr,
-                                     a.sel_w_out ? a.sel_w_out + r0 * a.topk : nullptr, st));
-    hipLaunchKernelGGL(k_union, dim3(1), dim3(64), 0, st, sel, selw, M, a.topk, (int)a.E, shared ? 1 : 0, ms, uidx,
-                       nsl, ugate);
+    int32_t* sel2 = a.sel_idx_out ? a.sel_idx_out + r0 * a.topk : nullptr;
+    uint16_t* selw2 = a.sel_w_out ? a.sel_w_out + r0 * a.topk : nullptr;
+    if (a.E <= kRouteMaxE && a.topk <= kRouteMaxTopk) {
+        hipLaunchKernelGGL(k_route_union, dim3(1), dim3(kRUThreads), 0, st, logits, M, (int)a.E, a.topk, a.scale_bits,
+                           sel, selw, sel2, selw2, shared ? 1 : 0, ms, uidx, nsl, ugate);
+    } else {
+        AIPU_TRY(launch_router_tail_rows(logits, M, (int)a.E, a.topk, a.scale_bits, sel, selw, sel2, selw2, st));
+        hipLaunchKernelGGL(k_union, dim3(1), dim3(64), 0, st, sel, selw, M, a.topk, (int)a.E, shared ? 1 : 0, ms, uidx,
+                           nsl, ugate);
+    }
     AIPU_TRY(hipGetLastError());
     MoeUnionArgs u;
     u.G = a.gate_exps;
