@@ -67,7 +67,7 @@ struct ProbPlain {
     int M;
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
-    static constexpr bool kTwoTiles = false;
+    static constexpr int kTiles = 1;
     static constexpr uint32_t kPolicy = kNT;   // weights stream past the caches
     static constexpr int kRows = MR;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
@@ -751,8 +751,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     constexpr int XI = (2 * XP + 63) / 64;   // pieces per lane for a pair of rows
     constexpr uint32_t kPair = GS * 1024u;   // operand entries of a pair of rows
     constexpr uint32_t kRed = kPair;         // block terms [n][column][block], after the entries in the slice
-    static_assert(kRed + kTR * kSmallMaxRows * GS * 4 <= (uint32_t)Dma<GS>::kBytes, "slice holds a pair and the block terms");
-    static_assert(!Prob::kTwoTiles || MR == 2, "the second tile's copy reuses the slice rows 2, 3 would use");
+    constexpr int NT = Prob::kTiles;         // tiles per workgroup (the next one copied while one computes)
+    constexpr int kCols = 2 * NT > kSmallMaxRows ? 2 * NT : kSmallMaxRows;   // block-term columns per row
+    static_assert(kRed + kTR * kCols * GS * 4 <= (uint32_t)Dma<GS>::kBytes, "slice holds a pair and the block terms");
+    static_assert(NT == 1 || MR == 2, "a later tile's copy reuses the slice rows 2, 3 would use");
     __shared__ __align__(16) uint8_t s_act[NW * kPair];
     extern __shared__ __align__(16) uint8_t s_w[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -827,12 +829,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
             R[b].q1 = *(const uint4*)(p + 32 + 32 * g);
         }
     };
+    auto copy_tile = [&](int k) {   // once the slice has been read: tile k into it
+        regs_consumed(R);
+        const TileRef tk = pb.tile(wg, k);
+        dma_group<GS, Prob::kPolicy>(buf_rsrc(tk.base, (uint32_t)(tk.nvalid * rb)), wW, rb, kb0, lane);
+    };
     read_slice();
-    if constexpr (Prob::kTwoTiles) {
-        regs_consumed(R);   // the slice has been read: copy the second tile into it
-        const TileRef t1 = pb.tile(wg, 1);
-        dma_group<GS, Prob::kPolicy>(buf_rsrc(t1.base, (uint32_t)(t1.nvalid * rb)), wW, rb, kb0, lane);
-    }
+    if constexpr (NT > 1) copy_tile(1);
     if (MR > 2 && rows > 2) stage_pair(xb, wW, sb);
 
     // 3. the blocks
@@ -844,13 +847,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     const int md = (n - 4 * g) & 3;   // the diagonal lanes' activation row
     const uint32_t abase = lds_addr((md < 2 ? wA : wW) + 16u * (uint32_t)(g * 2 + (md & 1)));
     const uint64_t mask = ((1ull << rows) - 1) * 0x1000010000100001ull;   // diag_mask(rows)
-    constexpr int NT = Prob::kTwoTiles ? 2 : 1;
     float bt[NT][GS];   // block terms: lane 16i + n holds row n, activation row i
 #pragma unroll
     for (int tile = 0; tile < NT; ++tile) {
-    if (tile > 0) {   // the second tile's weights (the compiler waits for the copies)
+    if (tile > 0) {   // this tile's weights (the compiler waits for the copies), then the next tile's copy
         __builtin_amdgcn_sched_barrier(0);
         read_slice();
+        if (tile + 1 < NT) copy_tile(tile + 1);
     }
 #pragma unroll
     for (int b = 0; b < GS; ++b) {
@@ -893,7 +896,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     {
         const int i = lane >> 4;   // activation row (MR = 2: rows 0, 1 twice)
         if (i < MR) {
-            float* te = (float*)(wW + kRed) + kSmallMaxRows * GS * n;
+            float* te = (float*)(wW + kRed) + kCols * GS * n;
 #pragma unroll
             for (int k = 0; k < NT; ++k)
 #pragma unroll
@@ -908,14 +911,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         const bool valid = o < kTR * kSmallMaxRows && r < rows;
         auto term = [&](int c, int b) {
             const int k = b / GS;   // the K part (wave) holding block b
-            return ((const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes + kRed))[(kSmallMaxRows * rn + c) * GS + (b - k * GS)];
+            return ((const float*)(s_w + (uint32_t)k * Dma<GS>::kBytes + kRed))[(kCols * rn + c) * GS + (b - k * GS)];
         };
-        const float v = canon_sum8(nsb, lane & 7, [&](int b) { return term(r, b); });
-        if constexpr (Prob::kTwoTiles) {
-            const float v2 = canon_sum8(nsb, lane & 7, [&](int b) { return term(2 + r, b); });
-            if (valid && (lane & 7) == 0) pb.store2(wg, rn, r, v, v2);
-        } else if (valid && (lane & 7) == 0) {
-            pb.store(wg, rn, r, v);
+        if constexpr (NT > 1) {
+            float v[NT];
+#pragma unroll
+            for (int k = 0; k < NT; ++k) v[k] = canon_sum8(nsb, lane & 7, [&](int b) { return term(2 * k + r, b); });
+            if (valid && (lane & 7) == 0) pb.store_tiles(wg, rn, r, v);
+        } else {
+            const float v = canon_sum8(nsb, lane & 7, [&](int b) { return term(r, b); });
+            if (valid && (lane & 7) == 0) pb.store(wg, rn, r, v);
         }
     }
 }
@@ -1288,7 +1293,7 @@ struct ProbUGateUp {
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
     static constexpr uint32_t kPolicy = kNT;   // streaming (default caching measured slower here)
-    static constexpr bool kTwoTiles = false;
+    static constexpr int kTiles = 1;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int wg) const { return wg / (2 * itiles) < *nslots; }
     __device__ const uint16_t* act(int, const uint16_t* X) const { return X; }
@@ -1317,7 +1322,7 @@ struct ProbUDown {
     static constexpr bool kRoutes = false;
     static constexpr bool kShareAct = false;
     static constexpr uint32_t kPolicy = kNT;   // streaming (default caching measured slower here)
-    static constexpr bool kTwoTiles = false;
+    static constexpr int kTiles = 1;
     __device__ void setup(int, uint32_t*, uint32_t*, int32_t*, uint16_t*) {}
     __device__ bool active(int wg) const { return wg / htiles < *nslots; }
     __device__ const uint16_t* act(int wg, const uint16_t*) const { return h + (int64_t)(wg / htiles) * M * I; }
@@ -1336,36 +1341,41 @@ struct ProbUDown {
     }
 };
 
-// The down leg of a two-row pass: workgroup (u * htiles2 + it) computes tiles 2it and 2it + 1
-// of slot u (the second copied while the first computes), each exactly as ProbUDown<2> would.
-struct ProbUDown2 {
+// The down leg of a two-row pass: workgroup (u * htilesT + it) computes tiles NT it .. NT it +
+// NT - 1 of slot u (each copied while the one before computes), each exactly as ProbUDown<2>
+// would.
+template <int NT>
+struct ProbUDownT {
     const uint8_t *D, *shD;
     const int32_t* uidx;
     const int32_t* nslots;
-    int htiles2, M;
+    int htilesT, M;
     int64_t rb, ebytes, I, H;
     const uint16_t* h;
     uint16_t* y;
     static constexpr uint32_t kPolicy = kNT;
-    static constexpr bool kTwoTiles = true;
-    __device__ bool active(int wg) const { return wg / htiles2 < *nslots; }
-    __device__ const uint16_t* act(int wg, const uint16_t*) const { return h + (int64_t)(wg / htiles2) * M * I; }
+    static constexpr int kTiles = NT;
+    __device__ bool active(int wg) const { return wg / htilesT < *nslots; }
+    __device__ const uint16_t* act(int wg, const uint16_t*) const { return h + (int64_t)(wg / htilesT) * M * I; }
     __device__ TileRef tile(int wg, int part) const {
-        const int u = wg / htiles2, it = 2 * (wg % htiles2) + part;
+        const int u = wg / htilesT, it = NT * (wg % htilesT) + part;
         const int e = __builtin_amdgcn_readfirstlane(uidx[u]);
         const uint8_t* base = e < 0 ? shD : D + (int64_t)e * ebytes;
-        const int64_t nv = H - (int64_t)it * kTR;   // a second tile past H reads as zero
+        const int64_t nv = H - (int64_t)it * kTR;   // a tile past H reads as zero
         return TileRef{base + (nv > 0 ? (int64_t)it * kTR * rb : 0), (int)(nv <= 0 ? 0 : nv < kTR ? nv : kTR), 0};
     }
-    __device__ void store2(int wg, int n, int r, float v0, float v1) const {
+    __device__ void store_tiles(int wg, int n, int r, const float (&v)[NT]) const {
         if (r >= M) return;
-        const int u = wg / htiles2, it = 2 * (wg % htiles2);
-        const int64_t d = (int64_t)it * kTR + n;
+        const int u = wg / htilesT;
         uint16_t* yr = y + ((int64_t)u * M + r) * H;
-        if (d < H) yr[d] = (uint16_t)bf16_rne(v0);
-        if (d + kTR < H) yr[d + kTR] = (uint16_t)bf16_rne(v1);
+#pragma unroll
+        for (int k = 0; k < NT; ++k) {
+            const int64_t d = (int64_t)(NT * (wg % htilesT) + k) * kTR + n;
+            if (d < H) yr[d] = (uint16_t)bf16_rne(v[k]);
+        }
     }
 };
+constexpr int kDownTiles = 4;
 
 // Gate/up with the SwiGLU fused, for the small-batch kernel: workgroup (u * itiles + it)
 // computes rows it*16.. of both the gate and the up projection of slot u (two tiles, the
@@ -1379,7 +1389,7 @@ struct ProbUGateUpH {
     int64_t rb, ebytes, I;
     uint16_t* h;
     static constexpr uint32_t kPolicy = kNT;   // streaming (default caching measured slower here)
-    static constexpr bool kTwoTiles = true;
+    static constexpr int kTiles = 2;
     __device__ bool active(int wg) const { return wg / itiles < *nslots; }
     __device__ const uint16_t* act(int, const uint16_t* X) const { return X; }
     __device__ TileRef tile(int wg, int part) const {
@@ -1388,10 +1398,11 @@ struct ProbUGateUpH {
         const uint8_t* base = e < 0 ? (part ? shU : shG) : (part ? U : G) + (int64_t)e * ebytes;
         return TileRef{base + (int64_t)it * kTR * rb, kTR, 0};
     }
-    __device__ void store2(int wg, int n, int r, float g, float v) const {
+    __device__ void store_tiles(int wg, int n, int r, const float (&v)[2]) const {
         if (r >= M) return;
+        const float g = v[0];
         const int u = wg / itiles, it = wg % itiles;
-        const uint32_t gb = bf16_rne(g), ub = bf16_rne(v);
+        const uint32_t gb = bf16_rne(g), ub = bf16_rne(v[1]);
         h[((int64_t)u * M + r) * I + (int64_t)it * kTR + n] =
             (uint16_t)bf16_rne(bf16_to_f32(glm_silu_bf16(gb)) * bf16_to_f32(ub));
     }
@@ -1431,10 +1442,10 @@ static hipError_t union_gemvs(const MoeUnionArgs& a, hipStream_t st) {
     }
     if (e != hipSuccess) return e;
     if (MR == 2 && make_plans((int)(a.I / QK_K), psI)) {
-        // two rows: two tiles of the slot per workgroup
-        const int htiles2 = (htiles + 1) / 2;
-        const ProbUDown2 pd{a.D, a.shD, a.uidx, a.nslots, htiles2, a.M, rbI, rbI * a.H, a.I, a.H, a.h, a.y};
-        return runs_mr<2>(pd, psI, (unsigned)(a.max_slots * htiles2), a.h, (int)a.I, st);
+        // two rows: kDownTiles tiles of the slot per workgroup
+        const int htilesT = (htiles + kDownTiles - 1) / kDownTiles;
+        const ProbUDownT<kDownTiles> pd{a.D, a.shD, a.uidx, a.nslots, htilesT, a.M, rbI, rbI * a.H, a.I, a.H, a.h, a.y};
+        return runs_mr<2>(pd, psI, (unsigned)(a.max_slots * htilesT), a.h, (int)a.I, st);
     }
     const ProbUDown<MR> pd{a.D, a.shD, a.uidx, a.nslots, htiles, a.M, rbI, rbI * a.H, a.I, a.H, a.h, a.y};
     return union_leg<MR>(pd, (int)(a.I / QK_K), (unsigned)(a.max_slots * htiles), a.h, (int)a.I, st);
