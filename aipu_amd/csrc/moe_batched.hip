@@ -95,50 +95,56 @@ __global__ __launch_bounds__(64) void k_union(const int32_t* __restrict__ sel, c
     }
 }
 
+// Largest value over the wave (DPP: prefix maxima within each row of 16 lanes, then rows 0-1 and
+// 0-3 meet in lanes 31 and 63).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x111, 0xF, 0xF, false));   // row_shr:1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x112, 0xF, 0xF, false));   // row_shr:2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x114, 0xF, 0xF, false));   // row_shr:4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x118, 0xF, 0xF, false));   // row_shr:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));   // row_bcast:15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // The routing of every row of a pass and their union in one workgroup, for E <= kRouteMaxE:
-// the decision of route_workgroup (k_router_rank_rows) for all rows at once -- the keys of
-// as many rows as give two threads per key, every key's rank counted by two threads over
-// half the keys each, the slot weights of each row on a lane of its own -- then the union of
-// k_union over the decisions held in LDS.  One launch instead of two.
-constexpr int kRUThreads = 2 * kRouteMaxE;
+// wave r routes row r (route.hpp's decision: lane l holds the keys of experts l + 64j, and
+// topk rounds each take the largest remaining key, so the winners come out in slot order),
+// its lane 0 forms the slot weights; then the union of k_union over the decisions held in
+// LDS.  One launch instead of two.
+constexpr int kRUThreads = 64 * kRowsPerPass;
+constexpr int kRUKeys = kRouteMaxE / 64;   // keys per lane
 __global__ __launch_bounds__(kRUThreads) void k_route_union(const uint16_t* __restrict__ logits, int M, int E,
                                                             int topk, uint32_t scale_bits, int32_t* __restrict__ sel,
                                                             uint16_t* __restrict__ selw, int32_t* sel2, uint16_t* selw2,
                                                             int shared, int ms, int32_t* __restrict__ uidx,
                                                             int32_t* __restrict__ nslots, uint32_t* __restrict__ ugate) {
-    __shared__ __align__(16) uint32_t keys[kRUThreads / 2];
     __shared__ uint32_t win[kRowsPerPass * kRouteMaxTopk];
     __shared__ int32_t s_sel[kRowsPerPass * kRouteMaxTopk];
     __shared__ uint16_t s_selw[kRowsPerPass * kRouteMaxTopk];
     __shared__ uint8_t flag[kRouteMaxE];
     __shared__ int32_t ulist[kRowsPerPass * kRouteMaxTopk];
     __shared__ int s_count;
-    const int t = threadIdx.x, nthr = blockDim.x;
-    const int e8 = (E + 7) & ~7;   // keys padded with zeros (below every key) to whole 16-B reads
-    const int rpi = (nthr / 2) / e8;   // rows ranked together (>= 1 for E <= kRouteMaxE)
-    for (int r0 = 0; r0 < M; r0 += rpi) {
-        const int nr = M - r0 < rpi ? M - r0 : rpi;
-        for (int i = t; i < nr * e8; i += nthr) {
-            const int rr = i / e8, e = i - rr * e8;
-            keys[i] = e < E ? route_key(logits[(int64_t)(r0 + rr) * E + e], e) : 0u;
+    const int t = threadIdx.x, nthr = blockDim.x, lane = t & 63;
+    const int r = __builtin_amdgcn_readfirstlane(t >> 6);
+    if (r < M) {
+        uint32_t k[kRUKeys];
+#pragma unroll
+        for (int j = 0; j < kRUKeys; ++j) {
+            const int e = lane + 64 * j;
+            k[j] = e < E ? route_key(logits[(int64_t)r * E + e], e) : 0u;   // 0 is below every key
         }
-        __syncthreads();
-        const int rr = t / (2 * e8), k = (t >> 1) - rr * e8, half = t & 1;
-        if (rr < nr && k < E) {
-            const uint32_t my = keys[rr * e8 + k];
-            const uint4* kp = (const uint4*)(keys + rr * e8 + half * (e8 / 2));
-            int rank = 0;
-#pragma unroll 8
-            for (int j = 0; j < e8 / 8; ++j) {
-                const uint4 k4 = kp[j];
-                rank += (k4.x > my) + (k4.y > my) + (k4.z > my) + (k4.w > my);
-            }
-            rank += __shfl_xor(rank, 1, 64);
-            if (rank < topk && half == 0) win[(r0 + rr) * kRouteMaxTopk + rank] = my;
+        for (int i = 0; i < topk; ++i) {
+            uint32_t head = k[0];
+#pragma unroll
+            for (int j = 1; j < kRUKeys; ++j) head = max(head, k[j]);
+            const uint32_t m = wave_max_u32(head);   // keys are distinct: one lane and register hold it
+#pragma unroll
+            for (int j = 0; j < kRUKeys; ++j) k[j] = k[j] == m ? 0u : k[j];
+            if (lane == 0) win[r * kRouteMaxTopk + i] = m;
         }
-        __syncthreads();
+        if (lane == 0) route_weights(win + r * kRouteMaxTopk, topk, scale_bits, s_sel + r * topk, s_selw + r * topk);
     }
-    if (t < M) route_weights(win + t * kRouteMaxTopk, topk, scale_bits, s_sel + t * topk, s_selw + t * topk);
     for (int e = t; e < E; e += nthr) flag[e] = 0;
     __syncthreads();
     for (int i = t; i < M * topk; i += nthr) {
@@ -172,11 +178,11 @@ __global__ __launch_bounds__(kRUThreads) void k_route_union(const uint16_t* __re
     __syncthreads();
     const int count = s_count;
     for (int i = t; i < M * count; i += nthr) {
-        const int r = i / count, u = i - r * count;
+        const int rr = i / count, u = i - rr * count;
         uint32_t g = kInactive;
-        for (int k = 0; k < topk; ++k)
-            if (s_sel[r * topk + k] == ulist[u]) g = (uint32_t)s_selw[r * topk + k] << 16;
-        ugate[r * ms + u] = g;
+        for (int q = 0; q < topk; ++q)
+            if (s_sel[rr * topk + q] == ulist[u]) g = (uint32_t)s_selw[rr * topk + q] << 16;
+        ugate[rr * ms + u] = g;
     }
 }
 
