@@ -296,26 +296,31 @@ struct MixArgs {
     int n, nwg, split;
 };
 
-// Per-wave activation region of one row: the operand entries [2XI blocks][8 MFMAs][4 K-groups]
-// of 16 B (512 B per block), then the sums the type's chains are seeded with (Q4_K: 8 sub-block
-// sums per block [b][g][h]; Q6_K: 16 sums of 16 [b][g][t]; Q8_0: 8 block sums [b][2g + c]).
+// Per-wave activation region of one row: a ring of four block slots, block b in slot b % 4.
+// A slot holds the operand entries [8 MFMAs][4 K-groups] of 16 B (512 B per block), and the
+// slots' sums that the type's chains are seeded with follow (Q4_K: 8 sub-block sums per block
+// [slot][g][h]; Q6_K: 16 sums of 16 [slot][g][t]; Q8_0: 8 block sums [slot][2g + c]).
 // Entry (b, s, g) holds the 8 activations that lane group g multiplies in MFMA s of block b:
 //   Q4_K: pieces 32b + 8g + s in the element order of mfma_gemv.hpp (act_perm);
 //   Q6_K: positions 128(g>>1) + 32(s>>1) + 16(g&1) + 8(s&1) + e, e = 0..7;
 //   Q8_0, F16, BF16: positions 64g + 8s + e;
-// fp16 (scaled) for Q8_0 and F16, bf16 otherwise.
-template <int XI>
+// fp16 (scaled) for Q8_0 and F16, bf16 otherwise.  A wave stages blocks 0..3 of its part
+// before its first group and blocks 2i, 2i + 1 (i >= 2) into the slots of blocks 2i - 4,
+// 2i - 3 just before the first group that needs them; groups of at most three blocks run in
+// order, so those blocks have been used by then.  Four slots per row, not the whole part,
+// keep four rows and the weight slices within half the CU's LDS: two workgroups share a CU.
+constexpr int kRing = 4;
 struct ActRegion {
-    static constexpr int kBlocks = 2 * XI;
-    static constexpr int kBytes = kBlocks * (512 + 64);
-    static constexpr int kSumOff = kBlocks * 512;
+    static constexpr int kBytes = kRing * (512 + 64);
+    static constexpr int kSumOff = kRing * 512;
 };
 
 template <int TYPE, int XI, int MR>
 __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16_t* __restrict__ X, int K, int M,
                                          uint8_t* wA, uint8_t* wW, float* red, uint16_t* Y, float* Yf, int64_t ys) {
     typedef Geom<TYPE> G;
-    typedef ActRegion<XI> AR;
+    typedef ActRegion AR;
+    static_assert(G::GS <= 3, "a group must not reach back to the slots it restages");
     constexpr bool kHalf = TYPE == T_Q8_0 || TYPE == T_F16;   // fp16 operands, scaled activations
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -346,12 +351,11 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
     dma.issue(wr, wW, kb0, bpk < G::GS ? bpk : G::GS);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. stage (every piece of the region, so blocks past bpk hold zeros); row m at m * kBytes
+    // 3. the row exponents (fp16 operands), then stage blocks 0..3 (every piece, so blocks past
+    // bpk hold zeros); row m at m * kBytes
     int ex[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-        uint8_t* rA = wA + m * AR::kBytes;
-        float* wS = (float*)(rA + AR::kSumOff);
         ex[m] = 0;
         if constexpr (kHalf) {
             uint32_t mx = 0;
@@ -365,9 +369,14 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
             for (int s = 32; s >= 1; s >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, s, 64));
             ex[m] = part_exponent(mx);
         }
+    }
+    // pieces q = lane + 64 i (blocks 2i, 2i + 1) of every row into their ring slots
+    auto stage = [&](int i) {
 #pragma unroll
-        for (int i = 0; i < XI; ++i) {
-            const int q = lane + 64 * i, bb = q >> 5, qq = q & 31;
+        for (int m = 0; m < MR; ++m) {
+            uint8_t* rA = wA + m * AR::kBytes;
+            float* wS = (float*)(rA + AR::kSumOff);
+            const int q = lane + 64 * i, bb = (q >> 5) & (kRing - 1), qq = q & 31;
             if constexpr (TYPE == T_Q4_K) {
                 const uint32_t ones = 0x3F803F80u;
                 float sm = 0.f;
@@ -416,7 +425,16 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
                 }
             }
         }
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < XI && i < kRing / 2; ++i) stage(i);
+    // the ring slot of block b, and the restaging of blocks 2i, 2i + 1 (i >= 2) before group gi
+    auto slot = [](int b) { return b & (kRing - 1); };
+    auto restage = [&](int gi) {
+#pragma unroll
+        for (int i = kRing / 2; i < XI; ++i)
+            if (gi == (2 * i) / G::GS) stage(i);
+    };
 
     // 4. group loop: the lane's weights of a group, made into operands once, against every row.
     // The diagonal lane 16g + 4g + m reads row m's entries (the others stay zero).
@@ -449,9 +467,10 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
                 const int nxt = (gi + 1) * G::GS;
                 dma.issue(wr, wW, kb0 + nxt, bpk - nxt);
             }
+            restage(gi);
 #pragma unroll
             for (int bb = 0; bb < G::GS; ++bb) {
-                const int b = gi * G::GS + bb;
+                const int b = slot(gi * G::GS + bb);
                 a_reads(A, aLane + 512u * (uint32_t)b, dmask);
                 float2 as[MR];
 #pragma unroll
@@ -476,9 +495,10 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
                 const int nxt = (gi + 1) * G::GS;
                 dma.issue(wr, wW, kb0 + nxt, bpk - nxt);
             }
+            restage(gi);
 #pragma unroll
             for (int bb = 0; bb < G::GS; ++bb) {
-                const int b = gi * G::GS + bb;
+                const int b = slot(gi * G::GS + bb);
                 a_reads(A, aLane + 512u * (uint32_t)b, dmask);
                 if constexpr (TYPE == T_Q6_K) {
                     float4 sg[MR];
@@ -506,7 +526,8 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
                 regs_consumed(R);   // the slice has been read: refill it
                 dma.issue(wr, wW, kb0 + gi + 1, bpk - gi - 1);
             }
-            a_reads(A, aLane + 512u * (uint32_t)gi, dmask);
+            restage(gi);
+            a_reads(A, aLane + 512u * (uint32_t)slot(gi), dmask);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const u32x4_t b0 = {R[0].v[s].x, R[0].v[s].y, R[0].v[s].z, R[0].v[s].w};
@@ -551,7 +572,7 @@ __device__ __forceinline__ void mix_body(const MixTile& T, int grp, const uint16
 template <int XI, int MR>
 __global__ __launch_bounds__(kMixW * 64) void k_mixed(MixArgs args, const uint16_t* __restrict__ X, int K, int M,
                                                       uint16_t* __restrict__ Y, float* __restrict__ Yf, int64_t ys) {
-    typedef ActRegion<XI> AR;
+    typedef ActRegion AR;
     // the staged activations live in a static LDS object of their own and the weight
     // slices in the dynamic one, so the compiler can tell the staging writes from the
     // direct-to-LDS loads in flight and does not make them wait for those
@@ -576,8 +597,8 @@ __global__ __launch_bounds__(kMixW * 64) void k_mixed(MixArgs args, const uint16
     }
 }
 
-// Blocks per wave the activation region of k_mixed<XI> holds (every type's groups rounded
-// up to whole groups must fit): 2 XI blocks.  A wave's bpk blocks round up to
+// Blocks per wave that k_mixed<XI> loads as XI 16-B pieces per lane and row (every type's groups
+// rounded up to whole groups must fit): 2 XI blocks.  A wave's bpk blocks round up to
 // max(3 ceil(bpk / 3), 2 ceil(bpk / 2)) = 3, 3, 4, 6, 6, 6, 9, 9, ... blocks, so 1-3 blocks per
 // wave take XI = 2, 4-6 take XI = 3 and 7-16 take XI = 8.
 int mix_xi(int64_t K) {
@@ -587,8 +608,8 @@ int mix_xi(int64_t K) {
     return need <= 4 ? 2 : need <= 6 ? 3 : need <= 16 ? 8 : 0;
 }
 
-// Activation rows per launch that the LDS holds beside the weight slices (160 KB): four up
-// to 6 blocks per wave (K <= 6144), two beyond (K <= 16384).
+// Activation rows per launch: four up to 6 blocks per wave (K <= 6144); beyond (K <= 16384) the
+// rows' eight piece registers per lane leave room for two.
 int mix_rows(int xi) { return xi <= 3 ? 4 : 2; }
 
 bool mix_type(int t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0 || t == T_F16 || t == T_BF16; }
