@@ -95,25 +95,11 @@ __global__ __launch_bounds__(64) void k_union(const int32_t* __restrict__ sel, c
     }
 }
 
-// Largest value over the wave (DPP: prefix maxima within each row of 16 lanes, then rows 0-1 and
-// 0-3 meet in lanes 31 and 63).
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x111, 0xF, 0xF, false));   // row_shr:1
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x112, 0xF, 0xF, false));   // row_shr:2
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x114, 0xF, 0xF, false));   // row_shr:4
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x118, 0xF, 0xF, false));   // row_shr:8
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));   // row_bcast:15
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));   // row_bcast:31
-    return __builtin_amdgcn_readlane(v, 63);
-}
-
 // The routing of every row of a pass and their union in one workgroup, for E <= kRouteMaxE:
-// wave r routes row r (route.hpp's decision: lane l holds the keys of experts l + 64j, and
-// topk rounds each take the largest remaining key, so the winners come out in slot order),
-// its lane 0 forms the slot weights; then the union of k_union over the decisions held in
+// wave r routes row r (route.hpp's decision, route_tournament on keys it forms itself), its
+// lane 0 forms the slot weights; then the union of k_union over the decisions held in
 // LDS.  One launch instead of two.
 constexpr int kRUThreads = 64 * kRowsPerPass;
-constexpr int kRUKeys = kRouteMaxE / 64;   // keys per lane
 __global__ __launch_bounds__(kRUThreads) void k_route_union(const uint16_t* __restrict__ logits, int M, int E,
                                                             int topk, uint32_t scale_bits, int32_t* __restrict__ sel,
                                                             uint16_t* __restrict__ selw, int32_t* sel2, uint16_t* selw2,
@@ -128,21 +114,13 @@ __global__ __launch_bounds__(kRUThreads) void k_route_union(const uint16_t* __re
     const int t = threadIdx.x, nthr = blockDim.x, lane = t & 63;
     const int r = __builtin_amdgcn_readfirstlane(t >> 6);
     if (r < M) {
-        uint32_t k[kRUKeys];
+        uint32_t k[kRouteKeysPerLane];
 #pragma unroll
-        for (int j = 0; j < kRUKeys; ++j) {
+        for (int j = 0; j < kRouteKeysPerLane; ++j) {
             const int e = lane + 64 * j;
             k[j] = e < E ? route_key(logits[(int64_t)r * E + e], e) : 0u;   // 0 is below every key
         }
-        for (int i = 0; i < topk; ++i) {
-            uint32_t head = k[0];
-#pragma unroll
-            for (int j = 1; j < kRUKeys; ++j) head = max(head, k[j]);
-            const uint32_t m = wave_max_u32(head);   // keys are distinct: one lane and register hold it
-#pragma unroll
-            for (int j = 0; j < kRUKeys; ++j) k[j] = k[j] == m ? 0u : k[j];
-            if (lane == 0) win[r * kRouteMaxTopk + i] = m;
-        }
+        route_tournament(k, topk, win + r * kRouteMaxTopk, lane);
         if (lane == 0) route_weights(win + r * kRouteMaxTopk, topk, scale_bits, s_sel + r * topk, s_selw + r * topk);
     }
     for (int e = t; e < E; e += nthr) flag[e] = 0;

@@ -383,14 +383,9 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack U
     // this wave's activation pair goes out before the routing
     uint4 xv = make_uint4(0u, 0u, 0u, 0u);
     if (w < kNCW && pr < np) xv = buf_load16(buf_rsrc(X, (uint32_t)nsb * 512u), (uint32_t)pr * 1024u + 16u * (uint32_t)lane);
-    // routing decision (its barriers also publish the zeroed counters)
-    route_workgroup(route.logits, E, topk, route.scale_bits, r_keys, r_win, r_sel, r_selw, wg == 0);
-    if (wg == 0 && tid < topk) {
-        route.sel_pub[tid] = r_sel[tid];
-        route.selw_pub[tid] = r_selw[tid];
-        if (route.sel_api) route.sel_api[tid] = r_sel[tid];
-        if (route.selw_api) route.selw_api[tid] = r_selw[tid];
-    }
+    // routing decision (its barriers also publish the zeroed counters); workgroup 0 forms the
+    // slot weights below, once its copies are in flight
+    route_workgroup(route.logits, E, topk, route.scale_bits, r_keys, r_win, r_sel, r_selw, false);
 
     if (w >= kNCW) {   // ---- copy wave c
         const int c = w - kNCW;
@@ -402,6 +397,15 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack U
             gc.advance(CW, it8, RJ, G);
         });
         return;
+    }
+    if (wg == 0 && w == 0) {   // publish the decision for the down leg and the caller
+        if (lane == 0) route_weights(r_win, topk, route.scale_bits, r_sel, r_selw);
+        if (lane < topk) {
+            route.sel_pub[lane] = r_sel[lane];
+            route.selw_pub[lane] = r_selw[lane];
+            if (route.sel_api) route.sel_api[lane] = r_sel[lane];
+            if (route.selw_api) route.selw_api[lane] = r_selw[lane];
+        }
     }
     if (pr >= np) return;
     // ---- compute wave (gam, p): pair pr of x, operands in registers

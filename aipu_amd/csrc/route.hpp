@@ -100,41 +100,53 @@ __device__ __forceinline__ float router_logit(const float* wsum) {
     return tot;
 }
 
+// Largest value over the wave (DPP: prefix maxima within each row of 16 lanes, then rows 0-1 and
+// 0-3 meet in lanes 31 and 63).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x111, 0xF, 0xF, false));   // row_shr:1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x112, 0xF, 0xF, false));   // row_shr:2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x114, 0xF, 0xF, false));   // row_shr:4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x118, 0xF, 0xF, false));   // row_shr:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));   // row_bcast:15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// The winners of one row by one wave (all 64 lanes): lane l holds keys k[j] of experts
+// l + 64j (0 past E, below every key), and topk rounds each take the largest remaining key, so
+// win[0..topk) comes out in slot order (keys are distinct: one lane and register hold each).
+constexpr int kRouteKeysPerLane = kRouteMaxE / 64;
+__device__ __forceinline__ void route_tournament(uint32_t (&k)[kRouteKeysPerLane], int topk, uint32_t* win, int lane) {
+    for (int i = 0; i < topk; ++i) {
+        uint32_t head = k[0];
+#pragma unroll
+        for (int j = 1; j < kRouteKeysPerLane; ++j) head = max(head, k[j]);
+        const uint32_t m = wave_max_u32(head);
+#pragma unroll
+        for (int j = 0; j < kRouteKeysPerLane; ++j) k[j] = k[j] == m ? 0u : k[j];
+        if (lane == 0) win[i] = m;
+    }
+}
+
 // The routing decision computed by one workgroup (all threads call it; E <= kRouteMaxE and
-// E rounded up to 8 <= the thread count, topk <= kRouteMaxTopk; keys holds >= that many).  An expert's rank is the number of larger
-// keys (all keys are distinct), so the top-k need no sort; with at least 2E threads two
-// threads count one key's rank over half the keys each.  Afterwards win[0..topk) holds the
-// winners' keys in slot order; with `weights`, sel / selw (LDS) are filled too.
+// E rounded up to 8 <= the thread count, topk <= kRouteMaxTopk; keys holds >= that many).
+// Every thread forms one key; wave 0 takes the top-k (route_tournament), so win[0..topk)
+// holds the winners' keys in slot order; with `weights`, lane 0 then fills sel / selw (LDS)
+// too.
 __device__ __forceinline__ void route_workgroup(const uint16_t* logits, int E, int topk, uint32_t scale_bits,
                                                 uint32_t* keys, uint32_t* win, int32_t* sel, uint16_t* selw,
                                                 bool weights) {
-    const int t = threadIdx.x, nthr = blockDim.x;
+    const int t = threadIdx.x;
     if (t < E) keys[t] = route_key(logits[t], t);
-    else if (t < ((E + 7) & ~7)) keys[t] = 0u;
     __syncthreads();
-    const bool two = 2 * E <= nthr;
-    const int k = two ? t >> 1 : t;
-    if (k < E) {
-        const uint32_t my = keys[k];
-        // keys are padded with zeros to a multiple of 8 (zero is below every key), so each
-        // half is a whole number of 16-B reads; the reads are unrolled so that they overlap
-        const int e8 = (E + 7) & ~7;
-        const int half = two ? e8 / 2 : e8;
-        const uint4* kp = (const uint4*)(keys + (two ? (t & 1) * half : 0));
-        int rank = 0;
-#pragma unroll 8
-        for (int j = 0; j < half / 4; ++j) {
-            const uint4 k4 = kp[j];
-            rank += (k4.x > my) + (k4.y > my) + (k4.z > my) + (k4.w > my);
-        }
-        if (two) rank += __shfl_xor(rank, 1, 64);
-        if (rank < topk && (!two || (t & 1) == 0)) win[rank] = my;
+    if (t < 64) {
+        uint32_t k[kRouteKeysPerLane];
+#pragma unroll
+        for (int j = 0; j < kRouteKeysPerLane; ++j) k[j] = t + 64 * j < E ? keys[t + 64 * j] : 0u;
+        route_tournament(k, topk, win, t);
+        if (weights && t == 0) route_weights(win, topk, scale_bits, sel, selw);
     }
     __syncthreads();
-    if (weights) {
-        if (t == 0) route_weights(win, topk, scale_bits, sel, selw);
-        __syncthreads();
-    }
 }
 
 }  // namespace aipu

@@ -13,15 +13,6 @@ namespace aipu {
 
 namespace {
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
-        v = o > v ? o : v;
-    }
-    return v;
-}
-
 constexpr int kMaxE = 4096;
 constexpr int kMaxTopk = 32;
 
