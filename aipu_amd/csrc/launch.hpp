@@ -109,8 +109,8 @@ hipError_t launch_moe_down_mfma(const uint8_t* D, const uint8_t* shD, const int3
 // route.logits in every workgroup.
 bool moe_persist_supported(int64_t E, int topk, int nslots, int64_t H, int64_t I);
 hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
-                                     const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
-                                     const uint16_t* x, uint16_t* h, hipStream_t st);
+                                     const uint8_t* D, const uint8_t* shD, const MoeRoute& route, int topk, int nslots,
+                                     int64_t E, int64_t H, int64_t I, const uint16_t* x, uint16_t* h, hipStream_t st);
 hipError_t launch_moe_down_persist(const uint8_t* D, const uint8_t* shD, const int32_t* sel, const uint16_t* selw,
                                    int topk, int nslots, int64_t E, int64_t H, int64_t I, const uint16_t* h,
                                    uint16_t* y, const uint16_t* resid, hipStream_t st);

@@ -129,8 +129,8 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
     if (fast && !a.ascending && moe_persist_supported(a.E, a.topk, nslots, a.H, a.I)) {
         // persistent legs: one workgroup per CU streams every expert row once (shared expert last)
         const MoeRoute route{nullptr, logits, a.scale_bits, sel, selw, a.sel_idx_out, a.sel_w_out};
-        AIPU_TRY(launch_moe_gateup_persist(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, route, a.topk, nslots, a.E, a.H,
-                                           a.I, a.x, h, st));
+        AIPU_TRY(launch_moe_gateup_persist(a.gate_exps, a.up_exps, a.sh_gate, a.sh_up, a.down_exps, a.sh_down, route,
+                                           a.topk, nslots, a.E, a.H, a.I, a.x, h, st));
         return launch_moe_down_persist(a.down_exps, a.sh_down, sel, selw, a.topk, nslots, a.E, a.H, a.I, h, a.y,
                                        a.resid, st);
     }

@@ -20,7 +20,10 @@
 // and keeps that pair's operands in registers for the whole kernel.  Reduction per row: the
 // 4R pair sums in a fixed order, then h = bf16(silu(bf16(g)) * bf16(u)).  Every workgroup
 // routes from the router logits itself before its first weight copy; workgroup 0 publishes
-// the decision for the down leg and the caller.
+// the decision for the down leg and the caller.  Once a copy wave has issued its own rounds it
+// loads the first kDnPrefetch rounds of the down leg's workgroup wg (slots 0, 1, ... of output
+// rows 8 wg ..) into a scratch kilobyte of LDS and waits for them, so that they sit in the
+// caches when the down leg starts (measured 0.4-0.5 us off the step).
 //
 // Down (k_moe_down_p): job = output rows d0 .. d0+7; round q = slot q (8 rows x 1152 B of
 // expert sel[q] or the shared expert, all I = 2048 weights of the rows); group gamma takes the slots q = gamma
@@ -56,6 +59,7 @@ constexpr int kMaxSlots = kMaxRouted + 1;     // and the shared expert
 constexpr int kMaxRJ = kMaxSlots;             // rounds per job (down: one per slot; gate/up: 2R <= 6)
 constexpr int kRedJob = kMaxSlots * kJR * 4;  // pair sums per job (floats; gate/up uses 16 x 12)
 constexpr int kGuNp = 12;                     // pair-sum stride of a gate/up row (4R <= 12)
+constexpr int kDnPrefetch = 7;                // down-leg rounds per workgroup the gate/up leg prefetches (its first Q)
 
 // Nine loads of round k of 8 rows (row stride rb) at `base` into the LDS slot `dst`.
 template <uint32_t POL>
@@ -358,9 +362,9 @@ __device__ __forceinline__ void x_operands(const uint4& xv, uint8_t* st, int lan
 
 // ------------------------------------------------------------------ gate/up
 template <int R, int NS, int Q, int CW, uint32_t POL>
-__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack Us, MoeRoute route, int E, int topk,
-                                                            const uint16_t* __restrict__ X, uint16_t* __restrict__ Hout,
-                                                            int I, int njobs) {
+__global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack Us, Stack Ds, MoeRoute route, int E,
+                                                            int topk, const uint16_t* __restrict__ X,
+                                                            uint16_t* __restrict__ Hout, int I, int njobs, int64_t Hd) {
     constexpr int RJ = 2 * R, np = 4 * R, nsb = 8 * R;
     extern __shared__ __align__(16) uint8_t s_dyn[];   // ring | staged pairs
     __shared__ float s_red[kMaxJobs * kRedJob];
@@ -369,6 +373,7 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack U
     __shared__ uint32_t r_win[kRouteMaxTopk];
     __shared__ int32_t r_sel[kRouteMaxTopk];
     __shared__ uint16_t r_selw[kRouteMaxTopk];
+    __shared__ __align__(16) uint8_t s_pf[1024];   // target of the down-leg prefetch (never read)
     uint8_t* const s_stage = s_dyn + NS * kSlot;
     const Ring rg{s_dyn, s_cnt, s_read, s_done, s_red};
     const int tid = threadIdx.x, lane = tid & 63;
@@ -396,6 +401,20 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack U
             gu_issue<R, POL>(gc, ev, Gs, Us, topk, s_dyn + (uint32_t)(u % NS) * kSlot, lane);
             gc.advance(CW, it8, RJ, G);
         });
+        // the first rounds of the down leg's workgroup wg (output rows 8 wg .., slots 0, 1, ...)
+        // into the caches while this workgroup's last sets compute
+        const int64_t d0 = (int64_t)wg * kJR;
+        if (d0 < Hd) {
+            const int nvalid = (int)(Hd - d0 < kJR ? Hd - d0 : kJR);
+            const uint32_t off = (uint32_t)(lane & 7) * kRoundRow + 16u * (uint32_t)(lane >> 3);
+            for (int q = c; q < kDnPrefetch && q < (Ds.shared ? topk + 1 : topk); q += CW) {
+                const __amdgpu_buffer_rsrc_t wr = buf_rsrc(Ds.slot(ev, q, topk) + d0 * (int64_t)kRoundRow,
+                                                           (uint32_t)nvalid * kRoundRow);
+#pragma unroll
+                for (int j = 0; j < kLoads; ++j) lds_dma16<0>(wr, s_pf, off + 128u * j);
+            }
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);   // no copy into this workgroup's LDS outlives it
+        }
         return;
     }
     if (wg == 0 && w == 0) {   // publish the decision for the down leg and the caller
@@ -483,13 +502,14 @@ bool moe_persist_supported(int64_t E, int topk, int nslots, int64_t H, int64_t I
 }
 
 hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const uint8_t* shG, const uint8_t* shU,
-                                     const MoeRoute& route, int topk, int nslots, int64_t E, int64_t H, int64_t I,
-                                     const uint16_t* x, uint16_t* h, hipStream_t st) {
+                                     const uint8_t* D, const uint8_t* shD, const MoeRoute& route, int topk, int nslots,
+                                     int64_t E, int64_t H, int64_t I, const uint16_t* x, uint16_t* h, hipStream_t st) {
     if (!moe_persist_supported(E, topk, nslots, H, I) || !route.logits || (nslots > topk && (!shG || !shU)))
         return hipErrorInvalidValue;
     const int R = (int)(H / 2048);
     const int64_t rb = row_bytes(T_Q4_K, H);
     const Stack Gs{G, shG, rb * I}, Us{U, shU, rb * I};
+    const Stack Ds{D, nslots > topk ? shD : nullptr, row_bytes(T_Q4_K, I) * H};
     const int njobs = (int)(nslots * (I / kJR));
     const int cus = device_cu_count();
     const int tpw = (njobs + cus - 1) / cus;
@@ -497,8 +517,8 @@ hipError_t launch_moe_gateup_persist(const uint8_t* G, const uint8_t* U, const u
     const dim3 grid(G2), block(64 * (kNCW + kGuCW));
 #define AIPU_GU(RV)                                                                                              \
     if (R == RV) {                                                                                               \
-        hipLaunchKernelGGL((k_moe_gu_p<RV, kGuNS, kGuQ, kGuCW, kNT>), grid, block, gu_lds(RV), st, Gs, Us, route, \
-                           (int)E, topk, x, h, (int)I, njobs);                                                   \
+        hipLaunchKernelGGL((k_moe_gu_p<RV, kGuNS, kGuQ, kGuCW, kNT>), grid, block, gu_lds(RV), st, Gs, Us, Ds, route, \
+                           (int)E, topk, x, h, (int)I, njobs, H);                                                \
         return hipGetLastError();                                                                                \
     }
     AIPU_GU(1) AIPU_GU(2) AIPU_GU(3)
