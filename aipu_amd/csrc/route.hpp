@@ -15,7 +15,7 @@
 
 namespace aipu {
 
-constexpr int kRouteMaxE = 512;    // in-kernel routing (one key per thread, rank by counting)
+constexpr int kRouteMaxE = 512;    // in-kernel routing (one key per thread, eight per lane of the top-k wave)
 constexpr int kRouteMaxTopk = 32;
 
 __device__ __forceinline__ uint32_t bf16_order_key(uint32_t b) {

@@ -58,8 +58,9 @@ __global__ __launch_bounds__(64) void k_router_tail(const uint16_t* __restrict__
     router_tail_wave(logits, E, topk, scale_bits, sel, selw, sel2, selw2, gates, keys, win);
 }
 
-// One routing decision per activation row (row = workgroup), E <= kRouteMaxE: every key's
-// rank counted in parallel (route.hpp), the same decision as the one-wave tail.
+// One routing decision per activation row (row = workgroup), E <= kRouteMaxE: every thread
+// forms one key and one wave takes the top-k (route.hpp), the same decision as the one-wave
+// tail.
 constexpr int kRankThreads = 2 * kRouteMaxE;
 
 __global__ __launch_bounds__(kRankThreads) void k_router_rank_rows(const uint16_t* __restrict__ logits, int E,
