@@ -376,15 +376,19 @@ __device__ __forceinline__ void half_block(const uint8_t* sa, const uint8_t* sb,
     }
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
+        // all kMS operand reads of the step go out before the B build and the MFMAs, so their
+        // LDS latency overlaps that work instead of stalling every other MFMA pair
+        h8_t A[kMS];
+#pragma unroll
+        for (int i = 0; i < kMS; ++i) A[i] = __builtin_bit_cast(h8_t, lds_u4(sa + ((tt * kMT + i0 + i) * 64 + lane) * 16));
         h8_t B[kNS];
 #pragma unroll
         for (int j = 0; j < kNS; ++j) B[j] = b_operand(dword_of(q[j], tt), ck[j], cm);
 #pragma unroll
         for (int i = 0; i < kMS; ++i) {
-            const h8_t A = __builtin_bit_cast(h8_t, lds_u4(sa + ((tt * kMT + i0 + i) * 64 + lane) * 16));
 #pragma unroll
             for (int j = 0; j < kNS; ++j)
-                D1[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], (half == 0 && tt == 0) ? zero : D1[i][j],
+                D1[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], (half == 0 && tt == 0) ? zero : D1[i][j],
                                                                   0, 0, 0);
         }
     }
