@@ -589,7 +589,7 @@ __global__ __launch_bounds__(kMaxW * 64) void k_gemv1(Prob pb0, const uint16_t* 
 // loads on every lane, so the compiler tracks every wait).
 
 template <int MR, int BPK, class Prob>
-__global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* __restrict__ X0, int K, int KP) {
+__global__ __launch_bounds__(kMaxW * 64) void k_gemvm(Prob pb, const uint16_t* __restrict__ X0, int K) {
     constexpr int MRQ = MR < 4 ? MR : 4;   // rows per MFMA set
     constexpr int NH = MR / MRQ;           // MFMA sets (1, or 2 for MR = 8)
     constexpr int kGrp = 144;                       // bytes per (b, g, m) group of 8 entries
@@ -746,7 +746,7 @@ constexpr int kSmallMaxRows = 4;
 
 template <int GS, int NW, int MR, class Prob>   // MR = 2: rows 0, 1 only; MR = 4: up to four rows
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemvs(
-    Prob pb, const uint16_t* __restrict__ X0, int K, int KP) {
+    Prob pb, const uint16_t* __restrict__ X0, int K) {
     constexpr int XP = GS * 32;              // 16-B pieces per activation row and wave
     constexpr int XI = (2 * XP + 63) / 64;   // pieces per lane for a pair of rows
     constexpr uint32_t kPair = GS * 1024u;   // operand entries of a pair of rows
@@ -933,7 +933,7 @@ hipError_t run_gemvm(const Prob& pb, int nsb, unsigned nwg, const uint16_t* x, i
         const int bpk = nsb / kp;
         const dim3 grid(nwg), block(64 * kp);
 #define AIPU_LM(B)                                                                       \
-    case B: hipLaunchKernelGGL((k_gemvm<MR, B, Prob>), grid, block, 0, st, pb, x, K, kp); return hipGetLastError();
+    case B: hipLaunchKernelGGL((k_gemvm<MR, B, Prob>), grid, block, 0, st, pb, x, K); return hipGetLastError();
         switch (bpk) {
             AIPU_LM(1)
             AIPU_LM(2)
@@ -1078,9 +1078,9 @@ hipError_t runs_mr(const Prob& pb, const PlanS& pl, unsigned nwg, const uint16_t
     const dim3 grid(nwg), block(64 * pl.KP);
     const size_t lds = (size_t)pl.lds;
     switch (pl.GS) {
-        case 1: hipLaunchKernelGGL((k_gemvs<1, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K, pl.KP); break;
-        case 2: hipLaunchKernelGGL((k_gemvs<2, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K, pl.KP); break;
-        default: hipLaunchKernelGGL((k_gemvs<3, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K, pl.KP); break;
+        case 1: hipLaunchKernelGGL((k_gemvs<1, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K); break;
+        case 2: hipLaunchKernelGGL((k_gemvs<2, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K); break;
+        default: hipLaunchKernelGGL((k_gemvs<3, kMaxW, MR, Prob>), grid, block, lds, st, pb, X, K); break;
     }
     return hipGetLastError();
 }

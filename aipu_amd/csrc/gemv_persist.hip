@@ -191,7 +191,7 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
                 : "=&v"(hv), "=&v"(q0), "=&v"(q1), "=&v"(cv)
                 : "v"(wrow), "v"(wrow + 16u + 32u * (uint32_t)g), "v"(lds_addr(&s_cnt[u]))
                 : "memory");
-            if (seen < u && __builtin_amdgcn_readfirstlane(cv) < 1u) {
+            if (seen < u && (uint32_t)__builtin_amdgcn_readfirstlane(cv) < 1u) {
                 spin_ge(&s_cnt[u], 1u);
                 asm volatile(
                     "ds_read_b128 %0, %3\n\t"

@@ -155,7 +155,7 @@ __global__ __launch_bounds__(64 * (4 * 3 + 1)) void k_gemvmp(const uint8_t* __re
             : "=&v"(hv), "=&v"(q0), "=&v"(q1), "=&v"(cv)
             : "v"(ah), "v"(aq), "v"(lds_addr(&s_cnt[u]))
             : "memory");
-        if (seen < u && __builtin_amdgcn_readfirstlane(cv) < 1u) {
+        if (seen < u && (uint32_t)__builtin_amdgcn_readfirstlane(cv) < 1u) {
             spin_ge(&s_cnt[u], 1u);
             asm volatile(
                 "ds_read_b128 %0, %3\n\t"
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(64 * (4 * 3 + 1)) void k_gemvmd(const uint8_t* __re
             : "=&v"(hv), "=&v"(q0), "=&v"(q1), "=&v"(q2), "=&v"(q3), "=&v"(cv)
             : "v"(ah), "v"(lds_addr(&s_cnt[u])), "v"(aq)
             : "memory");
-        if (seen < u && __builtin_amdgcn_readfirstlane(cv) < 1u) {
+        if (seen < u && (uint32_t)__builtin_amdgcn_readfirstlane(cv) < 1u) {
             spin_ge(&s_cnt[u], 1u);
             asm volatile(
                 "ds_read_b128 %0, %5\n\t"

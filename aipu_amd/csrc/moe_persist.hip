@@ -90,11 +90,11 @@ __device__ __forceinline__ void set_weights(uint32_t sl, uint32_t cnt, int pp, i
         : "=&v"(hv), "=&v"(q0), "=&v"(q1), "=&v"(cv)
         : "v"(ah), "v"(aq), "v"(cnt)
         : "memory");
-    if (!known && __builtin_amdgcn_readfirstlane(cv) < 1u) {
+    if (!known && (uint32_t)__builtin_amdgcn_readfirstlane(cv) < 1u) {
         for (uint32_t it = 0;; ++it) {
             uint32_t c;
             asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(c) : "v"(cnt) : "memory");
-            if (__builtin_amdgcn_readfirstlane(c) >= 1u) break;
+            if ((uint32_t)__builtin_amdgcn_readfirstlane(c) >= 1u) break;
             if (it == (1u << 22)) {   // give up (recorded), as spin_ge does
                 wait_gave_up();
                 break;
