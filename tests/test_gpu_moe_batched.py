@@ -106,6 +106,20 @@ def test_batched_fast_small(M, router_type, shared, topk):
     _check_fast(y, sel, sw, X, router_type, rw, ex, sh, E, H, I, topk)
 
 
+@pytest.mark.parametrize("shared", [True, False])
+def test_batched_fast_more_experts_than_one_workgroup_routes(shared):
+    """E = 600 > 512: a pass routes its rows with the one-wave tail kernel and forms the union
+    in a separate launch (the one-workgroup routing-and-union kernel takes E <= 512)."""
+    E, H, I, topk, M = 600, 256, 256, 4, 3
+    note(f"moe batched fast E={E} shared={shared}")
+    rng = np.random.default_rng(600 + shared)
+    rw, ex, sh = _case(rng, E, H, I, BF16)
+    sh = sh if shared else None
+    X = qo.random_bf16(rng, (M, H), scale=0.05)
+    y, sel, sw = _run(BF16, rw, ex, sh, E, H, I, topk, X, "fast")
+    _check_fast(y, sel, sw, X, BF16, rw, ex, sh, E, H, I, topk)
+
+
 @pytest.mark.parametrize("M", [2, 4])
 def test_batched_fast_c2_shape(M):
     """Config-2 expert shape (6144 <-> 2048, top-8) over 32 experts, shared expert; two rows
