@@ -96,8 +96,8 @@ __global__ __launch_bounds__(64) void k_union(const int32_t* __restrict__ sel, c
 }
 
 // The routing of every row of a pass and their union in one workgroup, for E <= kRouteMaxE:
-// wave r routes row r (route.hpp's decision, route_tournament on keys it forms itself), its
-// lane 0 forms the slot weights; then the union of k_union over the decisions held in
+// wave r routes row r (route.hpp's decision on keys it forms itself, the winners and slot
+// weights one per lane); then the union of k_union over the decisions held in
 // LDS.  One launch instead of two.
 constexpr int kRUThreads = 64 * kRowsPerPass;
 __global__ __launch_bounds__(kRUThreads) void k_route_union(const uint16_t* __restrict__ logits, int M, int E,
@@ -105,7 +105,6 @@ __global__ __launch_bounds__(kRUThreads) void k_route_union(const uint16_t* __re
                                                             uint16_t* __restrict__ selw, int32_t* sel2, uint16_t* selw2,
                                                             int shared, int ms, int32_t* __restrict__ uidx,
                                                             int32_t* __restrict__ nslots, uint32_t* __restrict__ ugate) {
-    __shared__ uint32_t win[kRowsPerPass * kRouteMaxTopk];
     __shared__ int32_t s_sel[kRowsPerPass * kRouteMaxTopk];
     __shared__ uint16_t s_selw[kRowsPerPass * kRouteMaxTopk];
     __shared__ uint8_t flag[kRouteMaxE];
@@ -113,25 +112,35 @@ __global__ __launch_bounds__(kRUThreads) void k_route_union(const uint16_t* __re
     __shared__ int s_count;
     const int t = threadIdx.x, nthr = blockDim.x, lane = t & 63;
     const int r = __builtin_amdgcn_readfirstlane(t >> 6);
+    uint32_t lb[kRouteKeysPerLane];   // this wave's row of logits, loaded before the barrier
+#pragma unroll
+    for (int j = 0; j < kRouteKeysPerLane; ++j) {
+        const int e = lane + 64 * j;
+        lb[j] = r < M && e < E ? logits[(int64_t)r * E + e] : 0u;
+    }
+    for (int e = t; e < E; e += nthr) flag[e] = 0;
+    __syncthreads();
     if (r < M) {
         uint32_t k[kRouteKeysPerLane];
 #pragma unroll
         for (int j = 0; j < kRouteKeysPerLane; ++j) {
             const int e = lane + 64 * j;
-            k[j] = e < E ? route_key(logits[(int64_t)r * E + e], e) : 0u;   // 0 is below every key
+            k[j] = e < E ? route_key(lb[j], e) : 0u;   // 0 is below every key
         }
-        route_tournament(k, topk, win + r * kRouteMaxTopk, lane);
-        if (lane == 0) route_weights(win + r * kRouteMaxTopk, topk, scale_bits, s_sel + r * topk, s_selw + r * topk);
-    }
-    for (int e = t; e < E; e += nthr) flag[e] = 0;
-    __syncthreads();
-    for (int i = t; i < M * topk; i += nthr) {
-        const int e = s_sel[i];
-        sel[i] = e;
-        selw[i] = s_selw[i];
-        if (sel2) sel2[i] = e;
-        if (selw2) selw2[i] = s_selw[i];
-        if (e >= 0 && e < E) flag[e] = 1;
+        const uint32_t wl = route_tournament_lanes(k, topk, lane);
+        int32_t sl;
+        uint16_t swl;
+        route_weights_wave(wl, topk, scale_bits, lane, sl, swl);
+        if (lane < topk) {
+            const int i = r * topk + lane;
+            s_sel[i] = sl;
+            s_selw[i] = swl;
+            sel[i] = sl;
+            selw[i] = swl;
+            if (sel2) sel2[i] = sl;
+            if (selw2) selw2[i] = swl;
+            if (sl >= 0 && sl < E) flag[sl] = 1;
+        }
     }
     __syncthreads();
     if (t < 64) {   // one wave lists the flagged experts in ascending index

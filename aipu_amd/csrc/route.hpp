@@ -128,6 +128,44 @@ __device__ __forceinline__ void route_tournament(uint32_t (&k)[kRouteKeysPerLane
     }
 }
 
+// route_tournament with the winners left one per lane: lane i < topk returns win[i].
+__device__ __forceinline__ uint32_t route_tournament_lanes(uint32_t (&k)[kRouteKeysPerLane], int topk, int lane) {
+    uint32_t mine = 0;
+    for (int i = 0; i < topk; ++i) {
+        uint32_t head = k[0];
+#pragma unroll
+        for (int j = 1; j < kRouteKeysPerLane; ++j) head = max(head, k[j]);
+        const uint32_t m = wave_max_u32(head);
+#pragma unroll
+        for (int j = 0; j < kRouteKeysPerLane; ++j) k[j] = k[j] == m ? 0u : k[j];
+        mine = lane == i ? m : mine;
+    }
+    return mine;
+}
+
+// route_weights with lane i < topk holding win[i]: the balanced +0-padded add tree over the
+// gates runs as DPP row shifts (level l adds lane x - 2^(l-1) into lane x; lane 2^l (j + 1) - 1
+// then holds node j of level l, since fp32 addition is commutative the bits are the serial
+// tree's), rs = rsqrt(s)^2 * scale from lane npow - 1, and every lane forms its own slot.
+__device__ __forceinline__ void route_weights_wave(uint32_t win_lane, int topk, uint32_t scale_bits, int lane,
+                                                   int32_t& sel, uint16_t& selw) {
+    const float g = bf16_to_f32(key_to_bf16(win_lane >> 16));
+    float v = lane < topk ? g : 0.0f;
+    int npow = 2;
+    while (npow < topk) npow <<= 1;
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, false));   // row_shr:1
+    if (npow >= 4) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xF, 0xF, false));
+    if (npow >= 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xF, 0xF, false));
+    if (npow >= 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xF, 0xF, false));
+    if (npow >= 32) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), npow - 1));
+    const float rr = glm_rsqrt(s);
+    const float rr2 = rr * rr;
+    const float rs = rr2 * __uint_as_float(scale_bits);
+    sel = (int32_t)(0xFFFFu - (win_lane & 0xFFFFu));
+    selw = (uint16_t)bf16_rne(g * rs);
+}
+
 // The routing decision computed by one workgroup (all threads call it; E <= kRouteMaxE and
 // E rounded up to 8 <= the thread count, topk <= kRouteMaxTopk; keys holds >= that many).
 // Every thread forms one key; wave 0 takes the top-k (route_tournament), so win[0..topk)
