@@ -371,8 +371,6 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack U
     __shared__ uint32_t s_cnt[kMaxJobs * kMaxRJ], s_read[kMaxJobs * kMaxRJ], s_done[kMaxJobs];
     __shared__ __align__(16) uint32_t r_keys[kRouteMaxE];
     __shared__ uint32_t r_win[kRouteMaxTopk];
-    __shared__ int32_t r_sel[kRouteMaxTopk];
-    __shared__ uint16_t r_selw[kRouteMaxTopk];
     __shared__ __align__(16) uint8_t s_pf[1024];   // target of the down-leg prefetch (never read)
     uint8_t* const s_stage = s_dyn + NS * kSlot;
     const Ring rg{s_dyn, s_cnt, s_read, s_done, s_red};
@@ -390,7 +388,7 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack U
     if (w < kNCW && pr < np) xv = buf_load16(buf_rsrc(X, (uint32_t)nsb * 512u), (uint32_t)pr * 1024u + 16u * (uint32_t)lane);
     // routing decision (its barriers also publish the zeroed counters); workgroup 0 forms the
     // slot weights below, once its copies are in flight
-    route_workgroup(route.logits, E, topk, route.scale_bits, r_keys, r_win, r_sel, r_selw, false);
+    route_workgroup(route.logits, E, topk, route.scale_bits, r_keys, r_win, nullptr, nullptr, false);
 
     if (w >= kNCW) {   // ---- copy wave c
         const int c = w - kNCW;
@@ -418,12 +416,14 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack U
         return;
     }
     if (wg == 0 && w == 0) {   // publish the decision for the down leg and the caller
-        if (lane == 0) route_weights(r_win, topk, route.scale_bits, r_sel, r_selw);
+        int32_t sl;
+        uint16_t swl;
+        route_weights_wave(lane < topk ? r_win[lane] : 0u, topk, route.scale_bits, lane, sl, swl);
         if (lane < topk) {
-            route.sel_pub[lane] = r_sel[lane];
-            route.selw_pub[lane] = r_selw[lane];
-            if (route.sel_api) route.sel_api[lane] = r_sel[lane];
-            if (route.selw_api) route.selw_api[lane] = r_selw[lane];
+            route.sel_pub[lane] = sl;
+            route.selw_pub[lane] = swl;
+            if (route.sel_api) route.sel_api[lane] = sl;
+            if (route.selw_api) route.selw_api[lane] = swl;
         }
     }
     if (pr >= np) return;

@@ -168,9 +168,9 @@ __device__ __forceinline__ void route_weights_wave(uint32_t win_lane, int topk, 
 
 // The routing decision computed by one workgroup (all threads call it; E <= kRouteMaxE and
 // E rounded up to 8 <= the thread count, topk <= kRouteMaxTopk; keys holds >= that many).
-// Every thread forms one key; wave 0 takes the top-k (route_tournament), so win[0..topk)
-// holds the winners' keys in slot order; with `weights`, lane 0 then fills sel / selw (LDS)
-// too.
+// Every thread forms one key; wave 0 takes the top-k (route_tournament_lanes), so
+// win[0..topk) holds the winners' keys in slot order; with `weights`, the wave also fills
+// sel / selw (LDS, route_weights_wave).
 __device__ __forceinline__ void route_workgroup(const uint16_t* logits, int E, int topk, uint32_t scale_bits,
                                                 uint32_t* keys, uint32_t* win, int32_t* sel, uint16_t* selw,
                                                 bool weights) {
@@ -181,8 +181,17 @@ __device__ __forceinline__ void route_workgroup(const uint16_t* logits, int E, i
         uint32_t k[kRouteKeysPerLane];
 #pragma unroll
         for (int j = 0; j < kRouteKeysPerLane; ++j) k[j] = t + 64 * j < E ? keys[t + 64 * j] : 0u;
-        route_tournament(k, topk, win, t);
-        if (weights && t == 0) route_weights(win, topk, scale_bits, sel, selw);
+        const uint32_t wl = route_tournament_lanes(k, topk, t);
+        if (t < topk) win[t] = wl;
+        if (weights) {
+            int32_t sl;
+            uint16_t swl;
+            route_weights_wave(wl, topk, scale_bits, t, sl, swl);
+            if (t < topk) {
+                sel[t] = sl;
+                selw[t] = swl;
+            }
+        }
     }
     __syncthreads();
 }
