@@ -170,3 +170,37 @@ def test_batched_fast_rows_independent_of_batch(H, I, topk):
             assert np.array_equal(sel[i], sel8[r]), f"row {r} routing in batch {rows}"
             assert_bits_equal(sw[i], sw8[r], f"row {r} sel_w in batch {rows}")
             assert_bits_equal(y[i], y8[r], f"row {r} y in batch {rows}")
+
+
+@pytest.mark.parametrize("H,topk,shared", [(2048, 4, False), (4096, 8, True), (6144, 3, False), (6144, 8, False)])
+def test_batched_fast_two_row_pass_equals_one_row_pass(H, topk, shared):
+    """At I = 2048 and H = 2048 R, with and without the shared expert and at topk 3 / 4 / 8: a
+    row of a two-row pass (both rows on every union expert) and the same row as the odd row of a
+    three-row batch (a one-row pass over its own experts) agree bit for bit in output, routing
+    and weights, and the two-row batch passes the fast-mode gate."""
+    E, I = 32, 2048
+    note(f"moe batched fast two-row pass H={H} topk={topk} shared={shared}")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(H + 10 * topk + shared)
+    exd = tuple(random_weights_gpu(Q4K, E * I, H, gen) if k < 2 else random_weights_gpu(Q4K, E * H, I, gen)
+                for k in range(3))
+    shd = ((random_weights_gpu(Q4K, I, H, gen), random_weights_gpu(Q4K, I, H, gen), random_weights_gpu(Q4K, H, I, gen))
+           if shared else None)
+    rng = np.random.default_rng(H + topk)
+    rw = qo.random_bf16(rng, (E, H), scale=0.05).view(np.uint8).reshape(-1)
+    X = qo.random_bf16(rng, (4, H), scale=0.05)
+
+    def run(rows):
+        y, sel, sw = dev.moe_swiglu_decode_batched(BF16, d_u8(rw), Q4K, *exd, E, H, I, topk, d_bf16(X[rows]),
+                                                   mode="fast", shared=shd)
+        return h_bits(y), sel.cpu().numpy(), h_bits(sw)
+
+    y2, sel2, sw2 = run([0, 1])
+    for r in (0, 1):
+        y3, sel3, sw3 = run([2, 3, r])   # row r alone in the second pass
+        assert np.array_equal(sel3[2], sel2[r]), f"row {r} routing"
+        assert_bits_equal(sw3[2], sw2[r], f"row {r} sel_w")
+        assert_bits_equal(y3[2], y2[r], f"row {r} y")
+    ex = tuple(t.cpu().numpy() for t in exd)
+    sh = tuple(t.cpu().numpy() for t in shd) if shared else None
+    _check_fast(y2, sel2, sw2, X[:2], BF16, rw, ex, sh, E, H, I, topk)
