@@ -24,6 +24,7 @@
 #include "common.hpp"
 #include "launch.hpp"
 #include "mfma_gemv.hpp"
+#include "norm.hpp"
 #include "persist.hpp"
 
 namespace aipu {
@@ -40,14 +41,26 @@ constexpr int kPMaxNsb = 32;      // K <= 8192
 constexpr int kPMaxPairs = kPMaxNsb / 2;
 constexpr int kPStage = kStgBytes; // per pair: operand entries + 16 sub-block sums
 
+// The FFN half's pre-FFN RMSNorm applied inside the router launch (NORM = true): compute wave
+// w's pair p (elements 512p .. 512p + 511) is exactly wave p of the separate fast RMSNorm, so
+// each wave forms that wave's sum of squares, the waves meet through LDS, and every wave
+// takes the total in norm.hpp's order and scales its own pair before staging it.  Workgroup 0
+// writes the normalised vector to `out` for the expert legs.  The bits equal the separate
+// RMSNorm's, and the logits those of this kernel on its output.
+struct NormIn {
+    const uint16_t* gamma;
+    uint32_t inv_len_bits;
+    uint16_t* out;
+};
+
 // R rounds per tile (ceil(row bytes / 1 KB)), TT tiles per workgroup, XPW pairs per compute
 // wave.  nsb = K / 256 is a runtime value with ceil(144 * nsb / 1024) == R.  COPY_ONLY = true
 // is a measurement variant (aipu_measure_gemv): the copy wave runs the same copy schedule and
 // the compute waves leave after the first barrier, so nothing is computed or written.
-template <int R, int TT, int XPW, bool COPY_ONLY = false>
+template <int R, int TT, int XPW, bool COPY_ONLY = false, bool NORM = false>
 __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __restrict__ W, int64_t N, int nsb,
                                                              const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
-                                                             float* __restrict__ Yf, int ntiles) {
+                                                             float* __restrict__ Yf, int ntiles, NormIn nm) {
     constexpr int NB = TT < 3 ? TT : 3;                        // tile buffers
     // rounds in flight: up to 4; with buffer reuse (TT > NB) at most (NB - 1) R + 1 (see the
     // reuse wait), without it at most the TT R rounds there are
@@ -60,6 +73,8 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     __shared__ uint32_t s_cnt[TT * R];                          // rounds landed
     __shared__ uint32_t s_done[TT];                             // pairs finished per tile
     __shared__ uint32_t s_freed[TT];                            // tile reduced, buffers free
+    __shared__ float s_part[kNormWaves];                        // NORM: the waves' sums of squares
+    __shared__ uint32_t s_normc;                                // NORM: sums posted
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int NCW = (int)(blockDim.x >> 6) - 1;
@@ -74,15 +89,18 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
         s_done[tid] = 0u;
         s_freed[tid] = 0u;
     }
+    if (NORM && tid == 0) s_normc = 0u;
 
     // activation loads of the wave's own pairs go out before any weight copy
-    uint4 xv[XPW];
+    uint4 xv[XPW], gv[XPW];
     if (w < NCW) {
         const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)nsb * 512u);   // an odd nsb's last pair reads zeros
+        const __amdgpu_buffer_rsrc_t gr = buf_rsrc(nm.gamma, NORM ? (uint32_t)nsb * 512u : 0u);
 #pragma unroll
         for (int i = 0; i < XPW; ++i) {
             const int p = w + NCW * i;
             xv[i] = buf_load16(xr, p < np ? (uint32_t)p * 1024u + 16u * (uint32_t)lane : kOOB);
+            if constexpr (NORM) gv[i] = buf_load16(gr, p < np ? (uint32_t)p * 1024u + 16u * (uint32_t)lane : kOOB);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -130,6 +148,28 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     }
 
     // ---- compute waves: stage the own pairs, keep their operands in registers
+    if constexpr (NORM) {
+        // pair p is wave p of the RMSNorm's reduction; pairs past the data (and waves past the
+        // pairs) count as zero, as the RMSNorm's idle waves do
+#pragma unroll
+        for (int i = 0; i < XPW; ++i) {
+            const int p = w + NCW * i;
+            const float s = norm_wave_sum(norm_sq8(xv[i]));
+            if (p < np && lane == 0) s_part[p] = s;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the sums written before the post
+        lds_post(&s_normc);
+        spin_ge(&s_normc, (uint32_t)NCW);
+        const float tot = norm_final_sum(lane < np ? s_part[lane] : 0.0f);
+        const float inv = norm_inv(__shfl(tot, 0, 64), nm.inv_len_bits);
+#pragma unroll
+        for (int i = 0; i < XPW; ++i) {
+            const int p = w + NCW * i;
+            xv[i] = norm_apply8(xv[i], gv[i], inv);
+            const uint32_t e = (uint32_t)p * 512u + 8u * (uint32_t)lane;   // first element of the lane's 8
+            if (wg == 0 && p < np && e < (uint32_t)nsb * 256u) *(uint4*)(nm.out + e) = xv[i];
+        }
+    }
     const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
     u32x4_t A[XPW][8];
     float2 as[XPW];
@@ -266,13 +306,22 @@ int cu_count() {
     return n;
 }
 
-template <int R, int XPW, bool COPY_ONLY = false>
+template <int R, int XPW, bool COPY_ONLY = false, bool NORM = false>
 hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16_t* y, float* yf, int TT, int G,
-                 int ntiles, int ncw, size_t lds, hipStream_t st) {
+                 int ntiles, int ncw, size_t lds, hipStream_t st, NormIn nm = NormIn{nullptr, 0u, nullptr}) {
     const dim3 grid(G), block(64 * (ncw + 1));
+    if constexpr (NORM) {   // the FFN half's router: at most two tiles per workgroup
+        if (TT == 1)
+            hipLaunchKernelGGL((k_gemv1p<R, 1, XPW, false, true>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm);
+        else if (TT == 2)
+            hipLaunchKernelGGL((k_gemv1p<R, 2, XPW, false, true>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm);
+        else
+            return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     switch (TT) {
 #define AIPU_P(TV) \
-    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, XPW, COPY_ONLY>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles); break;
+    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, XPW, COPY_ONLY>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm); break;
         AIPU_P(1)
         AIPU_P(2)
         AIPU_P(3)
@@ -287,6 +336,28 @@ hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16
     return hipGetLastError();
 }
 
+// Launch plan of a one-row GEMV of N rows over K (K <= 8192).
+struct PPlan {
+    int nsb, ntiles, TT, G, R, np, xpw, ncw, nb;
+    size_t lds;
+};
+PPlan p_plan(int64_t N, int64_t K) {
+    PPlan q;
+    q.nsb = (int)(K / QK_K);
+    q.ntiles = (int)((N + kPR - 1) / kPR);
+    const int cus = cu_count();
+    q.TT = (q.ntiles + cus - 1) / cus;
+    q.TT = q.TT > kPMaxTT ? kPMaxTT : q.TT;
+    q.G = (q.ntiles + q.TT - 1) / q.TT;
+    q.R = (144 * q.nsb + 1023) / 1024;
+    q.np = (q.nsb + 1) / 2;
+    q.xpw = q.np > kPMaxCW ? 2 : 1;
+    q.ncw = (q.np + q.xpw - 1) / q.xpw;
+    q.nb = q.TT < 3 ? q.TT : 3;
+    q.lds = (size_t)q.nb * kPR * tile_pitch((uint32_t)q.nsb * 144u);
+    return q;
+}
+
 }  // namespace
 
 bool gemv_persist_supported(int64_t N, int64_t K) {
@@ -298,18 +369,9 @@ bool gemv_persist_supported(int64_t N, int64_t K) {
 hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
                                hipStream_t st, int variant) {
     if (!gemv_persist_supported(N, K)) return hipErrorInvalidValue;
-    const int nsb = (int)(K / QK_K);
-    const int ntiles = (int)((N + kPR - 1) / kPR);
-    const int cus = cu_count();
-    int TT = (ntiles + cus - 1) / cus;
-    TT = TT > kPMaxTT ? kPMaxTT : TT;
-    const int G = (ntiles + TT - 1) / TT;
-    const int R = (144 * nsb + 1023) / 1024;
-    const int np = (nsb + 1) / 2;
-    const int xpw = np > kPMaxCW ? 2 : 1;
-    const int ncw = (np + xpw - 1) / xpw;
-    const int nb = TT < 3 ? TT : 3;
-    const size_t lds = (size_t)nb * kPR * tile_pitch((uint32_t)nsb * 144u);
+    const PPlan q = p_plan(N, K);
+    const int nsb = q.nsb, ntiles = q.ntiles, TT = q.TT, G = q.G, R = q.R, xpw = q.xpw, ncw = q.ncw, nb = q.nb;
+    const size_t lds = q.lds;
     if (variant == 2) {
         // the same dynamic LDS plus the kernel's static arrays
         const size_t stat = (size_t)kPMaxPairs * kPStage + (size_t)nb * kPR * kPMaxPairs * 4 + (size_t)TT * (R + 2) * 4;
@@ -334,6 +396,27 @@ hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uin
         case 4 * 4 + 1: return run_p<4, 1>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
         case 4 * 4 + 2: return run_p<4, 2>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
         case 5 * 4 + 2: return run_p<5, 2>(W, N, nsb, x, y, yf, TT, G, ntiles, ncw, lds, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool gemv_persist_norm_supported(int64_t N, int64_t K) {
+    return gemv_persist_supported(N, K) && p_plan(N, K).TT <= 2;
+}
+
+hipError_t launch_gemv_persist_norm(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, const uint16_t* gamma,
+                                    uint32_t inv_len_bits, uint16_t* x_norm, uint16_t* y, hipStream_t st) {
+    if (!gemv_persist_norm_supported(N, K)) return hipErrorInvalidValue;
+    const PPlan q = p_plan(N, K);
+    const NormIn nm{gamma, inv_len_bits, x_norm};
+    const int nsb = q.nsb, ntiles = q.ntiles, TT = q.TT, G = q.G, ncw = q.ncw;
+    switch (q.R * 4 + q.xpw) {
+        case 1 * 4 + 1: return run_p<1, 1, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
+        case 2 * 4 + 1: return run_p<2, 1, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
+        case 3 * 4 + 1: return run_p<3, 1, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
+        case 4 * 4 + 1: return run_p<4, 1, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
+        case 4 * 4 + 2: return run_p<4, 2, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
+        case 5 * 4 + 2: return run_p<5, 2, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
         default: return hipErrorInvalidValue;
     }
 }

@@ -58,6 +58,12 @@ hipError_t launch_gemv_mixed(const aipu_tile_desc* tiles, int n_tiles, int64_t K
 bool gemv_persist_supported(int64_t N, int64_t K);
 hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
                                hipStream_t st, int variant = 0);
+// The same with the fast RMSNorm of x in front (norm.hpp's order): y = (rmsnorm(x, gamma)) . W^T,
+// and x_norm receives the normalised x (bit-identical to launch_rmsnorm's fast mode followed by
+// the GEMV).  x, gamma and x_norm 16-B aligned; at most two 8-row tiles per CU.
+bool gemv_persist_norm_supported(int64_t N, int64_t K);
+hipError_t launch_gemv_persist_norm(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, const uint16_t* gamma,
+                                    uint32_t inv_len_bits, uint16_t* x_norm, uint16_t* y, hipStream_t st);
 
 // gemv_persist_m.hip -- persistent Q4_K GEMV for 2 .. 8 activation rows (tolerance mode,
 // K = 2048, 4096, 6144, at most three 8-row tiles per CU).  dense = false: row m is
@@ -160,6 +166,7 @@ struct MoeArgs {
     void* ws;
     const uint16_t* resid = nullptr;   // when set, y = bf16(resid + bf16(combine)) (block residual)
     bool ascending = false;            // combine the routed experts in ascending expert index
+    bool logits_ready = false;         // fast mode: the router logits are already in the workspace
 };
 int64_t moe_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
 hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st);

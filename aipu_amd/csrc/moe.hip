@@ -117,7 +117,9 @@ hipError_t launch_moe_decode(const MoeArgs& a, hipStream_t st) {
     const bool fast = a.mode == AIPU_MODE_FAST && a.type == T_Q4_K;
 
     // 1. router logits
-    if (a.mode == AIPU_MODE_FAST && a.router_type == T_BF16)
+    if (a.logits_ready && a.mode == AIPU_MODE_FAST)
+        ;   // formed by the caller's launch (the FFN half's router with its RMSNorm)
+    else if (a.mode == AIPU_MODE_FAST && a.router_type == T_BF16)
         AIPU_TRY(launch_router_bf16_logits((const uint16_t*)a.router_w, a.x, a.H, (int)a.E, logits, st));
     else if (a.mode == AIPU_MODE_FAST && a.router_type == T_Q4_K)
         AIPU_TRY(launch_gemv_fast(a.router_type, a.router_w, a.E, a.H, a.x, 1, logits, nullptr, st));
@@ -222,10 +224,21 @@ int64_t moe_layer_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk) {
 
 hipError_t launch_moe_layer_decode(const MoeArgs& a, const uint16_t* gamma, hipStream_t st) {
     uint16_t* nrm = (uint16_t*)((uint8_t*)a.ws + moe_workspace_bytes(a.E, a.H, a.I, a.topk));
-    AIPU_TRY(launch_rmsnorm(a.x, gamma, a.H, nrm, a.mode, st));
     MoeArgs m = a;
     m.x = nrm;
     m.resid = a.x;
+    // fast mode with a Q4_K router on the persistent one-row kernel: the RMSNorm runs in the
+    // router's launch (each compute wave's activation pair is one wave of the norm's reduction),
+    // with the same bits as the separate norm kernel followed by the router GEMV
+    if (a.mode == AIPU_MODE_FAST && a.router_type == T_Q4_K && a.H <= 8192 &&
+        ((uintptr_t)a.x | (uintptr_t)gamma | (uintptr_t)nrm) % 16 == 0 && gemv_persist_norm_supported(a.E, a.H)) {
+        uint16_t* logits = (uint16_t*)((uint8_t*)a.ws + ws_layout(a.E, a.H, a.I, a.topk).logits);
+        AIPU_TRY(launch_gemv_persist_norm((const uint8_t*)a.router_w, a.E, a.H, a.x, gamma, recip_fp32_bits(a.H), nrm,
+                                          logits, st));
+        m.logits_ready = true;
+        return launch_moe_decode(m, st);
+    }
+    AIPU_TRY(launch_rmsnorm(a.x, gamma, a.H, nrm, a.mode, st));
     return launch_moe_decode(m, st);
 }
 

@@ -11,13 +11,13 @@
 #include "common.hpp"
 #include "glm_act.hpp"
 #include "launch.hpp"
+#include "norm.hpp"
 
 namespace aipu {
 namespace {
 
 constexpr int kNormThreads = 256;
 constexpr int kSqChunk = 4096;                  // squares staged per round (16 KB)
-constexpr uint32_t kEpsBits = 0x3727C5ACu;      // 1e-5, tools/glm_model_q4k_ref.py:432
 
 __device__ __forceinline__ void norm_apply(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
                                            int64_t n, float inv, uint16_t* __restrict__ y) {
@@ -25,11 +25,6 @@ __device__ __forceinline__ void norm_apply(const uint16_t* __restrict__ x, const
         const float xs = bf16_to_f32(x[i]) * inv;
         y[i] = (uint16_t)bf16_rne(xs * bf16_to_f32(gamma[i]));
     }
-}
-
-__device__ __forceinline__ float norm_inv(float sumsq, uint32_t inv_len_bits) {
-    const float mean = sumsq * __uint_as_float(inv_len_bits);
-    return glm_rsqrt(mean + __uint_as_float(kEpsBits));
 }
 
 // Reference order: lane 0 adds the squares in element order.
@@ -81,13 +76,14 @@ __global__ void __launch_bounds__(kNormThreads) k_rmsnorm_seq(const uint16_t* __
 }
 
 // Tolerance mode, n <= 8 * 1024 with n % 8 == 0 and 16-B aligned vectors: each thread
-// holds 8 elements of x and gamma in registers across the tree reduction.
-constexpr int kTreeThreads = 1024;
+// holds 8 elements of x and gamma in registers across the tree reduction (norm.hpp's order;
+// the Q4_K router GEMV of the FFN half evaluates the same one, gemv_persist.hip).
+constexpr int kTreeThreads = 64 * kNormWaves;
 
 __global__ void __launch_bounds__(kTreeThreads) k_rmsnorm_vec(const uint4* __restrict__ x,
                                                               const uint4* __restrict__ gamma, int n8,
                                                               uint32_t inv_len_bits, uint4* __restrict__ y) {
-    __shared__ float part[kTreeThreads / 64];
+    __shared__ float part[kNormWaves];
     __shared__ float s_inv;
     const int t = threadIdx.x;
     uint4 xv = make_uint4(0, 0, 0, 0), gv = make_uint4(0, 0, 0, 0);
@@ -95,36 +91,16 @@ __global__ void __launch_bounds__(kTreeThreads) k_rmsnorm_vec(const uint4* __res
         xv = x[t];
         gv = gamma[t];
     }
-    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-    float s = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float a = __uint_as_float(xw[k] << 16), b = __uint_as_float(xw[k] & 0xFFFF0000u);
-        s = __builtin_fmaf(a, a, s);
-        s = __builtin_fmaf(b, b, s);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) s += shfl_xor_f(s, o);
+    const float s = norm_wave_sum(norm_sq8(xv));
     if ((t & 63) == 0) part[t >> 6] = s;
     __syncthreads();
     if (t < 64) {
-        float v = t < kTreeThreads / 64 ? part[t] : 0.0f;
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) v += shfl_xor_f(v, o);
+        const float v = norm_final_sum(t < kNormWaves ? part[t] : 0.0f);
         if (t == 0) s_inv = norm_inv(v, inv_len_bits);
     }
     __syncthreads();
     if (t >= n8) return;
-    const float inv = s_inv;
-    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float lo = (__uint_as_float(xw[k] << 16) * inv) * __uint_as_float(gw[k] << 16);
-        const float hi = (__uint_as_float(xw[k] & 0xFFFF0000u) * inv) * __uint_as_float(gw[k] & 0xFFFF0000u);
-        o[k] = bf16_rne(lo) | (bf16_rne(hi) << 16);
-    }
-    y[t] = make_uint4(o[0], o[1], o[2], o[3]);
+    y[t] = norm_apply8(xv, gv, s_inv);
 }
 
 // Tolerance mode, any n: per-thread strided sums, then a tree over the workgroup.

@@ -69,20 +69,23 @@ def test_moe_layer_random_ref():
     assert_bits_equal(h_bits(y), r["y"], "layer y random")
 
 
-def test_moe_layer_fast_c2_shape():
-    """Config-2 shape over 32 experts with a Q4_K router and a shared expert: the fused call
-    equals rmsnorm -> MoE step -> residual run as three separate calls (bitwise), and the
-    fast RMSNorm it starts from is within one bf16 ulp of the reference order."""
-    E, H, I, topk = 32, 6144, 2048, 8
-    note("moe layer fast C2")
+@pytest.mark.parametrize("E,H,I", [(32, 6144, 2048), (256, 6144, 2048), (16, 2304, 256), (16, 8192, 2048)])
+def test_moe_layer_fast_c2_shape(E, H, I):
+    """Q4_K router and a shared expert, at the config-2 expert shape (32 experts and all 256),
+    an odd count of 256-blocks (H = 2304) and two block pairs per router wave (H = 8192): the
+    fused call, whose router launch applies the RMSNorm itself, equals rmsnorm -> MoE step ->
+    residual run as three separate calls (bitwise), and the fast RMSNorm it starts from is
+    within one bf16 ulp of the reference order."""
+    topk = 8
+    note(f"moe layer fast E={E} H={H} I={I}")
     gen = torch.Generator(device="cuda")
-    gen.manual_seed(6)
+    gen.manual_seed(6 + H + E)
     ge = random_weights_gpu(Q4K, E * I, H, gen)
     ue = random_weights_gpu(Q4K, E * I, H, gen)
     de = random_weights_gpu(Q4K, E * H, I, gen)
     rw = random_weights_gpu(Q4K, E, H, gen)
     sh = (random_weights_gpu(Q4K, I, H, gen), random_weights_gpu(Q4K, I, H, gen), random_weights_gpu(Q4K, H, I, gen))
-    rng = np.random.default_rng(6)
+    rng = np.random.default_rng(6 + H + E)
     h = d_bf16(qo.random_bf16(rng, H, scale=0.5))
     g = d_bf16(qo.random_bf16(rng, H))
     y, sel, sw = dev.moe_layer_decode(Q4K, rw, Q4K, ge, ue, de, E, H, I, topk, h, g, mode="fast", shared=sh)
