@@ -99,6 +99,35 @@ def test_moe_layer_fast_c2_shape(E, H, I):
     assert qo.bf16_ulp_distance(h_bits(nrm), h_bits(nr)).max() <= 1
 
 
+@pytest.mark.parametrize("E,H,I,gamma_off", [(3000, 2304, 256, 0), (32, 6144, 2048, 1)])
+def test_moe_layer_fast_router_norm_edges(E, H, I, gamma_off):
+    """The RMSNorm in the router's launch at two router tiles per CU (3,000 experts, the one-wave
+    routing tail), and the separate RMSNorm launch it falls back to when gamma is not 16-B
+    aligned (the norm kernel then takes its unaligned order): the fused call equals rmsnorm ->
+    MoE step -> residual run as three separate calls (bitwise) either way."""
+    topk = 8
+    note(f"moe layer fast router norm E={E} H={H} I={I} gamma offset {gamma_off}")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(E + H)
+    ge = random_weights_gpu(Q4K, E * I, H, gen)
+    ue = random_weights_gpu(Q4K, E * I, H, gen)
+    de = random_weights_gpu(Q4K, E * H, I, gen)
+    rw = random_weights_gpu(Q4K, E, H, gen)
+    sh = (random_weights_gpu(Q4K, I, H, gen), random_weights_gpu(Q4K, I, H, gen), random_weights_gpu(Q4K, H, I, gen))
+    rng = np.random.default_rng(E + H)
+    h = d_bf16(qo.random_bf16(rng, H, scale=0.5))
+    gbuf = d_bf16(qo.random_bf16(rng, H + 8))
+    g = gbuf[gamma_off:gamma_off + H]
+    assert (g.data_ptr() % 16 == 0) == (gamma_off == 0)
+    y, sel, sw = dev.moe_layer_decode(Q4K, rw, Q4K, ge, ue, de, E, H, I, topk, h, g, mode="fast", shared=sh)
+    nrm = dev.rmsnorm(h, g, mode="fast")
+    f, sel2, sw2 = dev.moe_swiglu_decode(Q4K, rw, Q4K, ge, ue, de, E, H, I, topk, nrm, mode="fast", shared=sh)
+    want = (h.float() + f.float()).to(torch.bfloat16)     # RNE of an exact fp32 sum of two bf16
+    assert torch.equal(sel, sel2)
+    assert_bits_equal(h_bits(sw), h_bits(sw2), "sel_w")
+    assert_bits_equal(h_bits(y), h_bits(want), "layer = pieces")
+
+
 def test_moe_layer_fast_persistent_legs():
     """A layer without a shared expert and with a bf16 router runs the persistent expert legs,
     the residual added in the down leg's epilogue: the fused call equals rmsnorm -> MoE step ->
