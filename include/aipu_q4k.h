@@ -214,7 +214,10 @@ int aipu_rmsnorm(const uint16_t* x, const uint16_t* gamma, int64_t n, uint16_t* 
  * step (as aipu_moe_swiglu_decode) on rmsnorm(h, gamma).  Replaces
  * tools/glm_model_q4k_ref.py:797-810 (decoder_block after the attention residual).
  * Arguments as aipu_moe_swiglu_decode with x -> h and gamma[H] added; the workspace is
- * aipu_moe_layer_workspace_bytes(E, H, I, topk) bytes, any contents. */
+ * aipu_moe_layer_workspace_bytes(E, H, I, topk) bytes, any contents.  In AIPU_MODE_FAST the
+ * output equals aipu_rmsnorm (fast) followed by aipu_moe_swiglu_decode and the residual, bit for
+ * bit; with a Q4_K router, H <= 8192 and 16-B aligned h and gamma the norm runs inside the
+ * router's launch. */
 int64_t aipu_moe_layer_workspace_bytes(int64_t E, int64_t H, int64_t I, int topk);
 int aipu_moe_layer_decode(int router_type, const void* router_w, int ggml_type,
                           const void* gate_exps, const void* up_exps, const void* down_exps,
