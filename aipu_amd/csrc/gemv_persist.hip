@@ -57,10 +57,11 @@ struct NormIn {
 // wave.  nsb = K / 256 is a runtime value with ceil(144 * nsb / 1024) == R.  COPY_ONLY = true
 // is a measurement variant (aipu_measure_gemv): the copy wave runs the same copy schedule and
 // the compute waves leave after the first barrier, so nothing is computed or written.
-template <int R, int TT, int XPW, bool COPY_ONLY = false, bool NORM = false>
+template <int R, int TT, int XPW, bool COPY_ONLY = false, bool NORM = false, int MR = 1>
 __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __restrict__ W, int64_t N, int nsb,
                                                              const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
-                                                             float* __restrict__ Yf, int ntiles, NormIn nm) {
+                                                             float* __restrict__ Yf, int ntiles, NormIn nm, int64_t ys) {
+    static_assert(MR == 1 || (MR == 2 && XPW == 1 && !NORM && !COPY_ONLY), "two rows: one pair per wave");
     constexpr int NB = TT < 3 ? TT : 3;                        // tile buffers
     // rounds in flight: up to 4; with buffer reuse (TT > NB) at most (NB - 1) R + 1 (see the
     // reuse wait), without it at most the TT R rounds there are
@@ -68,8 +69,8 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     constexpr int Q = 4 < QL ? 4 : QL;
     static_assert(Q >= 1 && 8 * Q <= 63, "rounds in flight within vmcnt");
     extern __shared__ __align__(16) uint8_t s_tile[];          // NB * 8 * pitch (direct-to-LDS targets only)
-    __shared__ __align__(16) uint8_t s_stage[kPMaxPairs * kPStage];
-    __shared__ __align__(16) float s_red[NB * kPR * kPMaxPairs];
+    __shared__ __align__(16) uint8_t s_stage[kPMaxPairs * kPStage * MR];     // [pair][row]
+    __shared__ __align__(16) float s_red[NB * MR * kPR * kPMaxPairs];         // [buffer][row][tile row][pair]
     __shared__ uint32_t s_cnt[TT * R];                          // rounds landed
     __shared__ uint32_t s_done[TT];                             // pairs finished per tile
     __shared__ uint32_t s_freed[TT];                            // tile reduced, buffers free
@@ -92,9 +93,12 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     if (NORM && tid == 0) s_normc = 0u;
 
     // activation loads of the wave's own pairs go out before any weight copy
-    uint4 xv[XPW], gv[XPW];
+    uint4 xv[XPW], gv[XPW], xv1 = make_uint4(0u, 0u, 0u, 0u);
     if (w < NCW) {
         const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)nsb * 512u);   // an odd nsb's last pair reads zeros
+        if constexpr (MR == 2)   // the second row, X + K
+            xv1 = buf_load16(buf_rsrc(X + (int64_t)nsb * 256, (uint32_t)nsb * 512u),
+                             w < np ? (uint32_t)w * 1024u + 16u * (uint32_t)lane : kOOB);
         const __amdgpu_buffer_rsrc_t gr = buf_rsrc(nm.gamma, NORM ? (uint32_t)nsb * 512u : 0u);
 #pragma unroll
         for (int i = 0; i < XPW; ++i) {
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     }
     const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
     u32x4_t A[XPW][8];
-    float2 as[XPW];
+    float2 as[XPW], as1 = float2{0.f, 0.f};   // as1: the second row's sums (MR = 2)
 #pragma unroll
     for (int i = 0; i < XPW; ++i) {
 #pragma unroll
@@ -180,6 +184,40 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
         as[i] = float2{0.f, 0.f};
         const int p = w + NCW * i;
         if (p >= np) continue;
+        if constexpr (MR == 2) {
+            // both rows staged; A rows 4g + 2m + hh carry row m of block 2p + hh, so the diagonal
+            // lanes 16g + 4g + j (j < 4) read row j >> 1's entries of block j & 1
+            uint8_t* st0 = s_stage + (uint32_t)(2 * p) * kPStage;
+            uint8_t* st1 = st0 + kPStage;
+            stage_pair(xv[i], st0, lane);
+            stage_pair(xv1, st1, lane);
+            const int j = (n - 4 * g) & 3;
+            const uint32_t aa = lds_addr((j >> 1) & 1 ? st1 : st0) + 32u * (uint32_t)g + 16u * (uint32_t)(j & 1);
+            const uint32_t so = kStgSums + 8u * (uint32_t)(g * 2 + h);
+            uint64_t saved;
+            asm volatile(
+                "s_waitcnt lgkmcnt(0)\n\t"
+                "s_mov_b64 %[sv], exec\n\t"
+                "s_and_b64 exec, exec, %[mask]\n\t"
+                "ds_read_b128 %[a0], %[aa]\n\t"
+                "ds_read_b128 %[a1], %[aa] offset:144\n\t"
+                "ds_read_b128 %[a2], %[aa] offset:288\n\t"
+                "ds_read_b128 %[a3], %[aa] offset:432\n\t"
+                "ds_read_b128 %[a4], %[aa] offset:576\n\t"
+                "ds_read_b128 %[a5], %[aa] offset:720\n\t"
+                "ds_read_b128 %[a6], %[aa] offset:864\n\t"
+                "ds_read_b128 %[a7], %[aa] offset:1008\n\t"
+                "s_mov_b64 exec, %[sv]\n\t"
+                "ds_read_b64 %[s0], %[p0]\n\t"
+                "ds_read_b64 %[s1], %[p1]\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : [a0] "+v"(A[i][0]), [a1] "+v"(A[i][1]), [a2] "+v"(A[i][2]), [a3] "+v"(A[i][3]), [a4] "+v"(A[i][4]),
+                  [a5] "+v"(A[i][5]), [a6] "+v"(A[i][6]), [a7] "+v"(A[i][7]), [s0] "=&v"(as[i]), [s1] "=&v"(as1),
+                  [sv] "=&s"(saved)
+                : [aa] "v"(aa), [mask] "s"(diag_mask(4)), [p0] "v"(lds_addr(st0) + so), [p1] "v"(lds_addr(st1) + so)
+                : "memory", "scc");   // s_and_b64 writes SCC
+            continue;
+        }
         uint8_t* st = s_stage + (uint32_t)p * kPStage;
         stage_pair(xv[i], st, lane);
         // the operands (diagonal lanes 16g + 4g + h, h < 2) and this lane's sums
@@ -246,7 +284,12 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
             f32x4_t dlo, dhi;
             dlo[0] = dlo[1] = -kCodeBiasF * as[i].x;
             dhi[0] = dhi[1] = -kCodeBiasF * as[i].y;
-            dlo[2] = dlo[3] = dhi[2] = dhi[3] = 0.f;
+            if constexpr (MR == 2) {   // D[4g + 2m + hh][n]: row m's seeds in registers 2m, 2m + 1
+                dlo[2] = dlo[3] = -kCodeBiasF * as1.x;
+                dhi[2] = dhi[3] = -kCodeBiasF * as1.y;
+            } else {
+                dlo[2] = dlo[3] = dhi[2] = dhi[3] = 0.f;
+            }
             const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
@@ -254,12 +297,23 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
                 dhi = mfma(A[i][4 + tt], codes_hi(qd[2 * tt], qd[2 * tt + 1], ck), dhi);
             }
             const Hdr H = hdr_decode(make_uint4(hv.x, hv.y, hv.z, hv.w), hs);
-            const float bt = block_sum(block_term(H, h ? dlo[1] : dlo[0], h ? dhi[1] : dhi[0], as[i].x, as[i].y));
-            // pair sum on lanes 0..7 (row r): block 2p, then block 2p+1 from lane r + 8
+            float bt;
+            if constexpr (MR == 2) {   // lane 16i + n: row i & 1's block sum (the additions of block_sum)
+                const float t0 = block_term(H, h ? dlo[1] : dlo[0], h ? dhi[1] : dhi[0], as[i].x, as[i].y);
+                const float t1 = block_term(H, h ? dlo[3] : dlo[2], h ? dhi[3] : dhi[2], as1.x, as1.y);
+                bt = block_sum2(t0, t1);
+            } else {
+                bt = block_sum(block_term(H, h ? dlo[1] : dlo[0], h ? dhi[1] : dhi[0], as[i].x, as[i].y));
+            }
+            // pair sum on lanes 16i + r (row r): block 2p, then block 2p+1 from lane 16i + r + 8
             const float b1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bt), 0x108, 0xF, 0xF, false));
             const float ps = bt + (2 * p + 1 < nsb ? b1 : 0.0f);
-            float* rt = s_red + (t % NB) * (kPR * kPMaxPairs);
-            if (lane < kPR) rt[lane * kPMaxPairs + p] = ps;
+            float* rt = s_red + (t % NB) * (MR * kPR * kPMaxPairs);
+            if constexpr (MR == 2) {
+                if (lane < 32 && (lane & 15) < kPR) rt[((lane >> 4) * kPR + (lane & 7)) * kPMaxPairs + p] = ps;
+            } else {
+                if (lane < kPR) rt[lane * kPMaxPairs + p] = ps;
+            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
             if (t == T - 1) last_done = lds_add_rtn(&s_done[t]) == (uint32_t)np - 1u;
             else lds_post(&s_done[t]);
@@ -270,8 +324,9 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
         // whose post completes it reduces it, with no wait.
         if (t == T - 1 ? last_done : w == 0) {
             if (t < T - 1) spin_ge(&s_done[t], (uint32_t)np);
-            const float* rt = s_red + (t % NB) * (kPR * kPMaxPairs);
-            {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const float* rt = s_red + (t % NB) * (MR * kPR * kPMaxPairs) + m * (kPR * kPMaxPairs);
                 // v_k on lane 8 * row + k, then the tree (xor 1, xor 2, mirror)
                 const int rr = lane >> 3, k = lane & 7;
                 float v = k < np ? rt[rr * kPMaxPairs + k] : 0.0f;
@@ -281,12 +336,12 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
                 v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
                 const int64_t row = (int64_t)(wg + t * G) * kPR + rr;
                 if (k == 0 && row < N) {
-                    Y[row] = (uint16_t)bf16_rne(v);
-                    if (Yf) Yf[row] = v;
+                    Y[m * ys + row] = (uint16_t)bf16_rne(v);
+                    if (Yf) Yf[m * ys + row] = v;
                 }
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads of rt done before the buffer is reused
-                lds_post(&s_freed[t]);
             }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads of rt done before the buffer is reused
+            lds_post(&s_freed[t]);
         }
     }
 }
@@ -312,16 +367,19 @@ hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16
     const dim3 grid(G), block(64 * (ncw + 1));
     if constexpr (NORM) {   // the FFN half's router: at most two tiles per workgroup
         if (TT == 1)
-            hipLaunchKernelGGL((k_gemv1p<R, 1, XPW, false, true>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm);
+            hipLaunchKernelGGL((k_gemv1p<R, 1, XPW, false, true>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm,
+                               (int64_t)0);
         else if (TT == 2)
-            hipLaunchKernelGGL((k_gemv1p<R, 2, XPW, false, true>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm);
+            hipLaunchKernelGGL((k_gemv1p<R, 2, XPW, false, true>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm,
+                               (int64_t)0);
         else
             return hipErrorInvalidValue;
         return hipGetLastError();
     }
     switch (TT) {
 #define AIPU_P(TV) \
-    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, XPW, COPY_ONLY>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm); break;
+    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, XPW, COPY_ONLY>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm, \
+                                (int64_t)0); break;
         AIPU_P(1)
         AIPU_P(2)
         AIPU_P(3)
@@ -331,6 +389,26 @@ hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16
         AIPU_P(7)
         AIPU_P(8)
 #undef AIPU_P
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Two activation rows (K <= 6144: one block pair per compute wave), at most four tiles per workgroup.
+template <int R>
+hipError_t run_p2(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16_t* y, float* yf, int64_t ys, int TT,
+                  int G, int ntiles, int ncw, size_t lds, hipStream_t st) {
+    const dim3 grid(G), block(64 * (ncw + 1));
+    const NormIn nm{nullptr, 0u, nullptr};
+    switch (TT) {
+#define AIPU_P2(TV) \
+    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, 1, false, false, 2>), grid, block, lds, st, W, N, nsb, x, y, yf, \
+                                ntiles, nm, ys); break;
+        AIPU_P2(1)
+        AIPU_P2(2)
+        AIPU_P2(3)
+        AIPU_P2(4)
+#undef AIPU_P2
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -417,6 +495,26 @@ hipError_t launch_gemv_persist_norm(const uint8_t* W, int64_t N, int64_t K, cons
         case 4 * 4 + 1: return run_p<4, 1, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
         case 4 * 4 + 2: return run_p<4, 2, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
         case 5 * 4 + 2: return run_p<5, 2, false, true>(W, N, nsb, x, y, nullptr, TT, G, ntiles, ncw, q.lds, st, nm);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool gemv_persist2_supported(int64_t N, int64_t K) {
+    if (!gemv_persist_supported(N, K) || K > 6144) return false;
+    return p_plan(N, K).TT <= 4;
+}
+
+// Rows 0 and 1 of x (row stride K) in one launch; row m of y at y + m * ys.  Each row is formed
+// exactly as the one-row launch forms it (the same sets, block sums, pair sums and tree).
+hipError_t launch_gemv_persist2(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
+                                int64_t ys, hipStream_t st) {
+    if (!gemv_persist2_supported(N, K)) return hipErrorInvalidValue;
+    const PPlan q = p_plan(N, K);
+    switch (q.R) {
+        case 1: return run_p2<1>(W, N, q.nsb, x, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
+        case 2: return run_p2<2>(W, N, q.nsb, x, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
+        case 3: return run_p2<3>(W, N, q.nsb, x, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
+        case 4: return run_p2<4>(W, N, q.nsb, x, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
         default: return hipErrorInvalidValue;
     }
 }
