@@ -1,4 +1,6 @@
-// Persistent single-row Q4_K GEMV (tolerance mode) for K <= 8192: the M = 1 hot path.
+// Persistent single-row Q4_K GEMV (tolerance mode) for K <= 8192: the M = 1 hot path, also run
+// with two to four activation rows (MR, K <= 6144; below) and with the FFN half's RMSNorm in
+// front (NORM).
 //
 // Workgroup.  One workgroup per CU owns TT tiles of 8 rows (tiles wg, wg + G, ...), G =
 // #tiles / TT workgroups.  Wave NCW copies the tiles into LDS with direct-to-LDS buffer loads
@@ -17,7 +19,9 @@
 // MFMA set (v_mfma_f32_16x16x32_bf16, lane 16g + n): column n = row n & 7 of the tile, block
 // 2p + (n >> 3) of the pair; K-group g = qs bytes 32g .. 32g+31 of the block (sub-blocks 2g,
 // 2g+1).  A rows 4g + h carry block 2p + h's activations on group g, so D[4g + h][n] is the
-// sub-block sum of column n for h = n >> 3.  Codes, seeds and epilogue are those of
+// sub-block sum of column n for h = n >> 3.  With MR = 2 rows, A rows 4g + 2m + hh carry row m of
+// block 2p + hh (D register 2m + h holds row m's sum); MR = 4 adds a second set over the same codes
+// for rows 2, 3.  Codes, seeds and epilogue are those of
 // mfma_gemv.hpp, and the reduction follows its fast-mode order: block terms (block_sum),
 // pair sums (a row shift by 8), then the balanced tree over the pairs with three cross-lane
 // adds -- bit-identical to the canon_sum of the small-batch kernels (k_gemvs, k_gemvm).
