@@ -1143,7 +1143,7 @@ bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M) {
 
 // y[M][N] (row stride ystride) = x[M][K] . W^T, in passes of at most 8 activation rows.
 // A pass goes to a multi-row kernel only if that kernel forms each row exactly as the one-row
-// launch does (two to four rows on the persistent one-row kernel itself, the persistent row-pair
+// launch does (two rows on the persistent one-row kernel itself, the persistent row-pair
 // kernel, k_gemvm, k_gemvs: the order of mfma_gemv.hpp,
 // which the single-row kernels k_gemv1p and k_gemv1 follow); every other row runs as its own
 // one-row launch, so each row of the result is bit-identical to the one-row call on that row
@@ -1163,10 +1163,10 @@ hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t*
         uint16_t* ym = y + m0 * ystride;
         float* yfm = y_f32 ? y_f32 + m0 * ystride : nullptr;
         if (left >= 2 && canon1) {
-            if (!dense && gemv_persist_rows_supported(N, K, left)) {   // two to four rows on the one-row kernel
-                const hipError_t e = launch_gemv_persist_rows(W, N, K, xm, left, ym, yfm, ystride, st);
+            if (left == 2 && !dense && gemv_persist2_supported(N, K)) {   // two rows on the one-row kernel
+                const hipError_t e = launch_gemv_persist2(W, N, K, xm, ym, yfm, ystride, st);
                 if (e != hipSuccess) return e;
-                m0 += left;
+                m0 += 2;
                 continue;
             }
             if (gemv_persist_m_supported(N, K, left, dense)) {   // two to eight rows, one persistent pass

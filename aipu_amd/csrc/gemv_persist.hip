@@ -1,6 +1,6 @@
 // Persistent single-row Q4_K GEMV (tolerance mode) for K <= 8192: the M = 1 hot path, also run
-// with two to four activation rows (MR, K <= 6144; below) and with the FFN half's RMSNorm in
-// front (NORM).
+// with two activation rows (MR = 2, K <= 6144; below) and with the FFN half's RMSNorm in front
+// (NORM).
 //
 // Workgroup.  One workgroup per CU owns TT tiles of 8 rows (tiles wg, wg + G, ...), G =
 // #tiles / TT workgroups.  Wave NCW copies the tiles into LDS with direct-to-LDS buffer loads
@@ -20,8 +20,7 @@
 // 2p + (n >> 3) of the pair; K-group g = qs bytes 32g .. 32g+31 of the block (sub-blocks 2g,
 // 2g+1).  A rows 4g + h carry block 2p + h's activations on group g, so D[4g + h][n] is the
 // sub-block sum of column n for h = n >> 3.  With MR = 2 rows, A rows 4g + 2m + hh carry row m of
-// block 2p + hh (D register 2m + h holds row m's sum); MR = 4 adds a second set over the same codes
-// for rows 2, 3.  Codes, seeds and epilogue are those of
+// block 2p + hh (D register 2m + h holds row m's sum).  Codes, seeds and epilogue are those of
 // mfma_gemv.hpp, and the reduction follows its fast-mode order: block terms (block_sum),
 // pair sums (a row shift by 8), then the balanced tree over the pairs with three cross-lane
 // adds -- bit-identical to the canon_sum of the small-batch kernels (k_gemvs, k_gemvm).
@@ -64,10 +63,8 @@ struct NormIn {
 template <int R, int TT, int XPW, bool COPY_ONLY = false, bool NORM = false, int MR = 1>
 __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __restrict__ W, int64_t N, int nsb,
                                                              const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
-                                                             float* __restrict__ Yf, int ntiles, NormIn nm, int64_t ys,
-                                                             int mrows) {
-    static_assert(MR == 1 || ((MR == 2 || MR == 4) && XPW == 1 && !NORM && !COPY_ONLY), "rows: one pair per wave");
-    constexpr int kStagePairs = MR == 4 ? kPMaxCW : kPMaxPairs;   // four rows: K <= 6144 keeps the LDS in bounds
+                                                             float* __restrict__ Yf, int ntiles, NormIn nm, int64_t ys) {
+    static_assert(MR == 1 || (MR == 2 && XPW == 1 && !NORM && !COPY_ONLY), "two rows: one pair per wave");
     constexpr int NB = TT < 3 ? TT : 3;                        // tile buffers
     // rounds in flight: up to 4; with buffer reuse (TT > NB) at most (NB - 1) R + 1 (see the
     // reuse wait), without it at most the TT R rounds there are
@@ -75,14 +72,13 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     constexpr int Q = 4 < QL ? 4 : QL;
     static_assert(Q >= 1 && 8 * Q <= 63, "rounds in flight within vmcnt");
     extern __shared__ __align__(16) uint8_t s_tile[];          // NB * 8 * pitch (direct-to-LDS targets only)
-    __shared__ __align__(16) uint8_t s_stage[kStagePairs * kPStage * MR];    // [pair][row]
+    __shared__ __align__(16) uint8_t s_stage[kPMaxPairs * kPStage * MR];     // [pair][row]
     __shared__ __align__(16) float s_red[NB * MR * kPR * kPMaxPairs];         // [buffer][row][tile row][pair]
     __shared__ uint32_t s_cnt[TT * R];                          // rounds landed
     __shared__ uint32_t s_done[TT];                             // pairs finished per tile
     __shared__ uint32_t s_freed[TT];                            // tile reduced, buffers free
     __shared__ float s_part[kNormWaves];                        // NORM: the waves' sums of squares
     __shared__ uint32_t s_normc;                                // NORM: sums posted
-    __shared__ __align__(16) uint8_t s_zero[MR == 4 ? 1024 : 16];   // MR = 4: what off-diagonal lanes read
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int NCW = (int)(blockDim.x >> 6) - 1;
@@ -98,16 +94,14 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
         s_freed[tid] = 0u;
     }
     if (NORM && tid == 0) s_normc = 0u;
-    if (MR == 4 && tid < 64) *(uint4*)(s_zero + 16 * tid) = make_uint4(0u, 0u, 0u, 0u);
 
     // activation loads of the wave's own pairs go out before any weight copy
-    uint4 xv[XPW], gv[XPW], xvr[MR > 1 ? MR - 1 : 1];   // xvr: rows 1 .. MR-1 (rows past mrows read zeros)
+    uint4 xv[XPW], gv[XPW], xv1 = make_uint4(0u, 0u, 0u, 0u);
     if (w < NCW) {
         const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X, (uint32_t)nsb * 512u);   // an odd nsb's last pair reads zeros
-#pragma unroll
-        for (int m = 1; m < MR; ++m)   // row m at X + m K
-            xvr[m - 1] = buf_load16(buf_rsrc(X + (int64_t)m * nsb * 256, m < mrows ? (uint32_t)nsb * 512u : 0u),
-                                    w < np ? (uint32_t)w * 1024u + 16u * (uint32_t)lane : kOOB);
+        if constexpr (MR == 2)   // the second row, X + K
+            xv1 = buf_load16(buf_rsrc(X + (int64_t)nsb * 256, (uint32_t)nsb * 512u),
+                             w < np ? (uint32_t)w * 1024u + 16u * (uint32_t)lane : kOOB);
         const __amdgpu_buffer_rsrc_t gr = buf_rsrc(nm.gamma, NORM ? (uint32_t)nsb * 512u : 0u);
 #pragma unroll
         for (int i = 0; i < XPW; ++i) {
@@ -185,9 +179,7 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
     }
     const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
     u32x4_t A[XPW][8];
-    float2 as[XPW], as1 = float2{0.f, 0.f};   // as1: the second row's sums (MR >= 2)
-    float2 as2 = float2{0.f, 0.f}, as3 = float2{0.f, 0.f};   // rows 2, 3 (MR = 4)
-    uint32_t aa2 = 0u;   // MR = 4: where this lane reads rows 2, 3's operands in every set (a zero block off the diagonal)
+    float2 as[XPW], as1 = float2{0.f, 0.f};   // as1: the second row's sums (MR = 2)
 #pragma unroll
     for (int i = 0; i < XPW; ++i) {
 #pragma unroll
@@ -195,52 +187,38 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
         as[i] = float2{0.f, 0.f};
         const int p = w + NCW * i;
         if (p >= np) continue;
-        if constexpr (MR >= 2) {
-            // every row staged; A rows 4g + 2m + hh carry row m of block 2p + hh (rows 2k, 2k + 1 in
-            // row pair k), so the diagonal lanes 16g + 4g + j (j < 4) read row 2k + (j >> 1)'s
-            // entries of block j & 1
-            uint8_t* stp = s_stage + (uint32_t)(MR * p) * kPStage;
-            stage_pair(xv[i], stp, lane);
-#pragma unroll
-            for (int m = 1; m < MR; ++m) stage_pair(xvr[m - 1], stp + (uint32_t)m * kPStage, lane);
+        if constexpr (MR == 2) {
+            // both rows staged; A rows 4g + 2m + hh carry row m of block 2p + hh, so the diagonal
+            // lanes 16g + 4g + j (j < 4) read row j >> 1's entries of block j & 1
+            uint8_t* st0 = s_stage + (uint32_t)(2 * p) * kPStage;
+            uint8_t* st1 = st0 + kPStage;
+            stage_pair(xv[i], st0, lane);
+            stage_pair(xv1, st1, lane);
             const int j = (n - 4 * g) & 3;
+            const uint32_t aa = lds_addr((j >> 1) & 1 ? st1 : st0) + 32u * (uint32_t)g + 16u * (uint32_t)(j & 1);
             const uint32_t so = kStgSums + 8u * (uint32_t)(g * 2 + h);
-            if constexpr (MR == 4) {   // rows 2, 3: their sums now, their operands in every set
-                const uint32_t st2 = lds_addr(stp) + 2u * kPStage, st3 = st2 + kPStage;
-                aa2 = (n >> 2) == g ? ((j >> 1) & 1 ? st3 : st2) + 32u * (uint32_t)g + 16u * (uint32_t)(j & 1)
-                                    : lds_addr(s_zero);
-                asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b64 %0, %2\n\tds_read_b64 %1, %3\n\ts_waitcnt lgkmcnt(0)"
-                             : "=&v"(as2), "=&v"(as3) : "v"(st2 + so), "v"(st3 + so) : "memory");
-            }
-            {
-                const uint32_t st0 = lds_addr(stp), st1 = st0 + kPStage;
-                const uint32_t aa = ((j >> 1) & 1 ? st1 : st0) + 32u * (uint32_t)g + 16u * (uint32_t)(j & 1);
-                u32x4_t(&Ak)[8] = A[i];
-                float2& sa0 = as[i];
-                float2& sa1 = as1;
-                uint64_t saved;
-                asm volatile(
-                    "s_waitcnt lgkmcnt(0)\n\t"
-                    "s_mov_b64 %[sv], exec\n\t"
-                    "s_and_b64 exec, exec, %[mask]\n\t"
-                    "ds_read_b128 %[a0], %[aa]\n\t"
-                    "ds_read_b128 %[a1], %[aa] offset:144\n\t"
-                    "ds_read_b128 %[a2], %[aa] offset:288\n\t"
-                    "ds_read_b128 %[a3], %[aa] offset:432\n\t"
-                    "ds_read_b128 %[a4], %[aa] offset:576\n\t"
-                    "ds_read_b128 %[a5], %[aa] offset:720\n\t"
-                    "ds_read_b128 %[a6], %[aa] offset:864\n\t"
-                    "ds_read_b128 %[a7], %[aa] offset:1008\n\t"
-                    "s_mov_b64 exec, %[sv]\n\t"
-                    "ds_read_b64 %[s0], %[p0]\n\t"
-                    "ds_read_b64 %[s1], %[p1]\n\t"
-                    "s_waitcnt lgkmcnt(0)"
-                    : [a0] "+v"(Ak[0]), [a1] "+v"(Ak[1]), [a2] "+v"(Ak[2]), [a3] "+v"(Ak[3]), [a4] "+v"(Ak[4]),
-                      [a5] "+v"(Ak[5]), [a6] "+v"(Ak[6]), [a7] "+v"(Ak[7]), [s0] "=&v"(sa0), [s1] "=&v"(sa1),
-                      [sv] "=&s"(saved)
-                    : [aa] "v"(aa), [mask] "s"(diag_mask(4)), [p0] "v"(st0 + so), [p1] "v"(st1 + so)
-                    : "memory", "scc");   // s_and_b64 writes SCC
-            }
+            uint64_t saved;
+            asm volatile(
+                "s_waitcnt lgkmcnt(0)\n\t"
+                "s_mov_b64 %[sv], exec\n\t"
+                "s_and_b64 exec, exec, %[mask]\n\t"
+                "ds_read_b128 %[a0], %[aa]\n\t"
+                "ds_read_b128 %[a1], %[aa] offset:144\n\t"
+                "ds_read_b128 %[a2], %[aa] offset:288\n\t"
+                "ds_read_b128 %[a3], %[aa] offset:432\n\t"
+                "ds_read_b128 %[a4], %[aa] offset:576\n\t"
+                "ds_read_b128 %[a5], %[aa] offset:720\n\t"
+                "ds_read_b128 %[a6], %[aa] offset:864\n\t"
+                "ds_read_b128 %[a7], %[aa] offset:1008\n\t"
+                "s_mov_b64 exec, %[sv]\n\t"
+                "ds_read_b64 %[s0], %[p0]\n\t"
+                "ds_read_b64 %[s1], %[p1]\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : [a0] "+v"(A[i][0]), [a1] "+v"(A[i][1]), [a2] "+v"(A[i][2]), [a3] "+v"(A[i][3]), [a4] "+v"(A[i][4]),
+                  [a5] "+v"(A[i][5]), [a6] "+v"(A[i][6]), [a7] "+v"(A[i][7]), [s0] "=&v"(as[i]), [s1] "=&v"(as1),
+                  [sv] "=&s"(saved)
+                : [aa] "v"(aa), [mask] "s"(diag_mask(4)), [p0] "v"(lds_addr(st0) + so), [p1] "v"(lds_addr(st1) + so)
+                : "memory", "scc");   // s_and_b64 writes SCC
             continue;
         }
         uint8_t* st = s_stage + (uint32_t)p * kPStage;
@@ -309,56 +287,21 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
             f32x4_t dlo, dhi;
             dlo[0] = dlo[1] = -kCodeBiasF * as[i].x;
             dhi[0] = dhi[1] = -kCodeBiasF * as[i].y;
-            f32x4_t dlo2, dhi2;   // row pair 1 (MR = 4)
-            if constexpr (MR >= 2) {   // D[4g + 2m + hh][n]: row m's seeds in registers 2m, 2m + 1
+            if constexpr (MR == 2) {   // D[4g + 2m + hh][n]: row m's seeds in registers 2m, 2m + 1
                 dlo[2] = dlo[3] = -kCodeBiasF * as1.x;
                 dhi[2] = dhi[3] = -kCodeBiasF * as1.y;
             } else {
                 dlo[2] = dlo[3] = dhi[2] = dhi[3] = 0.f;
             }
-            if constexpr (MR == 4) {
-                dlo2[0] = dlo2[1] = -kCodeBiasF * as2.x;
-                dhi2[0] = dhi2[1] = -kCodeBiasF * as2.y;
-                dlo2[2] = dlo2[3] = -kCodeBiasF * as3.x;
-                dhi2[2] = dhi2[3] = -kCodeBiasF * as3.y;
-            }
-            u32x4_t A2[8];   // MR = 4: rows 2, 3's operands for this set (zeros off the diagonal)
-            if constexpr (MR == 4) {
-                asm volatile(
-                    "ds_read_b128 %0, %8\n\t"
-                    "ds_read_b128 %1, %8 offset:144\n\t"
-                    "ds_read_b128 %2, %8 offset:288\n\t"
-                    "ds_read_b128 %3, %8 offset:432\n\t"
-                    "ds_read_b128 %4, %8 offset:576\n\t"
-                    "ds_read_b128 %5, %8 offset:720\n\t"
-                    "ds_read_b128 %6, %8 offset:864\n\t"
-                    "ds_read_b128 %7, %8 offset:1008\n\t"
-                    "s_waitcnt lgkmcnt(0)"
-                    : "=&v"(A2[0]), "=&v"(A2[1]), "=&v"(A2[2]), "=&v"(A2[3]), "=&v"(A2[4]), "=&v"(A2[5]), "=&v"(A2[6]),
-                      "=&v"(A2[7])
-                    : "v"(aa2)
-                    : "memory");
-            }
             const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
-                const u32x4_t cl = codes_lo(qd[2 * tt], qd[2 * tt + 1], ck), ch = codes_hi(qd[2 * tt], qd[2 * tt + 1], ck);
-                dlo = mfma(A[i][tt], cl, dlo);
-                dhi = mfma(A[i][4 + tt], ch, dhi);
-                if constexpr (MR == 4) {   // the same codes against rows 2, 3
-                    dlo2 = mfma(A2[tt], cl, dlo2);
-                    dhi2 = mfma(A2[4 + tt], ch, dhi2);
-                }
+                dlo = mfma(A[i][tt], codes_lo(qd[2 * tt], qd[2 * tt + 1], ck), dlo);
+                dhi = mfma(A[i][4 + tt], codes_hi(qd[2 * tt], qd[2 * tt + 1], ck), dhi);
             }
             const Hdr H = hdr_decode(make_uint4(hv.x, hv.y, hv.z, hv.w), hs);
             float bt;
-            if constexpr (MR == 4) {   // lane 16i + n: row i's block sum (the additions of block_sum)
-                const float t0 = block_term(H, h ? dlo[1] : dlo[0], h ? dhi[1] : dhi[0], as[i].x, as[i].y);
-                const float t1 = block_term(H, h ? dlo[3] : dlo[2], h ? dhi[3] : dhi[2], as1.x, as1.y);
-                const float t2 = block_term(H, h ? dlo2[1] : dlo2[0], h ? dhi2[1] : dhi2[0], as2.x, as2.y);
-                const float t3 = block_term(H, h ? dlo2[3] : dlo2[2], h ? dhi2[3] : dhi2[2], as3.x, as3.y);
-                bt = block_sum4(t0, t1, t2, t3);
-            } else if constexpr (MR == 2) {   // lane 16i + n: row i & 1's block sum
+            if constexpr (MR == 2) {   // lane 16i + n: row i & 1's block sum (the additions of block_sum)
                 const float t0 = block_term(H, h ? dlo[1] : dlo[0], h ? dhi[1] : dhi[0], as[i].x, as[i].y);
                 const float t1 = block_term(H, h ? dlo[3] : dlo[2], h ? dhi[3] : dhi[2], as1.x, as1.y);
                 bt = block_sum2(t0, t1);
@@ -369,9 +312,7 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
             const float b1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bt), 0x108, 0xF, 0xF, false));
             const float ps = bt + (2 * p + 1 < nsb ? b1 : 0.0f);
             float* rt = s_red + (t % NB) * (MR * kPR * kPMaxPairs);
-            if constexpr (MR == 4) {
-                if ((lane & 15) < kPR) rt[((lane >> 4) * kPR + (lane & 7)) * kPMaxPairs + p] = ps;
-            } else if constexpr (MR == 2) {
+            if constexpr (MR == 2) {
                 if (lane < 32 && (lane & 15) < kPR) rt[((lane >> 4) * kPR + (lane & 7)) * kPMaxPairs + p] = ps;
             } else {
                 if (lane < kPR) rt[lane * kPMaxPairs + p] = ps;
@@ -397,7 +338,7 @@ __global__ __launch_bounds__(64 * (kPMaxCW + 1)) void k_gemv1p(const uint8_t* __
                 v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
                 v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
                 const int64_t row = (int64_t)(wg + t * G) * kPR + rr;
-                if (k == 0 && row < N && m < mrows) {
+                if (k == 0 && row < N) {
                     Y[m * ys + row] = (uint16_t)bf16_rne(v);
                     if (Yf) Yf[m * ys + row] = v;
                 }
@@ -430,10 +371,10 @@ hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16
     if constexpr (NORM) {   // the FFN half's router: at most two tiles per workgroup
         if (TT == 1)
             hipLaunchKernelGGL((k_gemv1p<R, 1, XPW, false, true>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm,
-                               (int64_t)0, 1);
+                               (int64_t)0);
         else if (TT == 2)
             hipLaunchKernelGGL((k_gemv1p<R, 2, XPW, false, true>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm,
-                               (int64_t)0, 1);
+                               (int64_t)0);
         else
             return hipErrorInvalidValue;
         return hipGetLastError();
@@ -441,7 +382,7 @@ hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16
     switch (TT) {
 #define AIPU_P(TV) \
     case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, XPW, COPY_ONLY>), grid, block, lds, st, W, N, nsb, x, y, yf, ntiles, nm, \
-                                (int64_t)0, 1); break;
+                                (int64_t)0); break;
         AIPU_P(1)
         AIPU_P(2)
         AIPU_P(3)
@@ -456,22 +397,21 @@ hipError_t run_p(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16
     return hipGetLastError();
 }
 
-// MRV activation rows (K <= 6144: one block pair per compute wave), at most four tiles per
-// workgroup; rows past mrows read as zero and are not stored.
-template <int R, int MRV>
-hipError_t run_pm(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, int mrows, uint16_t* y, float* yf,
-                  int64_t ys, int TT, int G, int ntiles, int ncw, size_t lds, hipStream_t st) {
+// Two activation rows (K <= 6144: one block pair per compute wave), at most four tiles per workgroup.
+template <int R>
+hipError_t run_p2(const uint8_t* W, int64_t N, int nsb, const uint16_t* x, uint16_t* y, float* yf, int64_t ys, int TT,
+                  int G, int ntiles, int ncw, size_t lds, hipStream_t st) {
     const dim3 grid(G), block(64 * (ncw + 1));
     const NormIn nm{nullptr, 0u, nullptr};
     switch (TT) {
-#define AIPU_PM(TV) \
-    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, 1, false, false, MRV>), grid, block, lds, st, W, N, nsb, x, y, yf, \
-                                ntiles, nm, ys, mrows); break;
-        AIPU_PM(1)
-        AIPU_PM(2)
-        AIPU_PM(3)
-        AIPU_PM(4)
-#undef AIPU_PM
+#define AIPU_P2(TV) \
+    case TV: hipLaunchKernelGGL((k_gemv1p<R, TV, 1, false, false, 2>), grid, block, lds, st, W, N, nsb, x, y, yf, \
+                                ntiles, nm, ys); break;
+        AIPU_P2(1)
+        AIPU_P2(2)
+        AIPU_P2(3)
+        AIPU_P2(4)
+#undef AIPU_P2
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -562,31 +502,24 @@ hipError_t launch_gemv_persist_norm(const uint8_t* W, int64_t N, int64_t K, cons
     }
 }
 
-bool gemv_persist_rows_supported(int64_t N, int64_t K, int64_t M) {
-    if (M < 2 || M > 4 || !gemv_persist_supported(N, K) || K > 6144) return false;
+bool gemv_persist2_supported(int64_t N, int64_t K) {
+    if (!gemv_persist_supported(N, K) || K > 6144) return false;
     return p_plan(N, K).TT <= 4;
 }
 
-// Rows 0 .. M-1 (2 <= M <= 4) of x (row stride K) in one launch; row m of y at y + m * ys.  Each
-// row is formed exactly as the one-row launch forms it (the same sets, block sums, pair sums
-// and tree); three rows run with a zero fourth.
-hipError_t launch_gemv_persist_rows(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
-                                    float* yf, int64_t ys, hipStream_t st) {
-    if (!gemv_persist_rows_supported(N, K, M)) return hipErrorInvalidValue;
+// Rows 0 and 1 of x (row stride K) in one launch; row m of y at y + m * ys.  Each row is formed
+// exactly as the one-row launch forms it (the same sets, block sums, pair sums and tree).
+hipError_t launch_gemv_persist2(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
+                                int64_t ys, hipStream_t st) {
+    if (!gemv_persist2_supported(N, K)) return hipErrorInvalidValue;
     const PPlan q = p_plan(N, K);
-    const int mr = (int)M;
-#define AIPU_PR(RV)                                                                                         \
-    case RV:                                                                                                \
-        return M == 2 ? run_pm<RV, 2>(W, N, q.nsb, x, mr, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st) \
-                      : run_pm<RV, 4>(W, N, q.nsb, x, mr, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
     switch (q.R) {
-        AIPU_PR(1)
-        AIPU_PR(2)
-        AIPU_PR(3)
-        AIPU_PR(4)
+        case 1: return run_p2<1>(W, N, q.nsb, x, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
+        case 2: return run_p2<2>(W, N, q.nsb, x, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
+        case 3: return run_p2<3>(W, N, q.nsb, x, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
+        case 4: return run_p2<4>(W, N, q.nsb, x, y, yf, ys, q.TT, q.G, q.ntiles, q.ncw, q.lds, st);
         default: return hipErrorInvalidValue;
     }
-#undef AIPU_PR
 }
 
 // Whether a bounded wait in this file's kernels gave up since the last call (then cleared).

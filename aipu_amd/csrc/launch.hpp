@@ -62,11 +62,11 @@ hipError_t launch_gemv_persist(const uint8_t* W, int64_t N, int64_t K, const uin
 // and x_norm receives the normalised x (bit-identical to launch_rmsnorm's fast mode followed by
 // the GEMV).  x, gamma and x_norm 16-B aligned; at most two 8-row tiles per CU.
 bool gemv_persist_norm_supported(int64_t N, int64_t K);
-// Two to four activation rows (x row stride K, y row stride ys) in one launch of the same
-// kernel, each row bit-identical to its one-row launch (K <= 6144, at most four 8-row tiles per CU).
-bool gemv_persist_rows_supported(int64_t N, int64_t K, int64_t M);
-hipError_t launch_gemv_persist_rows(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, int64_t M, uint16_t* y,
-                                    float* yf, int64_t ys, hipStream_t st);
+// Two activation rows (x row stride K, y row stride ys) in one launch of the same kernel, each
+// row bit-identical to its one-row launch (K <= 6144, at most four 8-row tiles per CU).
+bool gemv_persist2_supported(int64_t N, int64_t K);
+hipError_t launch_gemv_persist2(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, uint16_t* y, float* yf,
+                                int64_t ys, hipStream_t st);
 hipError_t launch_gemv_persist_norm(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x, const uint16_t* gamma,
                                     uint32_t inv_len_bits, uint16_t* x_norm, uint16_t* y, hipStream_t st);
 

@@ -239,9 +239,9 @@ INVARIANCE_CASES = [(6144, 6144, m) for m in (2, 3, 4, 5, 6, 7, 8)] + [
     # K > 8192: the one-row kernel is k_gemv1 (several weight-copy rounds); beyond the
     # matrix-core staging limit (K > 30464) every M runs the streaming kernel
     (64, 9216, 3), (40, 12288, 5), (64, 18432, 8), (16, 32768, 3),
-    # two to four rows on the persistent one-row kernel (the M = 2..4 cases above run there
-    # too): an odd block count (a half last pair), a ragged last tile, four tiles per CU, one
-    # tile too many for it, a single block
+    # two rows on the persistent one-row kernel (the M = 2 cases above run there too): an odd
+    # block count (a half last pair), a ragged last tile, four tiles per CU, one tile too many
+    # for it, a single block
     (100, 2304, 2), (6100, 6144, 2), (8192, 6144, 2), (8200, 4096, 2), (1, 256, 2)]
 
 
