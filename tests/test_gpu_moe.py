@@ -457,6 +457,65 @@ def test_mixed_tiles_ragged_fast():
     assert np.all(got_y[~covered] == qo.bf16_round_bits(np.float32(7.0)))
 
 
+def _ragged_spec(rng, n_tiles, K):
+    """Tiles of every type with uneven row counts, out of order, leaving gaps of uncovered rows."""
+    kinds = [Q4K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16, BF16]
+    spec, r0 = [], 0
+    for i in range(n_tiles):
+        n = int(rng.integers(1, 300)) if i % 5 else int(rng.integers(1, 12))
+        spec.append((kinds[i % 5], r0, n))
+        r0 += n + int(rng.integers(0, 3))
+    order = rng.permutation(n_tiles)
+    return [spec[i] for i in order], r0
+
+
+# Full-size one-row launches against the rows of a two-row batch (one weight pass for both):
+# every row must equal its one-row launch bit for bit.  Shapes: C3 (K = 6144), one type over
+# all rows at K = 4096 / 2048 / 1024 (four, two and one block per wave, so the last group of a
+# Q4_K wave covers blocks past its part), and 40 ragged tiles of all five types, out of order
+# and with gaps of uncovered rows, at K = 5120 (five blocks per wave).
+LARGE_ONE_ROW_CASES = [("c3", 6144, None), ("q6k", 4096, [(qo.GGML_Q6_K, 0, 4096)]),
+              ("q8_0", 2048, [(qo.GGML_Q8_0, 0, 4200)]), ("f16", 1024, [(qo.GGML_F16, 0, 4100)]),
+              ("q4k", 4096, [(Q4K, 0, 4352)]), ("ragged", 5120, "ragged")]
+
+
+@pytest.mark.parametrize("name,K,spec", LARGE_ONE_ROW_CASES)
+def test_mixed_tiles_large_one_row(name, K, spec):
+    note(f"tiles fast large one-row {name} K={K}")
+    rng = np.random.default_rng(K + len(name))
+    if spec is None:
+        spec = [(t, i * 256, 256) for i, t in enumerate([Q4K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16] * 6)]
+        N = 6144
+    elif spec == "ragged":
+        spec, N = _ragged_spec(rng, 40, K)
+    else:
+        N = spec[0][2]
+    tw = [_tile_weights(rng, t, n, K) for t, _, n in spec]
+    tiles = [(t, d_u8(r), r0, n) for (t, r0, n), (r, _) in zip(spec, tw)]
+    x = qo.random_bf16(rng, (2, K))
+    y2, yf2 = dev.gemv_tiles(tiles, N, K, d_bf16(x), mode="fast", out_f32=True)
+    y = torch.full((1, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    yf = torch.full((1, N), -3.0, dtype=torch.float32, device="cuda")
+    covered = np.zeros(N, bool)
+    for _, r0, n in spec:
+        covered[r0:r0 + n] = True
+    for r in range(2):
+        dev.gemv_tiles(tiles, N, K, d_bf16(x[r:r + 1]), mode="fast", out=y, out_f32=yf)
+        got_f, got_y = u32(h_f32(yf))[0], h_bits(y)[0]
+        assert_bits_equal(got_f[covered], u32(h_f32(yf2))[r][covered], f"row {r}: fp32 accumulators vs the batch")
+        assert_bits_equal(got_y[covered], h_bits(y2)[r][covered], f"row {r}: bf16 outputs vs the batch")
+        assert np.all(h_f32(yf)[0][~covered] == np.float32(-3.0)), "rows outside the tiles written"
+        assert np.all(got_y[~covered] == qo.bf16_round_bits(np.float32(7.0))), "rows outside the tiles written"
+    if name == "c3":
+        return   # the oracle comparison at this size: test_mixed_tiles_c3_full_shape
+    xf = qo.bf16_bits_to_f32(x[1:])
+    for (t, r0, n), (r, wdq) in zip(spec, tw):
+        acc, _ = co.gemv_ref(t, r, n, K, x[1:])
+        ok, worst = qo.tolerance_gate(wdq, xf, h_f32(yf)[:, r0:r0 + n])
+        assert ok, (name, t, r0, n, worst)
+        assert qo.bf16_parity(h_bits(y)[:, r0:r0 + n], acc, wdq, xf)[0], (name, t, r0, n)
+
+
 
 def _tile_weights(rng, t, rows, K):
     """(raw bytes, dequantised float32[rows, K]) of a tile; BF16 tiles hold N(0, 0.05^2) bf16."""
