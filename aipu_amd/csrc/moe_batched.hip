@@ -191,6 +191,7 @@ __global__ void k_union_silu(const uint16_t* __restrict__ gu, const int32_t* __r
 
 // out[m][d] = bf16(facc), facc over the routed union slots in ascending expert index (only
 // the row's own experts), then the shared slot with weight 1; resid (nullable) added after.
+constexpr int kCombineChunk = 16;   // a two-row pass of top-8 routing has at most 16 union slots
 __global__ void k_union_combine(const uint16_t* __restrict__ y, const uint32_t* __restrict__ ugate,
                                 const int32_t* __restrict__ nslots, int shared, int M, int64_t H, int ms,
                                 const uint16_t* __restrict__ resid, int64_t rstride, uint16_t* __restrict__ out,
@@ -202,11 +203,22 @@ __global__ void k_union_combine(const uint16_t* __restrict__ y, const uint32_t* 
         const int m = (int)(j / H);
         const int64_t d = j - (int64_t)m * H;
         float facc = 0.0f;
-        for (int u = 0; u < nu; ++u) {
-            const uint32_t g = ugate[m * ms + u];
-            if (g == kInactive) continue;
-            const float p = __uint_as_float(g) * bf16_to_f32(y[((int64_t)u * M + m) * H + d]);
-            facc = facc + p;
+        // the gates and outputs of up to kCombineChunk slots are loaded before their adds, so one
+        // memory round trip serves them (slots past the union reread the last one, unused)
+        for (int u0 = 0; u0 < nu; u0 += kCombineChunk) {
+            uint32_t g[kCombineChunk], yv[kCombineChunk];
+#pragma unroll
+            for (int k = 0; k < kCombineChunk; ++k) {
+                const int u = u0 + k < nu ? u0 + k : nu - 1;
+                g[k] = ugate[m * ms + u];
+                yv[k] = y[((int64_t)u * M + m) * H + d];
+            }
+#pragma unroll
+            for (int k = 0; k < kCombineChunk; ++k) {
+                if (u0 + k >= nu || g[k] == kInactive) continue;
+                const float p = __uint_as_float(g[k]) * bf16_to_f32(yv[k]);
+                facc = facc + p;
+            }
         }
         if (shared) facc = facc + bf16_to_f32(y[((int64_t)nu * M + m) * H + d]);
         uint32_t o = bf16_rne(facc);
