@@ -156,6 +156,102 @@ __device__ __forceinline__ float set_sum(const u32x4_t (&A)[8], float2 as, const
     return bt + b1;
 }
 
+// ---------------------------------------------- fp16 high-nibble operands (gate/up leg)
+// The gate/up leg builds the high-nibble codes as fp16 1024 + 16 q = (x & 0x00F0) | 0x6400, which
+// needs no shift (the low-nibble codes stay bf16 128 + q). Their MFMAs take the pair's
+// activations as fp16 scaled by 2^-e, e putting the pair's largest magnitude in [2^14, 2^15):
+// every bf16 value down to 2^-24 of it converts exactly, and a' (1024 + 16 q) is exact in fp32.
+// Seeded with -1024 * 2^-e * sum a, the chain ends at 16 * 2^-e * sum a q, which 2^(e - 4) scales
+// back exactly. This leg's order is its own (compared with exact arithmetic within the MoE bound).
+struct CodeKH {
+    uint32_t mask;   // wave-uniform (SGPR)
+    uint32_t bias;   // VGPR
+};
+
+__device__ __forceinline__ CodeKH code_kh() {
+    CodeKH k;
+    k.mask = 0x00F000F0u;
+    k.bias = 0x64006400u;   // fp16 1024.0 in both halves
+    asm volatile("" : "+s"(k.mask));
+    asm volatile("" : "+v"(k.bias));
+    return k;
+}
+
+// The high-nibble B operands of codes_hi in the same element places, as fp16 1024 + 16 q.
+__device__ __forceinline__ u32x4_t codes_hi16(uint32_t x0, uint32_t x1, const CodeKH& k) {
+    return u32x4_t{(x0 & k.mask) | k.bias, ((x0 >> 8) & k.mask) | k.bias, (x1 & k.mask) | k.bias,
+                   ((x1 >> 8) & k.mask) | k.bias};
+}
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+                                                  0, 0);
+}
+
+// The exponent e of a pair (64 lanes of 8 bf16) for its fp16 operands; 0 for an all-zero pair or
+// one holding inf / nan.
+__device__ __forceinline__ int pair_exponent(const uint4& xv) {
+    const uint32_t v[4] = {xv.x, xv.y, xv.z, xv.w};
+    uint32_t mx = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mx = max(mx, max(v[k] & 0x7FFFu, (v[k] >> 16) & 0x7FFFu));
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, s, 64));
+    if (mx == 0 || mx >= 0x7F80u) return 0;
+    int ex;
+    (void)frexpf(bf16_to_f32(mx), &ex);   // max = f * 2^ex, f in [0.5, 1)
+    return ex - 15;
+}
+
+// Two bf16 (one dword) times 2^-e as an fp16 pair, round to nearest even.
+__device__ __forceinline__ uint32_t f16_pair_scaled(uint32_t w, int e) {
+    const float lo = __builtin_ldexpf(__uint_as_float(w << 16), -e);
+    const float hi = __builtin_ldexpf(__uint_as_float(w & 0xFFFF0000u), -e);
+    return (uint32_t)__half_as_ushort(__float2half_rn(lo)) | ((uint32_t)__half_as_ushort(__float2half_rn(hi)) << 16);
+}
+
+// x pair pr into registers as x_operands does, the high-nibble operands (MFMAs t >= 4) as fp16
+// scaled by 2^-e; the sub-block sums stay those of the bf16 values.
+__device__ __forceinline__ void x_operands16(const uint4& xv, uint8_t* st, int lane, int e, u32x4_t (&A)[8],
+                                             float2& as) {
+    const int n = lane & 15, g = lane >> 4, h = n >> 3;
+    stage_pair(xv, st, lane);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if ((lane & 7) >= 4) {   // chunk t = lane & 7 of the pair: rewrite its entry in fp16
+        const uint4 hv = make_uint4(f16_pair_scaled(xv.x, e), f16_pair_scaled(xv.y, e), f16_pair_scaled(xv.z, e),
+                                    f16_pair_scaled(xv.w, e));
+        const int L = lane, hh = L >> 5, gg = (L >> 3) & 3, t = L & 7;
+        *(u32x4_t*)(st + 16u * (uint32_t)(9 * t + 2 * gg + hh)) = act_perm(hv);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) A[i] = u32x4_t{0u, 0u, 0u, 0u};
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    pair_operands(lds_addr(st), g, n, h, A, as);
+}
+
+// set_sum with the high-nibble chain on fp16 operands: seeded with seed_hi = -1024 * 2^-e * as.y,
+// its sum scaled by hscale = 2^(e - 4) before the block term.
+__device__ __forceinline__ float set_sum16(const u32x4_t (&A)[8], float2 as, float seed_hi, float hscale,
+                                           const u32x4_t& hv, const u32x4_t& q0, const u32x4_t& q1, const HdrSel& hs,
+                                           const CodeK& ck, const CodeKH& kh, int h) {
+    f32x4_t dlo, dhi;
+    dlo[0] = dlo[1] = -kCodeBiasF * as.x;
+    dhi[0] = dhi[1] = seed_hi;
+    dlo[2] = dlo[3] = dhi[2] = dhi[3] = 0.f;
+    const uint32_t qd[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+        dlo = mfma(A[tt], codes_lo(qd[2 * tt], qd[2 * tt + 1], ck), dlo);
+        dhi = mfma16(A[4 + tt], codes_hi16(qd[2 * tt], qd[2 * tt + 1], kh), dhi);
+    }
+    const Hdr H = hdr_decode(make_uint4(hv.x, hv.y, hv.z, hv.w), hs);
+    const float shi = (h ? dhi[1] : dhi[0]) * hscale;
+    const float bt = block_sum(block_term(H, h ? dlo[1] : dlo[0], shi, as.x, as.y));
+    const float b1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bt), 0x108, 0xF, 0xF, false));
+    return bt + b1;
+}
+
 // ------------------------------------------------------------------ job loops
 // LDS of a workgroup's ring: slots, per-round landed / read counters, per-job set counters,
 // per-job pair sums.
@@ -241,8 +337,9 @@ __device__ __forceinline__ int slot_experts(const uint32_t* win, int topk, int E
 // job t's rounds are u0 + 2R t + half R + gam; the job's last set forms its 8 h values.
 template <int R, int NS>
 __device__ __forceinline__ void gu_jobs(const Ring& rg, int T, int u0, int wg, int G, int it8, int I, int gam, int p,
-                                        const u32x4_t (&A)[8], float2 as, const HdrSel& hs, const CodeK& ck,
-                                        int& seen, uint16_t* __restrict__ Hout, int lane) {
+                                        const u32x4_t (&A)[8], float2 as, float seed_hi, float hscale,
+                                        const HdrSel& hs, const CodeK& ck, const CodeKH& kh, int& seen,
+                                        uint16_t* __restrict__ Hout, int lane) {
     constexpr int RJ = 2 * R, np = 4 * R;
     const int n = lane & 15, g = lane >> 4, h = n >> 3, r = n & 7;
     const int pr = 4 * gam + p;
@@ -256,7 +353,7 @@ __device__ __forceinline__ void gu_jobs(const Ring& rg, int T, int u0, int wg, i
                         hv, q0, q1);
             seen = seen < u ? u : seen;
             lds_post(&rg.read[u]);   // the weights are in registers: one reader fewer
-            const float ps = set_sum(A, as, hv, q0, q1, hs, ck, h);
+            const float ps = set_sum16(A, as, seed_hi, hscale, hv, q0, q1, hs, ck, kh, h);
             if (lane < kJR) rt[(half * kJR + lane) * kGuNp + pr] = ps;
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // pair sums written before the count
@@ -430,9 +527,12 @@ __global__ __launch_bounds__(64 * (kNCW + CW)) void k_moe_gu_p(Stack Gs, Stack U
     // ---- compute wave (gam, p): pair pr of x, operands in registers
     u32x4_t A[8];
     float2 as;
-    x_operands(xv, s_stage + (uint32_t)pr * kStgBytes, lane, A, as);
+    const int e = pair_exponent(xv);
+    x_operands16(xv, s_stage + (uint32_t)pr * kStgBytes, lane, e, A, as);
+    const float seed_hi = -1024.0f * __builtin_ldexpf(as.y, -e), hscale = __builtin_ldexpf(1.0f, e - 4);
     int seen = -1;
-    gu_jobs<R, NS>(rg, T, 0, wg, G, it8, I, gam, p, A, as, hdr_sel(lane >> 4), code_k(), seen, Hout, lane);
+    gu_jobs<R, NS>(rg, T, 0, wg, G, it8, I, gam, p, A, as, seed_hi, hscale, hdr_sel(lane >> 4), code_k(), code_kh(),
+                   seen, Hout, lane);
 }
 
 // ------------------------------------------------------------------ down
