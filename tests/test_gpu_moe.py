@@ -318,6 +318,32 @@ def test_moe_fast_persistent_legs(H, E, topk, shared):
     _check_moe_tight(yb, hw, x, sub, sh, ew, H, I)
 
 
+# The gate/up leg multiplies the high-nibble codes with each activation pair scaled by 2^-e in
+# fp16 (e puts the pair's largest magnitude in [2^14, 2^15)).  Activations far below and above 1,
+# a vector whose elements span 2^-40..2^40 inside every pair, and one all-zero pair beside
+# ordinary ones must still meet the routing contract and the two-stage bound.
+@pytest.mark.parametrize("case", ["small", "large", "span", "zero_pair"])
+def test_moe_fast_persistent_activation_range(case):
+    H, E, topk = 2048, 16, 2
+    note(f"moe persistent activation range {case}")
+    I, (ge, ue, de), rw, x = _moe_persistent_case(H, E, topk, 7000 + len(case))
+    rng = np.random.default_rng(7100 + len(case))
+    xf = qo.bf16_bits_to_f32(x).astype(np.float32)
+    if case == "small":
+        xf *= np.float32(2.0 ** -30)
+    elif case == "large":
+        xf *= np.float32(2.0 ** 30)
+    elif case == "span":
+        xf *= np.exp2(rng.integers(-40, 41, H)).astype(np.float32)
+    else:
+        xf[512:1024] = 0.0
+    x = qo.bf16_round_bits(xf)
+    yb, sel, sw, lg, hw = _fast_step(BF16, rw, (ge, ue, de), E, H, I, topk, x)
+    es, ew = _check_routing(BF16, rw, E, H, x, topk, sel, sw, lg)
+    sub = tuple(_expert_rows(t, E, es).reshape(topk, -1) for t in (ge, ue, de))
+    _check_moe_tight(yb, hw, x, sub, None, ew, H, I)
+
+
 def test_moe_persistent_detects_corrupted_expert():
     """Must-fail twin on the persistent legs: d of every block of the first routed expert's down
     matrix 10 % larger (a small error in one slot of the down leg) fails the two-stage bound;
