@@ -188,6 +188,128 @@ __global__ __launch_bounds__(kRows) void k_gemv_ref(const uint8_t* __restrict__ 
     }
 }
 
+// Q4_K in reference order with the weights in registers: the same operations in the same order
+// as k_gemv_ref<T_Q4_K> (so the same bits), arranged for the VALU.  Lane = output row; each
+// lane loads its row's 144-B super-block with nine 16-B loads, one block ahead of its use, and
+// the MC activation rows of the pass sit in LDS as fp32 (staged once, MC * K * 4 bytes), read
+// four at a time by every lane of the wave at one address.  Per weight: the nibble, its fp32
+// value (one byte conversion), w = D q - Mn, and for every activation row acc += x w.
+constexpr int kRefQ4LdsBytes = 128 * 1024;   // staged activations, at most
+
+// Byte B of v as fp32 in one instruction (plain C selects a bit-field extract, then the
+// conversion of byte 0).  VALU only, no hazard beyond what the hardware interlocks.
+template <int B>
+__device__ __forceinline__ float cvt_ubyte(uint32_t v) {
+    float r;
+    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+template <int MC>
+__global__ __launch_bounds__(kRows) void k_gemv_ref_q4k(const uint8_t* __restrict__ W, int64_t N, int64_t K,
+                                                        const uint16_t* __restrict__ X, int64_t M,
+                                                        uint16_t* __restrict__ Y, float* __restrict__ Yf,
+                                                        RefGather ga) {
+    if (ga.sel) {
+        const int z = blockIdx.z;
+        if (z < ga.topk) {
+            int e = ga.sel[z];
+            e = e < 0 ? 0 : (e >= ga.E ? (int)ga.E - 1 : e);
+            W += (int64_t)e * ga.wstride;
+        } else {
+            W = ga.W_alt;
+        }
+        X += (int64_t)z * ga.x_zstride;
+        Y += (int64_t)z * ga.y_zstride;
+        if (Yf) Yf += (int64_t)z * ga.y_zstride;
+    }
+    extern __shared__ __align__(16) float s_x[];   // [MC][K]
+    const int lane = threadIdx.x;
+    const int64_t row0 = (int64_t)blockIdx.x * kRows;
+    const int64_t m0 = (int64_t)blockIdx.y * MC;
+    const int mcnt = (int)((M - m0) < MC ? (M - m0) : MC);
+    const int nsb = (int)(K / QK_K);
+    const uint32_t rb = (uint32_t)nsb * 144u;
+    const int nrows = (int)((N - row0) < kRows ? (N - row0) : kRows);
+    // this lane's row (rows past N read zeros), one block ahead
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W + row0 * (int64_t)rb, (uint32_t)nrows * rb);
+    const uint32_t wrow = (uint32_t)lane * rb;
+    uint4 nxt[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) nxt[i] = buf_load16(wr, wrow + 16u * (uint32_t)i);
+    // the pass's activation rows as fp32 (rows past M as zeros)
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X + m0 * K, (uint32_t)mcnt * (uint32_t)K * 2u);
+    for (int c = lane; c < MC * (int)(K / 8); c += kRows) {
+        const int mm = c / (int)(K / 8), kk = 8 * (c - mm * (int)(K / 8));
+        const uint4 v = buf_load16(xr, mm < mcnt ? 2u * (uint32_t)(mm * K + kk) : 0xF0000000u);
+        float4* d = (float4*)(s_x + (int64_t)mm * K + kk);
+        d[0] = make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
+                           bf16_to_f32(v.y >> 16));
+        d[1] = make_float4(bf16_to_f32(v.z & 0xFFFFu), bf16_to_f32(v.z >> 16), bf16_to_f32(v.w & 0xFFFFu),
+                           bf16_to_f32(v.w >> 16));
+    }
+    __syncthreads();
+    float acc[MC];
+#pragma unroll
+    for (int i = 0; i < MC; ++i) acc[i] = 0.0f;
+    for (int b = 0; b < nsb; ++b) {
+        uint4 R[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) R[i] = nxt[i];
+        if (b + 1 < nsb) {
+#pragma unroll
+            for (int i = 0; i < 9; ++i) nxt[i] = buf_load16(wr, wrow + 144u * (uint32_t)(b + 1) + 16u * (uint32_t)i);
+        }
+        // tools/q4k_ref.py:45-60: d, dmin, the packed scales, then the 128 bytes of nibbles
+        const float d = f16_to_f32(R[0].x & 0xFFFFu);
+        const float dm = f16_to_f32(R[0].x >> 16);
+        const uint32_t s0 = R[0].y, s1 = R[0].z, s2 = R[0].w;
+        const uint32_t qd[32] = {R[1].x, R[1].y, R[1].z, R[1].w, R[2].x, R[2].y, R[2].z, R[2].w,
+                                 R[3].x, R[3].y, R[3].z, R[3].w, R[4].x, R[4].y, R[4].z, R[4].w,
+                                 R[5].x, R[5].y, R[5].z, R[5].w, R[6].x, R[6].y, R[6].z, R[6].w,
+                                 R[7].x, R[7].y, R[7].z, R[7].w, R[8].x, R[8].y, R[8].z, R[8].w};
+        const float* xb = s_x + (int64_t)b * QK_K;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t sc, mn;
+            q4k_scale_min(j, s0, s1, s2, sc, mn);
+            const float D = d * (float)sc;
+            const float Mn = dm * (float)mn;
+            const int g = j >> 1, hi = j & 1;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {   // bytes 4c .. 4c + 3 of the 32 of sub-block pair g
+                const uint32_t v = (hi ? qd[8 * g + c] >> 4 : qd[8 * g + c]) & 0x0F0F0F0Fu;
+                const float q[4] = {cvt_ubyte<0>(v), cvt_ubyte<1>(v), cvt_ubyte<2>(v), cvt_ubyte<3>(v)};
+                const int k = 32 * j + 4 * c;
+                float4 xv[MC];
+#pragma unroll
+                for (int mm = 0; mm < MC; ++mm) xv[mm] = *(const float4*)(xb + (int64_t)mm * K + k);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float wq = D * q[e];   // q4k_weight_exact: D * q, then - Mn
+                    const float we = wq - Mn;
+#pragma unroll
+                    for (int mm = 0; mm < MC; ++mm) {
+                        const float xe = e == 0 ? xv[mm].x : e == 1 ? xv[mm].y : e == 2 ? xv[mm].z : xv[mm].w;
+                        const float p = xe * we;
+                        acc[mm] = acc[mm] + p;
+                    }
+                }
+            }
+        }
+    }
+    const int64_t n = row0 + lane;
+    if (n < N) {
+        for (int mm = 0; mm < mcnt; ++mm) {
+            Y[(m0 + mm) * N + n] = (uint16_t)bf16_rne(acc[mm]);
+            if (Yf) Yf[(m0 + mm) * N + n] = acc[mm];
+        }
+    }
+}
+
 // Reference order on already-dequantised fp32 weights (matmul_q4k_col on a wdeq column).
 __global__ __launch_bounds__(kRows) void k_gemv_ref_f32(const float* __restrict__ W, int64_t N, int64_t K,
                                                         const float* __restrict__ X, int64_t M,
@@ -234,9 +356,23 @@ hipError_t launch_gemv_ref_gather(int type, const void* w, int64_t N, int64_t K,
                                   uint16_t* y, float* y_f32, int nslots, const int32_t* sel, int topk, int64_t E,
                                   int64_t wstride, const void* w_alt, int64_t x_zstride, int64_t y_zstride,
                                   hipStream_t st) {
-    const dim3 grid((unsigned)((N + kRows - 1) / kRows), (unsigned)((M + kMC - 1) / kMC), (unsigned)nslots);
     const uint8_t* W = (const uint8_t*)w;
     const RefGather ga{sel, topk, E, wstride, (const uint8_t*)w_alt, x_zstride, y_zstride};
+    if (type == T_Q4_K && K % QK_K == 0 && K * 4 <= kRefQ4LdsBytes) {
+        // the register kernel: MC activation rows per pass, as many as the staged rows allow
+        int mc = 8;
+        while (mc > 1 && (mc / 2 >= M || (int64_t)mc * K * 4 > kRefQ4LdsBytes)) mc /= 2;
+        const dim3 g4((unsigned)((N + kRows - 1) / kRows), (unsigned)((M + mc - 1) / mc), (unsigned)nslots);
+        const size_t lds = (size_t)mc * (size_t)K * 4;
+        switch (mc) {
+            case 8: hipLaunchKernelGGL(k_gemv_ref_q4k<8>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
+            case 4: hipLaunchKernelGGL(k_gemv_ref_q4k<4>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
+            case 2: hipLaunchKernelGGL(k_gemv_ref_q4k<2>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
+            default: hipLaunchKernelGGL(k_gemv_ref_q4k<1>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
+        }
+        return hipGetLastError();
+    }
+    const dim3 grid((unsigned)((N + kRows - 1) / kRows), (unsigned)((M + kMC - 1) / kMC), (unsigned)nslots);
     switch (type) {
         case T_Q4_K: hipLaunchKernelGGL(k_gemv_ref<T_Q4_K>, grid, dim3(kRows), 0, st, W, N, K, x, M, y, y_f32, ga); break;
         case T_Q6_K: hipLaunchKernelGGL(k_gemv_ref<T_Q6_K>, grid, dim3(kRows), 0, st, W, N, K, x, M, y, y_f32, ga); break;

@@ -102,8 +102,14 @@ def test_fp32_rsqrt_golden():
 
 
 # ------------------------------------------------------- reference-order GEMV
+# Q4_K runs on the register kernel (k_gemv_ref_q4k) while K * 4 bytes of staged activations fit
+# 128 KB, in passes of up to 8, 4, 2 or 1 rows as the staging allows: 9 rows at K = 256 (8 + 1),
+# 8 at K = 6144 (two passes of 4), 5 at K = 8192 (4 + 1), 2 at K = 32768 (one row per pass);
+# K = 40960 takes the staged-weights kernel.  Ragged N leaves part of the last wave idle.
 REF_CASES = [
     (qo.GGML_Q4_K, 200, 768, 1), (qo.GGML_Q4_K, 131, 512, 3), (qo.GGML_Q4_K, 64, 256, 9),
+    (qo.GGML_Q4_K, 130, 6144, 8), (qo.GGML_Q4_K, 33, 8192, 5), (qo.GGML_Q4_K, 70, 32768, 2),
+    (qo.GGML_Q4_K, 64, 40960, 1),
     (qo.GGML_Q6_K, 96, 512, 2), (qo.GGML_Q8_0, 70, 512, 1), (qo.GGML_F16, 65, 256, 2), (30, 64, 512, 1),
 ]
 
