@@ -240,16 +240,28 @@ __global__ __launch_bounds__(kRows) void k_gemv_ref_q4k(const uint8_t* __restric
     uint4 nxt[9];
 #pragma unroll
     for (int i = 0; i < 9; ++i) nxt[i] = buf_load16(wr, wrow + 16u * (uint32_t)i);
-    // the pass's activation rows as fp32 (rows past M as zeros)
+    // the pass's activation rows as fp32 (rows past M as zeros): chunks of 8 elements, eight
+    // chunks' loads in flight before their stores
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X + m0 * K, (uint32_t)mcnt * (uint32_t)K * 2u);
-    for (int c = lane; c < MC * (int)(K / 8); c += kRows) {
-        const int mm = c / (int)(K / 8), kk = 8 * (c - mm * (int)(K / 8));
-        const uint4 v = buf_load16(xr, mm < mcnt ? 2u * (uint32_t)(mm * K + kk) : 0xF0000000u);
-        float4* d = (float4*)(s_x + (int64_t)mm * K + kk);
-        d[0] = make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
-                           bf16_to_f32(v.y >> 16));
-        d[1] = make_float4(bf16_to_f32(v.z & 0xFFFFu), bf16_to_f32(v.z >> 16), bf16_to_f32(v.w & 0xFFFFu),
-                           bf16_to_f32(v.w >> 16));
+    const int nch = MC * (int)(K / 8);
+    for (int c0 = 0; c0 < nch; c0 += 8 * kRows) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + u * kRows + lane;
+            v[u] = buf_load16(xr, c < nch ? 16u * (uint32_t)c : 0xF0000000u);   // chunk c: row c / (K / 8)
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + u * kRows + lane;
+            if (c < nch) {
+                float4* d = (float4*)(s_x + 8 * (int64_t)c);
+                d[0] = make_float4(bf16_to_f32(v[u].x & 0xFFFFu), bf16_to_f32(v[u].x >> 16),
+                                   bf16_to_f32(v[u].y & 0xFFFFu), bf16_to_f32(v[u].y >> 16));
+                d[1] = make_float4(bf16_to_f32(v[u].z & 0xFFFFu), bf16_to_f32(v[u].z >> 16),
+                                   bf16_to_f32(v[u].w & 0xFFFFu), bf16_to_f32(v[u].w >> 16));
+            }
+        }
     }
     __syncthreads();
     float acc[MC];
