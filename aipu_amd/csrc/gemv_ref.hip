@@ -3,11 +3,13 @@
 // Contract (tools/q4k_ref.py:67-92, RTL order src/glm_matmul_q4k.v:261-270): for each
 // output (m, n) the weight row is dequantised exactly and
 //     acc = f32(acc + f32(x[m][k] * w[n][k]))     for k = 0 .. K-1, in order,
-// then y = bf16_RNE(acc).  One lane owns one output row and walks K sequentially; the
-// 64 rows of a workgroup are staged 256 weights at a time through LDS so the global
-// reads stay coalesced.  A last stage of fewer weights serves K that is a multiple of the
-// type's block but not of 256 (Q8_0: 32; F16 / BF16: any K).  The library is compiled with -ffp-contract=off, so the multiply
-// and the add below are two separately rounded ops.
+// then y = bf16_RNE(acc).  One lane owns one output row and walks K sequentially.  Q4_K with
+// K <= 32768 runs k_gemv_ref_q4k (row blocks in registers, activations staged once as fp32);
+// the other types and larger K run k_gemv_ref, whose 64 rows per workgroup are staged 256
+// weights at a time through LDS so the global reads stay coalesced, with a last stage of fewer
+// weights for K that is a multiple of the type's block but not of 256 (Q8_0: 32; F16 / BF16:
+// any K).  The library is compiled with -ffp-contract=off, so the multiply and the add below
+// are two separately rounded ops.
 #include "common.hpp"
 #include "launch.hpp"
 
