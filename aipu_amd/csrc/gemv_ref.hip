@@ -4,8 +4,9 @@
 // output (m, n) the weight row is dequantised exactly and
 //     acc = f32(acc + f32(x[m][k] * w[n][k]))     for k = 0 .. K-1, in order,
 // then y = bf16_RNE(acc).  One lane owns one output row and walks K sequentially.  Q4_K with
-// K <= 32768 runs k_gemv_ref_q4k (row blocks in registers, activations staged once as fp32);
-// the other types and larger K run k_gemv_ref, whose 64 rows per workgroup are staged 256
+// K <= 32768 runs k_gemv_ref_q4k (row blocks in registers, activations staged once as fp32),
+// Q8_0 / F16 / BF16 with K a multiple of 64 k_gemv_ref_reg (the same for their units), both
+// with aligned pointers; Q6_K, larger K and unaligned pointers run k_gemv_ref, whose 64 rows per workgroup are staged 256
 // weights at a time through LDS so the global reads stay coalesced, with a last stage of fewer
 // weights for K that is a multiple of the type's block but not of 256 (Q8_0: 32; F16 / BF16:
 // any K).  The library is compiled with -ffp-contract=off, so the multiply and the add below
@@ -324,6 +325,138 @@ __global__ __launch_bounds__(kRows) void k_gemv_ref_q4k(const uint8_t* __restric
     }
 }
 
+// Q8_0, F16 and BF16 in reference order with the weights in registers, as k_gemv_ref_q4k does
+// for Q4_K: the dequantisation of k_gemv_ref's stage_mac (so the same bits).  A unit is 64
+// weights: two Q8_0 blocks (68 B, 17 dwords: needs K % 64 == 0 so every unit starts 4-B
+// aligned) or 128 B of F16 / BF16 (needs K % 64 == 0 so rows start 16-B aligned).
+template <int TYPE>
+struct RegUnit {
+    static constexpr int kDw = TYPE == T_Q8_0 ? 17 : 32;   // dwords per unit
+    static constexpr int kBytes = 4 * kDw;
+};
+
+template <int TYPE, int MC>
+__global__ __launch_bounds__(kRows) void k_gemv_ref_reg(const uint8_t* __restrict__ W, int64_t N, int64_t K,
+                                                        const uint16_t* __restrict__ X, int64_t M,
+                                                        uint16_t* __restrict__ Y, float* __restrict__ Yf,
+                                                        RefGather ga) {
+    typedef RegUnit<TYPE> U;
+    if (ga.sel) {
+        const int z = blockIdx.z;
+        if (z < ga.topk) {
+            int e = ga.sel[z];
+            e = e < 0 ? 0 : (e >= ga.E ? (int)ga.E - 1 : e);
+            W += (int64_t)e * ga.wstride;
+        } else {
+            W = ga.W_alt;
+        }
+        X += (int64_t)z * ga.x_zstride;
+        Y += (int64_t)z * ga.y_zstride;
+        if (Yf) Yf += (int64_t)z * ga.y_zstride;
+    }
+    extern __shared__ __align__(16) float s_x[];   // [MC][K]
+    const int lane = threadIdx.x;
+    const int64_t row0 = (int64_t)blockIdx.x * kRows;
+    const int64_t m0 = (int64_t)blockIdx.y * MC;
+    const int mcnt = (int)((M - m0) < MC ? (M - m0) : MC);
+    const int nu = (int)(K / 64);
+    const uint32_t rb = (uint32_t)nu * (uint32_t)U::kBytes;
+    const int nrows = (int)((N - row0) < kRows ? (N - row0) : kRows);
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W + row0 * (int64_t)rb, (uint32_t)nrows * rb);
+    const uint32_t wrow = (uint32_t)lane * rb;
+    uint32_t nxt[U::kDw];
+    auto load_unit = [&](int u) {
+        const uint32_t o = wrow + (uint32_t)U::kBytes * (uint32_t)u;
+        if constexpr (TYPE == T_Q8_0) {
+#pragma unroll
+            for (int i = 0; i < U::kDw; ++i) nxt[i] = buf_load4(wr, o + 4u * (uint32_t)i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < U::kDw / 4; ++i) {
+                const uint4 v = buf_load16(wr, o + 16u * (uint32_t)i);
+                nxt[4 * i] = v.x;
+                nxt[4 * i + 1] = v.y;
+                nxt[4 * i + 2] = v.z;
+                nxt[4 * i + 3] = v.w;
+            }
+        }
+    };
+    load_unit(0);
+    // the pass's activation rows as fp32 (rows past M as zeros), eight loads in flight per lane
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X + m0 * K, (uint32_t)mcnt * (uint32_t)K * 2u);
+    const int nch = MC * (int)(K / 8);
+    for (int c0 = 0; c0 < nch; c0 += 8 * kRows) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + u * kRows + lane;
+            v[u] = buf_load16(xr, c < nch ? 16u * (uint32_t)c : 0xF0000000u);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + u * kRows + lane;
+            if (c < nch) {
+                float4* d = (float4*)(s_x + 8 * (int64_t)c);
+                d[0] = make_float4(bf16_to_f32(v[u].x & 0xFFFFu), bf16_to_f32(v[u].x >> 16),
+                                   bf16_to_f32(v[u].y & 0xFFFFu), bf16_to_f32(v[u].y >> 16));
+                d[1] = make_float4(bf16_to_f32(v[u].z & 0xFFFFu), bf16_to_f32(v[u].z >> 16),
+                                   bf16_to_f32(v[u].w & 0xFFFFu), bf16_to_f32(v[u].w >> 16));
+            }
+        }
+    }
+    __syncthreads();
+    float acc[MC];
+#pragma unroll
+    for (int i = 0; i < MC; ++i) acc[i] = 0.0f;
+    for (int u = 0; u < nu; ++u) {
+        uint32_t R[U::kDw];
+#pragma unroll
+        for (int i = 0; i < U::kDw; ++i) R[i] = nxt[i];
+        if (u + 1 < nu) load_unit(u + 1);
+        const float* xb = s_x + (int64_t)u * 64;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {   // weights 4c .. 4c + 3 of the unit
+            float w[4];
+            if constexpr (TYPE == T_Q8_0) {
+                // block c / 8: fp16 d at bytes 34 (c / 8), codes at bytes 34 (c / 8) + 2 + ..
+                const int blk = c >> 3, i0 = 4 * (c & 7);
+                const float d = f16_to_f32(blk == 0 ? (R[0] & 0xFFFFu) : (R[8] >> 16));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int byte = 34 * blk + 2 + i0 + e;   // byte of the unit
+                    const uint32_t q = (R[byte >> 2] >> (8 * (byte & 3))) & 0xFFu;
+                    w[e] = d * (float)(int8_t)q;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t h = (R[2 * c + (e >> 1)] >> (16 * (e & 1))) & 0xFFFFu;
+                    w[e] = TYPE == T_F16 ? f16_to_f32(h) : bf16_to_f32(h);
+                }
+            }
+            float4 xv[MC];
+#pragma unroll
+            for (int mm = 0; mm < MC; ++mm) xv[mm] = *(const float4*)(xb + (int64_t)mm * K + 4 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                for (int mm = 0; mm < MC; ++mm) {
+                    const float xe = e == 0 ? xv[mm].x : e == 1 ? xv[mm].y : e == 2 ? xv[mm].z : xv[mm].w;
+                    const float p = xe * w[e];
+                    acc[mm] = acc[mm] + p;
+                }
+            }
+        }
+    }
+    const int64_t n = row0 + lane;
+    if (n < N) {
+        for (int mm = 0; mm < mcnt; ++mm) {
+            Y[(m0 + mm) * N + n] = (uint16_t)bf16_rne(acc[mm]);
+            if (Yf) Yf[(m0 + mm) * N + n] = acc[mm];
+        }
+    }
+}
+
 // Reference order on already-dequantised fp32 weights (matmul_q4k_col on a wdeq column).
 __global__ __launch_bounds__(kRows) void k_gemv_ref_f32(const float* __restrict__ W, int64_t N, int64_t K,
                                                         const float* __restrict__ X, int64_t M,
@@ -372,7 +505,12 @@ hipError_t launch_gemv_ref_gather(int type, const void* w, int64_t N, int64_t K,
                                   hipStream_t st) {
     const uint8_t* W = (const uint8_t*)w;
     const RefGather ga{sel, topk, E, wstride, (const uint8_t*)w_alt, x_zstride, y_zstride};
-    if (type == T_Q4_K && K % QK_K == 0 && K * 4 <= kRefQ4LdsBytes) {
+    // the register kernels load 16 B of activations and whole dwords / 16 B of weights at a time:
+    // the pointers they start from must be aligned for that (the ABI asks less in this mode)
+    auto al = [](const void* p, uintptr_t a) { return p == nullptr || ((uintptr_t)p & (a - 1)) == 0; };
+    const uintptr_t wa = type == T_Q8_0 ? 4 : 16;
+    const bool reg_ok = al(x, 16) && al(w, wa) && al(w_alt, wa) && (x_zstride * 2) % 16 == 0 && wstride % (int64_t)wa == 0;
+    if (reg_ok && type == T_Q4_K && K % QK_K == 0 && K * 4 <= kRefQ4LdsBytes) {
         // the register kernel: MC activation rows per pass, as many as the staged rows allow
         int mc = 8;
         while (mc > 1 && (mc / 2 >= M || (int64_t)mc * K * 4 > kRefQ4LdsBytes)) mc /= 2;
@@ -384,6 +522,24 @@ hipError_t launch_gemv_ref_gather(int type, const void* w, int64_t N, int64_t K,
             case 2: hipLaunchKernelGGL(k_gemv_ref_q4k<2>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
             default: hipLaunchKernelGGL(k_gemv_ref_q4k<1>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
         }
+        return hipGetLastError();
+    }
+    if (reg_ok && (type == T_Q8_0 || type == T_F16 || type == T_BF16) && K % 64 == 0 && K * 4 <= kRefQ4LdsBytes) {
+        int mc = 8;
+        while (mc > 1 && (mc / 2 >= M || (int64_t)mc * K * 4 > kRefQ4LdsBytes)) mc /= 2;
+        const dim3 g4((unsigned)((N + kRows - 1) / kRows), (unsigned)((M + mc - 1) / mc), (unsigned)nslots);
+        const size_t lds = (size_t)mc * (size_t)K * 4;
+#define AIPU_REFREG(T)                                                                                                 \
+    switch (mc) {                                                                                                      \
+        case 8: hipLaunchKernelGGL((k_gemv_ref_reg<T, 8>), g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break; \
+        case 4: hipLaunchKernelGGL((k_gemv_ref_reg<T, 4>), g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break; \
+        case 2: hipLaunchKernelGGL((k_gemv_ref_reg<T, 2>), g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break; \
+        default: hipLaunchKernelGGL((k_gemv_ref_reg<T, 1>), g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break; \
+    }
+        if (type == T_Q8_0) { AIPU_REFREG(T_Q8_0) }
+        else if (type == T_F16) { AIPU_REFREG(T_F16) }
+        else { AIPU_REFREG(T_BF16) }
+#undef AIPU_REFREG
         return hipGetLastError();
     }
     const dim3 grid((unsigned)((N + kRows - 1) / kRows), (unsigned)((M + kMC - 1) / kMC), (unsigned)nslots);

@@ -105,11 +105,12 @@ def test_fp32_rsqrt_golden():
 # Q4_K runs on the register kernel (k_gemv_ref_q4k) while K * 4 bytes of staged activations fit
 # 128 KB, in passes of up to 8, 4, 2 or 1 rows as the staging allows: 9 rows at K = 256 (8 + 1),
 # 8 at K = 6144 (two passes of 4), 5 at K = 8192 (4 + 1), 2 at K = 32768 (one row per pass);
-# K = 40960 takes the staged-weights kernel.  Ragged N leaves part of the last wave idle.
+# K = 40960 takes the staged-weights kernel.  Q8_0, F16 and BF16 take their register kernel
+# (k_gemv_ref_reg) at K a multiple of 64.  Ragged N leaves part of the last wave idle.
 REF_CASES = [
     (qo.GGML_Q4_K, 200, 768, 1), (qo.GGML_Q4_K, 131, 512, 3), (qo.GGML_Q4_K, 64, 256, 9),
     (qo.GGML_Q4_K, 130, 6144, 8), (qo.GGML_Q4_K, 33, 8192, 5), (qo.GGML_Q4_K, 70, 32768, 2),
-    (qo.GGML_Q4_K, 64, 40960, 1),
+    (qo.GGML_Q4_K, 64, 40960, 1), (qo.GGML_Q8_0, 130, 6144, 8), (qo.GGML_F16, 70, 4096, 3), (30, 33, 8192, 5),
     (qo.GGML_Q6_K, 96, 512, 2), (qo.GGML_Q8_0, 70, 512, 1), (qo.GGML_F16, 65, 256, 2), (30, 64, 512, 1),
 ]
 
@@ -125,6 +126,25 @@ def test_gemv_ref_bitexact(t, N, K, M):
         acc, ye = qo.gemv_ref(qo.bf16_bits_to_f32(raw.view(np.uint16)).reshape(N, K), qo.bf16_bits_to_f32(x))
     else:
         acc, ye = co.gemv_ref(t, raw, N, K, x)
+    assert_bits_equal(u32(h_f32(yf)), u32(acc), "acc")
+    assert_bits_equal(h_bits(y), ye, "y")
+
+
+@pytest.mark.parametrize("t", [qo.GGML_Q4_K, qo.GGML_Q8_0, qo.GGML_F16])
+def test_gemv_ref_unaligned_activations(t):
+    """Reference mode asks only 2-byte aligned activations (and, below Q4_K, weights): a vector
+    that starts one element into its buffer takes the staged-weights kernel and stays bit-exact."""
+    N, K, M = 96, 1024, 2
+    note(f"gemv ref unaligned activations type={t}")
+    rng = np.random.default_rng(4242 + t)
+    raw = qo.random_weights(rng, t, N, K)
+    x = qo.random_bf16(rng, (M, K))
+    buf = torch.zeros(M * K + 1, dtype=torch.int16, device="cuda")
+    buf[1:] = torch.from_numpy(x.reshape(-1).view(np.int16)).to("cuda")
+    xd = buf[1:].view(torch.bfloat16).view(M, K)
+    assert xd.data_ptr() % 16 == 2
+    y, yf = dev.gemv(t, d_u8(raw), N, K, xd, mode="ref", out_f32=True)
+    acc, ye = co.gemv_ref(t, raw, N, K, x)
     assert_bits_equal(u32(h_f32(yf)), u32(acc), "acc")
     assert_bits_equal(h_bits(y), ye, "y")
 
