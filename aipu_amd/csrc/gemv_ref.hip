@@ -5,8 +5,9 @@
 //     acc = f32(acc + f32(x[m][k] * w[n][k]))     for k = 0 .. K-1, in order,
 // then y = bf16_RNE(acc).  One lane owns one output row and walks K sequentially.  Q4_K with
 // K <= 32768 runs k_gemv_ref_q4k (row blocks in registers, activations staged once as fp32),
-// Q8_0 / F16 / BF16 with K a multiple of 64 k_gemv_ref_reg (the same for their units), both
-// with aligned pointers; Q6_K, larger K and unaligned pointers run k_gemv_ref, whose 64 rows per workgroup are staged 256
+// Q8_0 / F16 / BF16 with K a multiple of 64 k_gemv_ref_reg and Q6_K with K a multiple of 512
+// k_gemv_ref_q6k (the same for their blocks), all with aligned pointers; larger K, other K and
+// unaligned pointers run k_gemv_ref, whose 64 rows per workgroup are staged 256
 // weights at a time through LDS so the global reads stay coalesced, with a last stage of fewer
 // weights for K that is a multiple of the type's block but not of 256 (Q8_0: 32; F16 / BF16:
 // any K).  The library is compiled with -ffp-contract=off, so the multiply and the add below
@@ -457,6 +458,128 @@ __global__ __launch_bounds__(kRows) void k_gemv_ref_reg(const uint8_t* __restric
     }
 }
 
+// Q6_K in reference order with the weights in registers: stage_mac's Q6_K dequantisation (so
+// the same bits).  A 210-B block starts 4-B aligned when its index is even and 2 B past a dword
+// when it is odd (K a multiple of 512, rows 4-B aligned); each lane loads the 53 dwords that
+// span its block, one block ahead, and realigns the dwords it uses by `par` (0 or 2) bytes.
+// Four weights at a time: code = nibble | 2-bit high part << 4 for four bytes in one dword,
+// then per weight (float)(code - 32) (as cvt(code) - 32, exact) times d * sc.
+__device__ __forceinline__ uint32_t q6_dword(const uint32_t (&R)[53], int o, uint32_t par) {   // bytes o .. o + 3, o % 4 == 0, o <= 204
+    return __builtin_amdgcn_alignbyte(R[(o >> 2) + 1], R[o >> 2], par);
+}
+
+template <int MC>
+__device__ __forceinline__ void q6_block_ref(const uint32_t (&R)[53], uint32_t par, const float* xb, int64_t K,
+                                             float (&acc)[MC]) {
+    const float d = f16_to_f32(par ? R[52] >> 16 : R[52] & 0xFFFFu);   // d: block bytes 208..209, the span's last dword
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            __builtin_amdgcn_sched_barrier(0);   // one run of 32 weights at a time (registers)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {   // weights 128h + 32t + 4c .. + 3
+                const uint32_t ql = q6_dword(R, 64 * h + 32 * (t & 1) + 4 * c, par);
+                const uint32_t qh = q6_dword(R, 128 + 32 * h + 4 * c, par);
+                const uint32_t code = ((t < 2 ? ql : ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * t)) & 0x03030303u) << 4);
+                const int si = 8 * h + 2 * t + (c >> 2);   // scale index k >> 4
+                const uint32_t sw = q6_dword(R, 192 + (si & ~3), par);
+                const float ds = d * (float)(int8_t)(uint8_t)(sw >> (8 * (si & 3)));
+                const float q[4] = {cvt_ubyte<0>(code), cvt_ubyte<1>(code), cvt_ubyte<2>(code), cvt_ubyte<3>(code)};
+                const int k = 128 * h + 32 * t + 4 * c;
+                float4 xv[MC];
+#pragma unroll
+                for (int mm = 0; mm < MC; ++mm) xv[mm] = *(const float4*)(xb + (int64_t)mm * K + k);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float w = ds * (q[e] - 32.0f);
+#pragma unroll
+                    for (int mm = 0; mm < MC; ++mm) {
+                        const float xe = e == 0 ? xv[mm].x : e == 1 ? xv[mm].y : e == 2 ? xv[mm].z : xv[mm].w;
+                        const float p = xe * w;
+                        acc[mm] = acc[mm] + p;
+                    }
+                }
+            }
+        }
+}
+
+template <int MC>
+__global__ __launch_bounds__(kRows) void k_gemv_ref_q6k(const uint8_t* __restrict__ W, int64_t N, int64_t K,
+                                                        const uint16_t* __restrict__ X, int64_t M,
+                                                        uint16_t* __restrict__ Y, float* __restrict__ Yf,
+                                                        RefGather ga) {
+    if (ga.sel) {
+        const int z = blockIdx.z;
+        if (z < ga.topk) {
+            int e = ga.sel[z];
+            e = e < 0 ? 0 : (e >= ga.E ? (int)ga.E - 1 : e);
+            W += (int64_t)e * ga.wstride;
+        } else {
+            W = ga.W_alt;
+        }
+        X += (int64_t)z * ga.x_zstride;
+        Y += (int64_t)z * ga.y_zstride;
+        if (Yf) Yf += (int64_t)z * ga.y_zstride;
+    }
+    extern __shared__ __align__(16) float s_x[];   // [MC][K]
+    const int lane = threadIdx.x;
+    const int64_t row0 = (int64_t)blockIdx.x * kRows;
+    const int64_t m0 = (int64_t)blockIdx.y * MC;
+    const int mcnt = (int)((M - m0) < MC ? (M - m0) : MC);
+    const int nsb = (int)(K / QK_K);
+    const uint32_t rb = (uint32_t)nsb * 210u;
+    const int nrows = (int)((N - row0) < kRows ? (N - row0) : kRows);
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W + row0 * (int64_t)rb, (uint32_t)nrows * rb);
+    const uint32_t wrow = (uint32_t)lane * rb;
+    uint32_t nxt[53];
+    auto load_block = [&](int b) {   // the dwords spanning block b (the last one may read past the row: zeros or junk)
+        const uint32_t o = wrow + ((210u * (uint32_t)b) & ~3u);
+#pragma unroll
+        for (int i = 0; i < 53; ++i) nxt[i] = buf_load4(wr, o + 4u * (uint32_t)i);
+    };
+    load_block(0);
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X + m0 * K, (uint32_t)mcnt * (uint32_t)K * 2u);
+    const int nch = MC * (int)(K / 8);
+    for (int c0 = 0; c0 < nch; c0 += 8 * kRows) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + u * kRows + lane;
+            v[u] = buf_load16(xr, c < nch ? 16u * (uint32_t)c : 0xF0000000u);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + u * kRows + lane;
+            if (c < nch) {
+                float4* d = (float4*)(s_x + 8 * (int64_t)c);
+                d[0] = make_float4(bf16_to_f32(v[u].x & 0xFFFFu), bf16_to_f32(v[u].x >> 16),
+                                   bf16_to_f32(v[u].y & 0xFFFFu), bf16_to_f32(v[u].y >> 16));
+                d[1] = make_float4(bf16_to_f32(v[u].z & 0xFFFFu), bf16_to_f32(v[u].z >> 16),
+                                   bf16_to_f32(v[u].w & 0xFFFFu), bf16_to_f32(v[u].w >> 16));
+            }
+        }
+    }
+    __syncthreads();
+    float acc[MC];
+#pragma unroll
+    for (int i = 0; i < MC; ++i) acc[i] = 0.0f;
+    for (int b = 0; b < nsb; ++b) {
+        uint32_t R[53];
+#pragma unroll
+        for (int i = 0; i < 53; ++i) R[i] = nxt[i];
+        if (b + 1 < nsb) load_block(b + 1);
+        q6_block_ref<MC>(R, (210u * (uint32_t)b) & 3u, s_x + (int64_t)b * QK_K, K, acc);
+    }
+    const int64_t n = row0 + lane;
+    if (n < N) {
+        for (int mm = 0; mm < mcnt; ++mm) {
+            Y[(m0 + mm) * N + n] = (uint16_t)bf16_rne(acc[mm]);
+            if (Yf) Yf[(m0 + mm) * N + n] = acc[mm];
+        }
+    }
+}
+
 // Reference order on already-dequantised fp32 weights (matmul_q4k_col on a wdeq column).
 __global__ __launch_bounds__(kRows) void k_gemv_ref_f32(const float* __restrict__ W, int64_t N, int64_t K,
                                                         const float* __restrict__ X, int64_t M,
@@ -508,7 +631,7 @@ hipError_t launch_gemv_ref_gather(int type, const void* w, int64_t N, int64_t K,
     // the register kernels load 16 B of activations and whole dwords / 16 B of weights at a time:
     // the pointers they start from must be aligned for that (the ABI asks less in this mode)
     auto al = [](const void* p, uintptr_t a) { return p == nullptr || ((uintptr_t)p & (a - 1)) == 0; };
-    const uintptr_t wa = type == T_Q8_0 ? 4 : 16;
+    const uintptr_t wa = (type == T_Q8_0 || type == T_Q6_K) ? 4 : 16;
     const bool reg_ok = al(x, 16) && al(w, wa) && al(w_alt, wa) && (x_zstride * 2) % 16 == 0 && wstride % (int64_t)wa == 0;
     if (reg_ok && type == T_Q4_K && K % QK_K == 0 && K * 4 <= kRefQ4LdsBytes) {
         // the register kernel: MC activation rows per pass, as many as the staged rows allow
@@ -521,6 +644,19 @@ hipError_t launch_gemv_ref_gather(int type, const void* w, int64_t N, int64_t K,
             case 4: hipLaunchKernelGGL(k_gemv_ref_q4k<4>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
             case 2: hipLaunchKernelGGL(k_gemv_ref_q4k<2>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
             default: hipLaunchKernelGGL(k_gemv_ref_q4k<1>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
+        }
+        return hipGetLastError();
+    }
+    if (reg_ok && type == T_Q6_K && K % 512 == 0 && K * 4 <= kRefQ4LdsBytes) {
+        int mc = 8;
+        while (mc > 1 && (mc / 2 >= M || (int64_t)mc * K * 4 > kRefQ4LdsBytes)) mc /= 2;
+        const dim3 g4((unsigned)((N + kRows - 1) / kRows), (unsigned)((M + mc - 1) / mc), (unsigned)nslots);
+        const size_t lds = (size_t)mc * (size_t)K * 4;
+        switch (mc) {
+            case 8: hipLaunchKernelGGL(k_gemv_ref_q6k<8>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
+            case 4: hipLaunchKernelGGL(k_gemv_ref_q6k<4>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
+            case 2: hipLaunchKernelGGL(k_gemv_ref_q6k<2>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
+            default: hipLaunchKernelGGL(k_gemv_ref_q6k<1>, g4, dim3(kRows), lds, st, W, N, K, x, M, y, y_f32, ga); break;
         }
         return hipGetLastError();
     }

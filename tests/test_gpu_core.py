@@ -106,11 +106,14 @@ def test_fp32_rsqrt_golden():
 # 128 KB, in passes of up to 8, 4, 2 or 1 rows as the staging allows: 9 rows at K = 256 (8 + 1),
 # 8 at K = 6144 (two passes of 4), 5 at K = 8192 (4 + 1), 2 at K = 32768 (one row per pass);
 # K = 40960 takes the staged-weights kernel.  Q8_0, F16 and BF16 take their register kernel
-# (k_gemv_ref_reg) at K a multiple of 64.  Ragged N leaves part of the last wave idle.
+# (k_gemv_ref_reg) at K a multiple of 64, Q6_K its own (k_gemv_ref_q6k, blocks alternately 4-B
+# aligned and 2 B past a dword) at K a multiple of 512 (K = 1280 stays on the staged kernel).
+# Ragged N leaves part of the last wave idle.
 REF_CASES = [
     (qo.GGML_Q4_K, 200, 768, 1), (qo.GGML_Q4_K, 131, 512, 3), (qo.GGML_Q4_K, 64, 256, 9),
     (qo.GGML_Q4_K, 130, 6144, 8), (qo.GGML_Q4_K, 33, 8192, 5), (qo.GGML_Q4_K, 70, 32768, 2),
     (qo.GGML_Q4_K, 64, 40960, 1), (qo.GGML_Q8_0, 130, 6144, 8), (qo.GGML_F16, 70, 4096, 3), (30, 33, 8192, 5),
+    (qo.GGML_Q6_K, 130, 6144, 8), (qo.GGML_Q6_K, 65, 1024, 1), (qo.GGML_Q6_K, 40, 1280, 2),
     (qo.GGML_Q6_K, 96, 512, 2), (qo.GGML_Q8_0, 70, 512, 1), (qo.GGML_F16, 65, 256, 2), (30, 64, 512, 1),
 ]
 
@@ -130,7 +133,7 @@ def test_gemv_ref_bitexact(t, N, K, M):
     assert_bits_equal(h_bits(y), ye, "y")
 
 
-@pytest.mark.parametrize("t", [qo.GGML_Q4_K, qo.GGML_Q8_0, qo.GGML_F16])
+@pytest.mark.parametrize("t", [qo.GGML_Q4_K, qo.GGML_Q6_K, qo.GGML_Q8_0, qo.GGML_F16])
 def test_gemv_ref_unaligned_activations(t):
     """Reference mode asks only 2-byte aligned activations (and, below Q4_K, weights): a vector
     that starts one element into its buffer takes the staged-weights kernel and stays bit-exact."""
