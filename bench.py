@@ -710,6 +710,7 @@ def main():
             extra[f"gemv_c1_dense_m{M}"] = bench_gemv(dev, torch, 6144, 6144, M, 500, 20, rot, mode="fast_dense",
                                                       label="C1 dense")
         extra["exact_order"] = bench_exact(dev, torch, rot)
+        extra["moe_decode_c2_ref"] = bench_moe(dev, torch, 20, mode="ref")   # the bit-exact step
         extra["mixed_tiles_c3"] = bench_tiles(dev, torch)
         extra["mixed_tiles_c3_m4"] = bench_tiles(dev, torch, M=4)
         extra["prefill_c4"] = bench_prefill(dev, torch)
