@@ -152,6 +152,39 @@ def test_gemv_ref_unaligned_activations(t):
     assert_bits_equal(h_bits(y), ye, "y")
 
 
+def _random_ref_cases(n=24, seed=20261202):
+    """Seeded shapes for the reference-order kernels: every type, ragged N, M = 1..9, K at the
+    register kernels' multiples (Q4_K 256, Q6_K 512, Q8_0 / F16 / BF16 64) and off them."""
+    rng = np.random.default_rng(seed)
+    kinds = [(qo.GGML_Q4_K, 256), (qo.GGML_Q6_K, 256), (qo.GGML_Q8_0, 32), (qo.GGML_F16, 1), (30, 1)]
+    cases = []
+    for i in range(n):
+        t, blk = kinds[i % len(kinds)]
+        if t in (qo.GGML_Q4_K, qo.GGML_Q6_K):
+            K = 256 * int(rng.integers(1, 25))
+        elif t == qo.GGML_Q8_0:
+            K = 32 * int(rng.integers(1, 160))
+        else:
+            K = int(rng.integers(1, 5000)) if i % 2 else 64 * int(rng.integers(1, 80))
+        cases.append((t, int(rng.integers(1, 300)), K, int(rng.integers(1, 10))))
+    return cases
+
+
+@pytest.mark.parametrize("t,N,K,M", _random_ref_cases())
+def test_gemv_ref_random_shapes(t, N, K, M):
+    note(f"gemv ref random type={t} N={N} K={K} M={M}")
+    rng = np.random.default_rng(N * 7919 + K * 31 + M)
+    raw = qo.random_bf16(rng, N * K).view(np.uint8) if t == 30 else qo.random_weights(rng, t, N, K)
+    x = qo.random_bf16(rng, (M, K))
+    y, yf = dev.gemv(t, d_u8(raw), N, K, d_bf16(x), mode="ref", out_f32=True)
+    if t == 30:
+        acc, ye = qo.gemv_ref(qo.bf16_bits_to_f32(raw.view(np.uint16)).reshape(N, K), qo.bf16_bits_to_f32(x))
+    else:
+        acc, ye = co.gemv_ref(t, raw, N, K, x)
+    assert_bits_equal(u32(h_f32(yf)), u32(acc), "acc")
+    assert_bits_equal(h_bits(y), ye, "y")
+
+
 PARTIAL_CASES = [
     (qo.GGML_Q8_0, 70, 288, 1), (qo.GGML_Q8_0, 64, 4128, 3), (qo.GGML_F16, 65, 100, 2), (qo.GGML_F16, 33, 513, 1),
     (30, 64, 264, 4), (30, 17, 7, 1),
