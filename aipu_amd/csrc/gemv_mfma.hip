@@ -1132,10 +1132,14 @@ hipError_t plain_pass(const uint8_t* W, int64_t N, int64_t K, const uint16_t* x,
 
 }  // namespace
 
-// Whether the matrix-core GEMV serves this shape (Q4_K, any M, the staging limits).
+// Whether the matrix-core GEMV serves this shape (Q4_K, any M, the staging limits).  Every
+// shape of the persistent one-row kernel is served (K <= 8192, block counts such as 17, 19,
+// 23, 29 and 31 included, which no k_mfma_gemv plan splits): a row without a multi-row kernel
+// in that order runs as its own one-row launch, so the rows of a batch keep their one-row bits.
 bool gemv_mfma_supported(int64_t N, int64_t K, int64_t M) {
     if (N < 1 || K < QK_K || K % QK_K != 0 || M < 1) return false;
     if (N * row_bytes(T_Q4_K, K) >= (int64_t)1 << 40) return false;
+    if (gemv_persist_supported(N, K)) return true;
     Plan pl;
     const int mr = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
     return K <= (1 << 20) && make_plan((int)(K / QK_K), 1, 1, mr, kMaxW, pl);
@@ -1188,6 +1192,12 @@ hipError_t launch_gemv_mfma(const void* w, int64_t N, int64_t K, const uint16_t*
                 const hipError_t e = runs(pb, ps, (unsigned)((N + kTR - 1) / kTR), xm, (int)K, st);
                 if (e != hipSuccess) return e;
                 m0 += mr;
+                continue;
+            }
+            if (gemv_persist2_supported(N, K)) {   // no other multi-row kernel: two rows at a time
+                const hipError_t e = launch_gemv_persist2(W, N, K, xm, ym, yfm, ystride, st);
+                if (e != hipSuccess) return e;
+                m0 += 2;
                 continue;
             }
         }

@@ -285,7 +285,8 @@ def test_gemv_fast_tolerance(N, K, M):
 # (M = 2..8 at K = 2048/4096/6144), k_gemvs / k_gemvm elsewhere, and a launch per row where no
 # multi-row kernel forms rows in the one-row order (K / 256 not split into at most 8 parts of
 # at most 4 blocks: 2816, 5632; M = 1 off the persistent kernel: K > 8192), and the streaming
-# kernel beyond the matrix-core staging limit.
+# kernel beyond the matrix-core staging limit.  Two rows share a persistent launch wherever
+# nothing else takes them (odd prime block counts such as 23).
 # Covers every row count of a verify batch at the BASELINE shape, the other matrix-core shapes
 # (ragged N, passes of 8 + remainder), the shapes without a multi-row kernel, and K > 8192.
 INVARIANCE_CASES = [(6144, 6144, m) for m in (2, 3, 4, 5, 6, 7, 8)] + [
@@ -304,7 +305,11 @@ INVARIANCE_CASES = [(6144, 6144, m) for m in (2, 3, 4, 5, 6, 7, 8)] + [
     # two rows on the persistent one-row kernel (the M = 2 cases above run there too): an odd
     # block count (a half last pair), a ragged last tile, four tiles per CU, one tile too many
     # for it, a single block
-    (100, 2304, 2), (6100, 6144, 2), (8192, 6144, 2), (8200, 4096, 2), (1, 256, 2)]
+    (100, 2304, 2), (6100, 6144, 2), (8192, 6144, 2), (8200, 4096, 2), (1, 256, 2),
+    # block counts that no k_mfma_gemv plan splits (17, 19, 23, 29, 31 blocks): one-row calls on
+    # the persistent kernel, batches two rows at a time on it (K <= 6144) or a launch per row;
+    # and 37 blocks (K > 8192), where every M runs the streaming kernel
+    (2000, 4352, 3), (3000, 4864, 8), (6390, 5888, 6), (2000, 7424, 5), (4100, 7936, 2), (100, 9472, 3)]
 
 
 def _fast_rows(t, wd, N, K, rows, mode):
@@ -328,6 +333,34 @@ def test_gemv_fast_batch_invariance(N, K, M):
     w = qo.dequant_q4k(raw).reshape(N, K)
     ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), yfb.view(np.float32), rel=1e-5)
     assert ok, f"batch of M={M}: fp32 accumulators {worst:.3f} of the tolerance"
+
+
+def _random_fast_cases(n=20, seed=1202):
+    """Seeded Q4_K shapes for the fast mode's kernel choice: N from one tile to many per CU, K from
+    one block to 8192 (one- and two-pair persistent waves, odd block counts), M = 1..8."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 3000)), int(rng.integers(3000, 9000))])),
+             256 * int(rng.integers(1, 33)), int(rng.integers(1, 9))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("N,K,M", _random_fast_cases())
+def test_gemv_fast_random_shapes(N, K, M):
+    """Every row of a fast-mode batch equals its one-row launch bit for bit, and the batch meets
+    the tolerance gate, at seeded random shapes (whichever kernels the dispatch picks)."""
+    note(f"gemv fast random N={N} K={K} M={M}")
+    rng = np.random.default_rng(13 * N + K + M)
+    raw = qo.random_q4k_blocks(rng, N * K // 256)
+    x = qo.random_bf16(rng, (M, K))
+    wd = d_u8(raw)
+    yb, yfb = _fast_rows(qo.GGML_Q4_K, wd, N, K, x, "fast")
+    for r in range(M):
+        y1, yf1 = _fast_rows(qo.GGML_Q4_K, wd, N, K, x[r:r + 1], "fast")
+        assert_bits_equal(yf1[0], yfb[r], f"row {r} of M={M}: fp32 accumulators")
+        assert_bits_equal(y1[0], yb[r], f"row {r} of M={M}: bf16 outputs")
+    w = qo.dequant_q4k(raw).reshape(N, K)
+    ok, worst = qo.tolerance_gate(w, qo.bf16_bits_to_f32(x), yfb.view(np.float32), rel=1e-5)
+    assert ok, f"batch of M={M}: fp32 accumulators {worst:.3f} of the tolerance"
+    assert not dev.wait_timeouts(), "a bounded wait gave up"
 
 
 @pytest.mark.parametrize("N,K,M", [(300, 4096, 2), (513, 6144, 3), (4100, 4096, 4)])
