@@ -543,6 +543,42 @@ def test_mixed_tiles_large_one_row(name, K, spec):
 
 
 
+
+def _random_tile_cases(n=16, seed=1303):
+    """Seeded (K, M, tiles): K from one block to 12288, M = 1..8, 1..10 ragged tiles of all five
+    types (on and off the one-launch path, whose limit depends on K)."""
+    rng = np.random.default_rng(seed)
+    return [(256 * int(rng.integers(1, 49)), int(rng.integers(1, 9)), int(rng.integers(1, 11))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("K,M,n_tiles", _random_tile_cases())
+def test_mixed_tiles_random_shapes(K, M, n_tiles):
+    """Fast-mode tile GEMV at seeded random shapes: every row of the batch equals its one-row
+    launch bit for bit, rows outside the tiles stay untouched, and each tile meets the gate."""
+    note(f"tiles fast random K={K} M={M} tiles={n_tiles}")
+    rng = np.random.default_rng(K * 31 + M * 7 + n_tiles)
+    spec, N = _ragged_spec(rng, n_tiles, K)
+    tw = [_tile_weights(rng, t, n, K) for t, _, n in spec]
+    tiles = [(t, d_u8(r), r0, n) for (t, r0, n), (r, _) in zip(spec, tw)]
+    x = qo.random_bf16(rng, (M, K))
+    covered = np.zeros(N, bool)
+    for _, r0, n in spec:
+        covered[r0:r0 + n] = True
+    yb = torch.full((M, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    yfb = torch.full((M, N), -3.0, dtype=torch.float32, device="cuda")
+    dev.gemv_tiles(tiles, N, K, d_bf16(x), mode="fast", out=yb, out_f32=yfb)
+    bb, bfb = h_bits(yb), u32(h_f32(yfb))
+    assert np.all(h_f32(yfb)[:, ~covered] == np.float32(-3.0)), "rows outside the tiles written"
+    assert np.all(bb[:, ~covered] == qo.bf16_round_bits(np.float32(7.0))), "rows outside the tiles written"
+    for r in range(M):
+        y1, yf1 = dev.gemv_tiles(tiles, N, K, d_bf16(x[r:r + 1]), mode="fast", out_f32=True)
+        assert_bits_equal(u32(h_f32(yf1))[0][covered], bfb[r][covered], f"row {r} of M={M}: fp32 accumulators")
+        assert_bits_equal(h_bits(y1)[0][covered], bb[r][covered], f"row {r} of M={M}: bf16 outputs")
+    xf = qo.bf16_bits_to_f32(x)
+    for (t, r0, n), (r, wdq) in zip(spec, tw):
+        ok, worst = qo.tolerance_gate(wdq, xf, h_f32(yfb)[:, r0:r0 + n])
+        assert ok, (t, r0, n, worst)
+
 def _tile_weights(rng, t, rows, K):
     """(raw bytes, dequantised float32[rows, K]) of a tile; BF16 tiles hold N(0, 0.05^2) bf16."""
     if t == BF16:
