@@ -283,6 +283,41 @@ def test_moe_c2_full_256_experts(mode):
         assert_bits_equal(h_bits(y), yref, "moe ref C2 E=256")
 
 
+
+def _random_moe_cases(n=10, seed=1404):
+    """Seeded MoE shapes: E = topk..96 experts, H = 256..3072, I = 256..1536, top-1..8, bf16 or
+    Q4_K router, with or without the shared expert."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        topk = int(rng.integers(1, 9))
+        out.append((int(rng.integers(topk, 97)), 256 * int(rng.integers(1, 13)), 256 * int(rng.integers(1, 7)), topk,
+                    BF16 if rng.integers(0, 2) else Q4K, bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("mode", ["ref", "fast"])
+@pytest.mark.parametrize("E,H,I,topk,router_type,shared", _random_moe_cases())
+def test_moe_random_shapes(E, H, I, topk, router_type, shared, mode):
+    """One MoE step at seeded random shapes, whichever kernels the dispatch picks: in ref mode
+    routing and y bit-exact against the oracle; in fast mode the routing is the reference tail
+    of the step's own logits and h and y meet the two-stage bound."""
+    note(f"moe random {mode} E={E} H={H} I={I} topk={topk} router={router_type} shared={shared}")
+    rng = np.random.default_rng(E * 1000 + H + I + topk + shared)
+    rw, ex, sh, x = _moe_case(rng, E, H, I, router_type, shared)
+    shd = tuple(d_u8(a) for a in sh) if sh else None
+    if mode == "ref":
+        y, sel, sw = dev.moe_swiglu_decode(router_type, d_u8(rw), Q4K, d_u8(ex[0]), d_u8(ex[1]), d_u8(ex[2]), E, H,
+                                           I, topk, d_bf16(x), mode="ref", shared=shd)
+        r = go.moe_decode_ref(x, router_type, rw, ex, Q4K, E, H, I, topk, shared=sh)
+        assert np.array_equal(sel.cpu().numpy(), r["sel_idx"])
+        assert_bits_equal(h_bits(sw), r["sel_w"], "sel_w")
+        assert_bits_equal(h_bits(y), r["y"], "y")
+        return
+    yb, sel, sw, lg, hw = _fast_step(router_type, rw, tuple(d_u8(a) for a in ex), E, H, I, topk, x, shd)
+    es, ew = _check_routing(router_type, rw, E, H, x, topk, sel, sw, lg)
+    _check_moe_tight(yb, hw, x, tuple(a.reshape(E, -1)[es] for a in ex), sh, ew, H, I)
+
 def _moe_persistent_case(H, E, topk, seed):
     I = 2048
     g = torch.Generator(device="cuda")
