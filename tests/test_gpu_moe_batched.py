@@ -204,3 +204,41 @@ def test_batched_fast_two_row_pass_equals_one_row_pass(H, topk, shared):
     ex = tuple(t.cpu().numpy() for t in exd)
     sh = tuple(t.cpu().numpy() for t in shd) if shared else None
     _check_fast(y2, sel2, sw2, X[:2], BF16, rw, ex, sh, E, H, I, topk)
+
+
+def _random_batched_cases(n=10, seed=1505):
+    """Seeded batched MoE shapes: M = 1..9 rows, E = topk..64 experts, H = 256..3072, I = 256..1536,
+    top-1..8, bf16 or Q4_K router, with or without the shared expert."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        topk = int(rng.integers(1, 9))
+        out.append((int(rng.integers(1, 10)), int(rng.integers(max(topk, 2), 65)), 256 * int(rng.integers(1, 13)),
+                    256 * int(rng.integers(1, 7)), topk, BF16 if rng.integers(0, 2) else Q4K, bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("mode", ["ref", "fast"])
+@pytest.mark.parametrize("M,E,H,I,topk,router_type,shared", _random_batched_cases())
+def test_batched_random_shapes(M, E, H, I, topk, router_type, shared, mode):
+    """The batched step at seeded random shapes: ref mode bit-exact against the oracle; fast mode
+    routed on its own logits within the fast-mode bound, and (from three rows) each row's bits
+    independent of the batch's order."""
+    note(f"moe batched random {mode} M={M} E={E} H={H} I={I} topk={topk} router={router_type} shared={shared}")
+    rng = np.random.default_rng(M * 100000 + E * 1000 + H + I + topk)
+    rw, ex, sh = _case(rng, E, H, I, router_type)
+    sh = sh if shared else None
+    X = qo.random_bf16(rng, (M, H), scale=0.05)
+    y, sel, sw = _run(router_type, rw, ex, sh, E, H, I, topk, X, mode)
+    if mode == "ref":
+        r = go.moe_decode_batched_ref(X, router_type, rw, ex, Q4K, E, H, I, topk, shared=sh)
+        assert np.array_equal(sel, r["sel_idx"])
+        assert_bits_equal(sw, r["sel_w"], "sel_w")
+        assert_bits_equal(y, r["y"], "y")
+        return
+    _check_fast(y, sel, sw, X, router_type, rw, ex, sh, E, H, I, topk)
+    if M >= 3:
+        yr, selr, swr = _run(router_type, rw, ex, sh, E, H, I, topk, X[::-1].copy(), mode)
+        assert np.array_equal(selr[::-1], sel), "routing depends on the batch order"
+        assert_bits_equal(swr[::-1], sw, "sel_w with the batch reversed")
+        assert_bits_equal(yr[::-1], y, "y with the batch reversed")
