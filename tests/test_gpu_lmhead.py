@@ -166,3 +166,19 @@ def test_lm_head_detects_corrupted_row():
     assert not np.array_equal(got, exp), "logits of a corrupted head equal the oracle's"
     assert am == 17 and eam != 17, (am, eam)
     _check(w, x, "clean twin")
+
+
+def _random_lm_cases(n=10, seed=1707):
+    """Seeded (V, K): V = 1..5000 vocabulary rows, K = 8..16384 in steps of 8 (both kernels,
+    ragged chunk tails)."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 5001)), 8 * int(rng.integers(1, 2049))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("V,K", _random_lm_cases())
+def test_lm_head_random_shapes(V, K):
+    note(f"lm_head random V={V} K={K}")
+    rng = np.random.default_rng(V * 17 + K)
+    w = qo.random_bf16(rng, (V, K))
+    x = qo.random_bf16(rng, K)
+    _check(w, x, f"V={V} K={K}")

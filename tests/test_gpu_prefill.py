@@ -160,3 +160,21 @@ def test_prefill_detects_corrupted_weights():
     # the clean weights pass the same gate (the twin's other half)
     y, yf = _prefill(raw, N, K, x)
     assert qo.tolerance_gate(wdeq, qo.bf16_bits_to_f32(x), yf)[0]
+
+
+def _random_prefill_cases(n=10, seed=1606):
+    """Seeded (M, N, K): M = 1..600 rows, N = 1..1200 weight rows, K = 256..8192."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 601)), int(rng.integers(1, 1201)), 256 * int(rng.integers(1, 33))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("M,N,K", _random_prefill_cases())
+def test_prefill_random_shapes(M, N, K):
+    """The prefill GEMM at seeded random shapes (ragged M and N tiles, any super-block count)
+    meets the accumulator gate and the bf16 1-ulp bound."""
+    note(f"prefill random M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 11 + N * 5 + K)
+    raw = qo.random_q4k_blocks(rng, N * K // 256)
+    x = qo.random_bf16(rng, (M, K))
+    y, yf = _prefill(raw, N, K, x)
+    _check(raw, N, K, x, y, yf, f"M={M} N={N} K={K}")
