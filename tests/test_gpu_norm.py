@@ -187,3 +187,48 @@ def test_glm_mirror_rmsnorm_ffn_block_lm_head():
     logits, lbits, am = gm.lm_head(list(qo.bf16_bits_to_f32(xb)), [list(qo.bf16_bits_to_f32(r)) for r in Wb])
     le, ae = co.lm_head(Wb, xb)
     assert lbits == [int(v) for v in le] and am == ae
+
+
+def _random_layer_cases(n=8, seed=1808):
+    """Seeded FFN-half shapes: E = topk..64, H = 256..4096, I = 256..1536, top-1..8, bf16 or
+    Q4_K router, with or without the shared expert."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        topk = int(rng.integers(1, 9))
+        out.append((int(rng.integers(topk, 65)), 256 * int(rng.integers(1, 17)), 256 * int(rng.integers(1, 7)), topk,
+                    BF16 if rng.integers(0, 2) else Q4K, bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("mode", ["ref", "fast"])
+@pytest.mark.parametrize("E,H,I,topk,router_type,shared", _random_layer_cases())
+def test_moe_layer_random_shapes(E, H, I, topk, router_type, shared, mode):
+    """The FFN half at seeded random shapes: ref mode bit-exact against the oracle; fast mode
+    equal (bitwise) to rmsnorm -> MoE step -> residual run as three separate calls."""
+    note(f"moe layer random {mode} E={E} H={H} I={I} topk={topk} router={router_type} shared={shared}")
+    rng = np.random.default_rng(E * 7 + H + I * 3 + topk)
+    if router_type == BF16:
+        rw = qo.random_bf16(rng, (E, H), scale=0.05).view(np.uint8).reshape(-1)
+    else:
+        rw = qo.random_q4k_blocks(rng, E * H // 256)
+    ex = tuple(qo.random_q4k_blocks(rng, E * I * H // 256) for _ in range(3))
+    sh = tuple(qo.random_q4k_blocks(rng, I * H // 256) for _ in range(3)) if shared else None
+    h = qo.random_bf16(rng, H, scale=0.5)
+    g = qo.random_bf16(rng, H)
+    rwd, exd = d_u8(rw), tuple(d_u8(a) for a in ex)
+    shd = tuple(d_u8(a) for a in sh) if sh else None
+    y, sel, sw = dev.moe_layer_decode(router_type, rwd, Q4K, *exd, E, H, I, topk, d_bf16(h), d_bf16(g), mode=mode,
+                                      shared=shd)
+    if mode == "ref":
+        r = go.moe_layer_ref(h, g, router_type, rw, ex, Q4K, E, H, I, topk, shared=sh)
+        assert list(sel.cpu().numpy()) == list(r["sel_idx"])
+        assert_bits_equal(h_bits(y), r["y"], "layer y")
+        return
+    hd = d_bf16(h)
+    nrm = dev.rmsnorm(hd, d_bf16(g), mode="fast")
+    f, sel2, sw2 = dev.moe_swiglu_decode(router_type, rwd, Q4K, *exd, E, H, I, topk, nrm, mode="fast", shared=shd)
+    want = (hd.float() + f.float()).to(torch.bfloat16)   # RNE of an exact fp32 sum of two bf16
+    assert torch.equal(sel, sel2)
+    assert_bits_equal(h_bits(sw), h_bits(sw2), "sel_w")
+    assert_bits_equal(h_bits(y), h_bits(want), "layer = pieces")
