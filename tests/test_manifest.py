@@ -36,3 +36,11 @@ def test_collected_counts_match_manifest():
     assert not missing and not extra, (
         "collected test counts differ from tests/expected_test_counts.txt: expected "
         f"{ {k: exp[k] for k in missing} } got { {k: got.get(k, 0) for k in missing} }; files not in the manifest: {extra}")
+
+
+def test_bench_refuses_several_gpus():
+    """bench.py measures one GPU; asked for more it exits non-zero with a message saying so."""
+    r = subprocess.run([sys.executable, "bench.py", "--gpus", "2"], cwd=ROOT, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
