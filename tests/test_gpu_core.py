@@ -383,8 +383,18 @@ def test_gemv_fast_batch_invariance_bf16(N, K, M):
 # gate, bf16 within 1 ulp where well conditioned), and its bits depend neither on the other
 # rows of the batch nor on its position -- reversing the batch, or sending the row in another
 # batch, gives the same bits.  Shapes it does not serve behave as AIPU_MODE_FAST.
+def _random_dense_cases(n=10, seed=1909):
+    """Seeded (N, K, M) for the dense mode: mostly its K = 2048 / 4096 / 6144, sometimes another K
+    (where it behaves as the fast mode), N up to one tile past the dense kernel's limit."""
+    rng = np.random.default_rng(seed)
+    ks = [2048, 4096, 6144, 2048, 4096, 6144, 1280, 4352]
+    return [(int(rng.integers(1, 6169)), int(ks[int(rng.integers(0, len(ks)))]), int(rng.integers(2, 12)))
+            for _ in range(n)]
+
+
 DENSE_CASES = [(6144, 6144, m) for m in (2, 4, 7, 8)] + [
-    (6100, 6144, 3), (2050, 4096, 6), (8, 2048, 2), (1001, 2048, 8), (6144 + 24, 6144, 8), (300, 2816, 5)]
+    (6100, 6144, 3), (2050, 4096, 6), (8, 2048, 2), (1001, 2048, 8), (6144 + 24, 6144, 8), (300, 2816, 5)
+] + _random_dense_cases()
 
 
 def _dense_row(N, K, M, r):
