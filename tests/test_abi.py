@@ -2,11 +2,16 @@
 include/aipu_q4k.h declares, and rejects bad arguments with the documented status codes
 before it touches the GPU (fake device pointers below are never dereferenced)."""
 import ctypes
+import os
+import subprocess
+import sys
 
 import pytest
 
 from aipu_amd import _lib
 from aipu_amd._lib import TileDesc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 FAKE = ctypes.c_void_p(0x100000)       # 16-B aligned, never dereferenced
 FAKE_ODD = ctypes.c_void_p(0x100001)
@@ -189,3 +194,20 @@ def test_lm_head_validation():
     assert f(FAKE, 1000, 64, FAKE, FAKE, FAKE, FAKE, need - 1, S) == WS
     assert f(FAKE, 1000, 64, FAKE, FAKE, FAKE, NULL, need, S) == WS
     assert f(FAKE, 1000, 64, FAKE, FAKE, FAKE, ctypes.c_void_p(0x100010), need, S) == ALIGN
+
+
+def test_missing_library_fails_loudly():
+    """Without the built HIP library every call raises AipuLibraryMissing: there is no CPU
+    fallback to run instead (checked in a child process, with the loader pointed at a path
+    that does not exist)."""
+    code = ("import aipu_amd._lib as L, aipu_amd.device as dev, torch\n"
+            "L.LIB_PATH = '/nonexistent/libaipu_q4k.so'; L._lib = None\n"
+            "try:\n"
+            "    L.call('aipu_last_error')\n"
+            "except L.AipuLibraryMissing as e:\n"
+            "    print('missing:', e)\n"
+            "else:\n"
+            "    raise SystemExit('no error')\n")
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "missing:" in r.stdout
